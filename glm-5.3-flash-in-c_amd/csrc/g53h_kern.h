@@ -1,0 +1,17 @@
+/* g53h_kern.h - declarations shared between the library's HIP translation units. */
+#ifndef G53H_KERN_H
+#define G53H_KERN_H
+
+#include "g53h.h"
+
+#define GLM53F_MAX_TOPK_DEV 64
+/* G53hMat.pad_ of an expert's gate matrix: the expert failed to load (contributions zero). */
+#define G53_DROPPED 1
+
+int g53h_slot_mm_generic(float *y, const float *x, int T, int K, int nslots,
+                         const G53hExpert *experts, const int *idx, const G53hExpert *shared,
+                         int which, int rows, int cols, int x_per_slot);
+int g53h_combine_into(float *out, const float *contrib, const float *wts, int T, int E, int K, int nslots);
+int g53h_swiglu_split(float *y, const float *g, const float *u, long m, float limit);
+
+#endif /* G53H_KERN_H */

@@ -1,0 +1,322 @@
+/* g53h_ops.hip - the expert path's building blocks on gfx950, bit-exact with the reference:
+ *
+ *   k_mm_f8_generic   FP8 block-scaled matvec for any shape (ragged blocks, any br/bc),
+ *                     one thread per (token, row). Used for odd shapes and as the
+ *                     unit-level glm53f_mm; the decode layer uses the tiled kernels of
+ *                     g53h_moe.hip for the expert shapes.
+ *   k_swiglu          clamped SwiGLU.
+ *   k_router_scores   sigmoid(W x) and sigmoid + bias for T tokens, one wave per expert.
+ *   k_router_select   top-k by repeated argmax (strict >, lowest index), renormalise, scale.
+ *   k_route_topn      next-layer prediction.
+ */
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "g53h.h"
+#include "g53h_core.h"
+#include "g53h_kern.h"
+#include "g53h_runtime.h"
+
+/* ------------------------------------------------------------- FP8 matvec ---- */
+/* The reference's per-block arithmetic (src/core/glm53f_ops.c:195-227): eight fp32 lanes of
+ * fused products stepping by 8 columns, reduced in double by a fixed tree, the block tail
+ * added in double, the block sum scaled in double and accumulated over blocks in order. */
+__device__ double g53_block_dot(const uint8_t *row, const float *x, int j0, int j1)
+{
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int j = j0;
+    for (; j + 8 <= j1; j += 8)
+        for (int l = 0; l < 8; l++) a[l] = __builtin_fmaf(g53_e4m3_to_f32(row[j + l]), x[j + l], a[l]);
+    double bsum = (((double)a[0] + a[4]) + ((double)a[2] + a[6]))
+                + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
+    for (; j < j1; j++) bsum += (double)g53_e4m3_to_f32(row[j]) * (double)x[j];
+    return bsum;
+}
+
+__device__ float g53_row_dot(const G53hMat &m, int o, const float *x)
+{
+    const uint8_t *row = m.w + (size_t)o * m.cols;
+    const float *srow = m.s + (size_t)(o / m.br) * m.scols;
+    double acc = 0.0;
+    for (int b = 0, j0 = 0; j0 < m.cols; b++, j0 += m.bc) {
+        const int j1 = (j0 + m.bc < m.cols) ? j0 + m.bc : m.cols;
+        const double bsum = g53_block_dot(row, x, j0, j1);
+        const double p = bsum * (double)srow[b];
+        acc = acc + p;
+    }
+    return (float)acc;
+}
+
+__global__ void k_mm_f8_generic(float *__restrict__ y, const float *__restrict__ x, int T, G53hMat m)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * m.rows) return;
+    const int t = (int)(i / m.rows), o = (int)(i % m.rows);
+    y[(size_t)t * m.rows + o] = g53_row_dot(m, o, x + (size_t)t * m.cols);
+}
+
+extern "C" int g53h_mm_f8(float *y, const float *x, int T, const G53hMat *m)
+{
+    if (g53h_ready()) return -1;
+    if (T <= 0) return 0;
+    if (!m || !m->w || !m->s) return g53h_fail("g53h_mm_f8: unbound matrix");
+    if (m->rows <= 0 || m->cols <= 0 || m->br <= 0 || m->bc <= 0 ||
+        m->scols != (m->cols + m->bc - 1) / m->bc)
+        return g53h_fail("g53h_mm_f8: bad geometry %dx%d block %dx%d scols %d", m->rows, m->cols,
+                         m->br, m->bc, m->scols);
+    const long n = (long)T * m->rows;
+    hipLaunchKernelGGL(k_mm_f8_generic, dim3((unsigned)((n + 127) / 128)), dim3(128), 0,
+                       g53h_stream(), y, x, T, *m);
+    G53_LAUNCHED("k_mm_f8_generic");
+    return 0;
+}
+
+/* Generic per-slot expert matvec for the layer fallback: slot s of token t uses expert
+ * idx[t][s] (s < K) or the shared expert (s == K). which: 0 gate, 1 up, 2 down. */
+__global__ void k_slot_mm_generic(float *__restrict__ y, const float *__restrict__ x, int T, int K,
+                                  int nslots, const G53hExpert *__restrict__ experts,
+                                  const int *__restrict__ idx, const G53hExpert *__restrict__ shared,
+                                  int which, int rows, int cols, int x_per_slot)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * nslots * rows) return;
+    const int o = (int)(i % rows);
+    const int s = (int)((i / rows) % nslots);
+    const int t = (int)(i / ((long)rows * nslots));
+    const G53hExpert *e = s < K ? &experts[idx[(size_t)t * K + s]] : shared;
+    const G53hMat &m = which == 0 ? e->gate : (which == 1 ? e->up : e->down);
+    const float *xt = x + ((size_t)t * (x_per_slot ? nslots : 1) + (x_per_slot ? s : 0)) * cols;
+    float v = 0.0f;
+    if (e->gate.w) v = g53_row_dot(m, o, xt);
+    else if (e->gate.pad_ != G53_DROPPED) return;      /* absent from this batch */
+    y[((size_t)t * nslots + s) * rows + o] = v;
+}
+
+int g53h_slot_mm_generic(float *y, const float *x, int T, int K, int nslots,
+                         const G53hExpert *experts, const int *idx, const G53hExpert *shared,
+                         int which, int rows, int cols, int x_per_slot)
+{
+    const long n = (long)T * nslots * rows;
+    hipLaunchKernelGGL(k_slot_mm_generic, dim3((unsigned)((n + 127) / 128)), dim3(128), 0,
+                       g53h_stream(), y, x, T, K, nslots, experts, idx, shared, which, rows, cols,
+                       x_per_slot);
+    G53_LAUNCHED("k_slot_mm_generic");
+    return 0;
+}
+
+/* ----------------------------------------------------------------- SwiGLU ---- */
+__global__ void k_swiglu(float *__restrict__ y, const float *__restrict__ gu, int n, int T, float limit)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n * T) return;
+    const int t = (int)(i / n), k = (int)(i % n);
+    const float *g = gu + (size_t)t * 2 * n;
+    y[i] = g53_swiglu1(g[k], g[n + k], limit);
+}
+
+extern "C" int g53h_swiglu(float *y, const float *gu, int n, int T, float limit)
+{
+    if (g53h_ready()) return -1;
+    const long m = (long)n * T;
+    if (m <= 0) return 0;
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((m + 255) / 256)), dim3(256), 0, g53h_stream(), y,
+                       gu, n, T, limit);
+    G53_LAUNCHED("k_swiglu");
+    return 0;
+}
+
+/* Swiglu over separate gate/up slot outputs: g, u [rows_total][n] -> y. */
+__global__ void k_swiglu_split(float *__restrict__ y, const float *__restrict__ g,
+                               const float *__restrict__ u, long m, float limit)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < m) y[i] = g53_swiglu1(g[i], u[i], limit);
+}
+
+int g53h_swiglu_split(float *y, const float *g, const float *u, long m, float limit)
+{
+    if (m <= 0) return 0;
+    hipLaunchKernelGGL(k_swiglu_split, dim3((unsigned)((m + 255) / 256)), dim3(256), 0,
+                       g53h_stream(), y, g, u, m, limit);
+    G53_LAUNCHED("k_swiglu_split");
+    return 0;
+}
+
+/* ----------------------------------------------------------------- router ---- */
+/* Dot products in double. Every product of two floats is exact in double, so the only
+ * rounding is in the additions; the reference adds sequentially, this adds per lane and
+ * then across the wave. The double sums agree whenever the additions are exact (always
+ * for bf16-valued router and input rows of ordinary range) and otherwise differ in the last
+ * double bits, which changes the float score only if it lies within that distance of a
+ * float rounding boundary. */
+__device__ float g53_router_dot(const void *gate, int dt, int e, int E, const float *x, int lane)
+{
+    double acc = 0.0;
+    if (dt == 1) {
+        const uint16_t *row = (const uint16_t *)gate + (size_t)e * E;
+        for (int i = lane; i < E; i += 64)
+            acc += (double)g53_bitsf((uint32_t)row[i] << 16) * (double)x[i];
+    } else {
+        const float *row = (const float *)gate + (size_t)e * E;
+        for (int i = lane; i < E; i += 64) acc += (double)row[i] * (double)x[i];
+    }
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    return (float)acc;
+}
+
+/* scores[t][e] = sigmoid(dot); choice[t][e] = score + bias[e]. One wave per (token, expert). */
+__global__ void __launch_bounds__(256) k_router_scores(float *__restrict__ score,
+                                                       float *__restrict__ choice,
+                                                       const float *__restrict__ x, int T,
+                                                       const void *__restrict__ gate, int dt,
+                                                       const float *__restrict__ bias, int NE, int E)
+{
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t = blockIdx.y;
+    if (e >= NE) return;
+    const float d = g53_router_dot(gate, dt, e, E, x + (size_t)t * E, lane);
+    if (lane == 0) {
+        const float s = g53_sigmoidf(d);
+        score[(size_t)t * NE + e] = s;
+        if (choice) choice[(size_t)t * NE + e] = s + bias[e];
+    }
+}
+
+/* Lane-local and wave-wide argmax with the reference's rule: strictly greater wins, so the
+ * lowest index among equal maxima; NaN never wins; -inf is never selected. */
+__device__ inline void g53_argmax_merge(float &bv, int &bi, float ov, int oi)
+{
+    if (oi < 0) return;
+    if (bi < 0 || ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+#define G53_SEL_PER_LANE 16   /* up to 1024 experts per wave */
+
+__global__ void __launch_bounds__(64) k_router_select(int *__restrict__ idx, float *__restrict__ w,
+                                                      const float *__restrict__ score,
+                                                      const float *__restrict__ choice, int NE, int K,
+                                                      int norm_topk, float routed_scale,
+                                                      int *__restrict__ nan_flag)
+{
+    const int t = blockIdx.x, lane = threadIdx.x;
+    float c[G53_SEL_PER_LANE];
+    for (int k = 0; k < G53_SEL_PER_LANE; k++) {
+        const int e = lane + 64 * k;
+        c[k] = e < NE ? choice[(size_t)t * NE + e] : -INFINITY;
+    }
+    __shared__ float sw[GLM53F_MAX_TOPK_DEV];
+    __shared__ int si[GLM53F_MAX_TOPK_DEV];
+    for (int j = 0; j < K; j++) {
+        float bv = -INFINITY;
+        int bi = -1;
+        for (int k = 0; k < G53_SEL_PER_LANE; k++)          /* ascending expert index */
+            if (c[k] > bv) { bv = c[k]; bi = lane + 64 * k; }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            g53_argmax_merge(bv, bi, ov, oi);
+        }
+        for (int k = 0; k < G53_SEL_PER_LANE; k++)
+            if (lane + 64 * k == bi) c[k] = -INFINITY;
+        if (lane == 0) si[j] = bi;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        int bad = 0;
+        for (int j = 0; j < K; j++) {
+            if (si[j] < 0) { bad = 1; si[j] = 0; }
+            sw[j] = score[(size_t)t * NE + si[j]];
+        }
+        if (bad && nan_flag) atomicOr(nan_flag, 1);
+        if (norm_topk) {
+            double s = 0.0;
+            for (int j = 0; j < K; j++) s += (double)sw[j];
+            for (int j = 0; j < K; j++) sw[j] = (float)((double)sw[j] / (s + 1e-20));
+        }
+        for (int j = 0; j < K; j++) {
+            idx[(size_t)t * K + j] = si[j];
+            w[(size_t)t * K + j] = sw[j] * routed_scale;
+        }
+    }
+}
+
+int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate, int gate_dt,
+                     const float *bias, int NE, int E, int K, int norm_topk, float routed_scale,
+                     int *nan_flag, float *scratch)
+{
+    if (NE < 1 || NE > 64 * G53_SEL_PER_LANE) return g53h_fail("g53h_router: %d experts (max 1024)", NE);
+    if (K < 1 || K > NE || K > GLM53F_MAX_TOPK_DEV) return g53h_fail("g53h_router: topk %d", K);
+    float *score = scratch, *choice = scratch + (size_t)T * NE;
+    hipLaunchKernelGGL(k_router_scores, dim3((NE + 3) / 4, T), dim3(256), 0, g53h_stream(), score,
+                       choice, x, T, gate, gate_dt, bias, NE, E);
+    G53_LAUNCHED("k_router_scores");
+    hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), 0, g53h_stream(), idx, w, score, choice,
+                       NE, K, norm_topk, routed_scale, nan_flag);
+    G53_LAUNCHED("k_router_select");
+    return 0;
+}
+
+extern "C" int g53h_router(int *idx, float *w, const float *x, int T, const void *gate, int gate_dt,
+                           const float *bias, int NE, int E, int K, int norm_topk,
+                           float routed_scale, int *nan_flag)
+{
+    if (g53h_ready()) return -1;
+    if (T <= 0) return 0;
+    float *ws = (float *)g53h_workspace((size_t)2 * T * (NE > 0 ? NE : 1) * sizeof(float));
+    if (!ws) return -1;
+    return g53h_router_into(idx, w, x, T, gate, gate_dt, bias, NE, E, K, norm_topk, routed_scale,
+                            nan_flag, ws);
+}
+
+/* route_topn (src/core/glm53f_ops.c:1021-1042): the scan starts from expert 0, so a NaN at
+ * index 0 wins every round and NaN elsewhere is skipped. */
+__global__ void __launch_bounds__(64) k_route_topn(int *__restrict__ idx, int n,
+                                                   const float *__restrict__ choice, int NE)
+{
+    const int lane = threadIdx.x;
+    float c[G53_SEL_PER_LANE];
+    for (int k = 0; k < G53_SEL_PER_LANE; k++) {
+        const int e = lane + 64 * k;
+        c[k] = e < NE ? choice[e] : NAN;
+    }
+    for (int j = 0; j < n; j++) {
+        const float c0 = __shfl(c[0], 0);
+        int best;
+        if (c0 != c0) {
+            best = 0;
+        } else {
+            float bv = -INFINITY;
+            int bi = -1;
+            for (int k = 0; k < G53_SEL_PER_LANE; k++) {
+                const int e = lane + 64 * k;
+                if (e < NE && c[k] == c[k] && (bi < 0 || c[k] > bv)) { bv = c[k]; bi = e; }
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const int oi = __shfl_xor(bi, o);
+                g53_argmax_merge(bv, bi, ov, oi);
+            }
+            best = bi < 0 ? 0 : bi;
+        }
+        for (int k = 0; k < G53_SEL_PER_LANE; k++)
+            if (lane + 64 * k == best) c[k] = -INFINITY;
+        if (lane == 0) idx[j] = best;
+    }
+}
+
+extern "C" int g53h_route_topn(int *idx, int n, const float *x, const void *gate, int gate_dt,
+                               const float *bias, int NE, int E)
+{
+    if (g53h_ready()) return -1;
+    if (n <= 0) return 0;
+    if (NE < 1 || NE > 64 * G53_SEL_PER_LANE) return g53h_fail("g53h_route_topn: %d experts", NE);
+    float *ws = (float *)g53h_workspace((size_t)2 * NE * sizeof(float));
+    if (!ws) return -1;
+    hipLaunchKernelGGL(k_router_scores, dim3((NE + 3) / 4, 1), dim3(256), 0, g53h_stream(), ws + NE,
+                       ws, x, 1, gate, gate_dt, bias, NE, E);
+    G53_LAUNCHED("k_router_scores");
+    hipLaunchKernelGGL(k_route_topn, dim3(1), dim3(64), 0, g53h_stream(), idx, n, ws, NE);
+    G53_LAUNCHED("k_route_topn");
+    return 0;
+}

@@ -1,0 +1,39 @@
+/* g53h_runtime.h - internal runtime state of the g53h library (one process, one device). */
+#ifndef G53H_RUNTIME_H
+#define G53H_RUNTIME_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#include "g53h.h"
+
+extern "C" {
+/* Record a failure message; returns -1 so callers can `return g53h_fail(...)`. */
+int  g53h_fail(const char *fmt, ...);
+/* Check a HIP status; on failure record it with the call site and return -1. */
+int  g53h_check(hipError_t e, const char *what, const char *file, int line);
+int  g53h_ready(void);         /* g53h_init(current) if needed; 0 ok            */
+int  g53h_num_cus(void);
+}
+#define G53_TRY(call) do { if (g53h_check((call), #call, __FILE__, __LINE__)) return -1; } while (0)
+/* Check the last kernel launch. */
+#define G53_LAUNCHED(name) do { if (g53h_check(hipGetLastError(), name, __FILE__, __LINE__)) return -1; } while (0)
+
+hipStream_t g53h_stream(void);        /* compute stream (initialises on first use)      */
+hipStream_t g53h_copy_stream(void);   /* side stream for host-to-HBM expert copies     */
+
+/* Library workspace in HBM, grown on demand (grow = sync + free + alloc), 256-B aligned.
+ * Regions are carved from it per call; nothing in it survives between calls except the
+ * counters region, which kernels leave zeroed. */
+void       *g53h_workspace(size_t bytes);
+/* A zero-initialised region of 4096 ints that kernels use as arrival counters and flags and
+ * always restore to zero before they exit. */
+int        *g53h_counters(void);
+
+/* Kernel timing marks (no-ops unless g53h_prof_enable(1)): tag 0 opens an interval, the
+ * tags below close the interval since the previous mark. */
+enum { G53_PROF_START = 0, G53_PROF_ROUTER = 1, G53_PROF_GATEUP = 2, G53_PROF_DOWN = 3,
+       G53_PROF_GENERIC = 4, G53_PROF_GROUPED = 5, G53_PROF_NTAGS = 8 };
+void        g53h_prof_mark(int tag);
+
+#endif /* G53H_RUNTIME_H */

@@ -1,0 +1,251 @@
+/* g53h_runtime.hip - device selection, streams, memory, timing and the workspace. */
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "g53h.h"
+#include "g53h_runtime.h"
+
+static char        g_err[512];
+static int         g_ready = 0;
+static int         g_device = -1;
+static int         g_cus = 0;
+static hipStream_t g_stream = nullptr;
+static hipStream_t g_copy = nullptr;
+static hipEvent_t  g_ev[2] = {nullptr, nullptr};
+static int         g_ev_next = 0;
+static void       *g_ws = nullptr;
+static size_t      g_ws_bytes = 0;
+static int        *g_counters = nullptr;
+
+extern "C" int g53h_fail(const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return -1;
+}
+
+extern "C" int g53h_check(hipError_t e, const char *what, const char *file, int line)
+{
+    if (e == hipSuccess) return 0;
+    return g53h_fail("%s failed at %s:%d: %s", what, file, line, hipGetErrorString(e));
+}
+
+extern "C" const char *g53h_error(void) { return g_err; }
+
+extern "C" int g53h_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+extern "C" int g53h_init(int device)
+{
+    if (g_ready && device == g_device) return 0;
+    if (g_ready) return g53h_fail("g53h_init: already bound to device %d", g_device);
+    int n = 0;
+    G53_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return g53h_fail("g53h_init: device %d of %d", device, n);
+    G53_TRY(hipSetDevice(device));
+    hipDeviceProp_t p;
+    G53_TRY(hipGetDeviceProperties(&p, device));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return g53h_fail("g53h_init: device %d is %s; this library is built for gfx950 only",
+                         device, p.gcnArchName);
+    g_cus = p.multiProcessorCount;
+    /* default priority only: streams of other priorities are not used by this library */
+    G53_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    G53_TRY(hipStreamCreateWithFlags(&g_copy, hipStreamNonBlocking));
+    G53_TRY(hipEventCreate(&g_ev[0]));
+    G53_TRY(hipEventCreate(&g_ev[1]));
+    G53_TRY(hipMalloc((void **)&g_counters, 4096 * sizeof(int)));
+    G53_TRY(hipMemset(g_counters, 0, 4096 * sizeof(int)));
+    G53_TRY(hipDeviceSynchronize());
+    g_device = device;
+    g_ready = 1;
+    return 0;
+}
+
+extern "C" int g53h_ready(void) { return g_ready ? 0 : g53h_init(0); }
+extern "C" int g53h_num_cus(void) { return g_cus; }
+hipStream_t g53h_stream(void) { return g_stream; }
+hipStream_t g53h_copy_stream(void) { return g_copy; }
+int *g53h_counters(void) { return g_counters; }
+
+extern "C" int g53h_sync(void)
+{
+    if (g53h_ready()) return -1;
+    G53_TRY(hipStreamSynchronize(g_stream));
+    G53_TRY(hipStreamSynchronize(g_copy));
+    return 0;
+}
+
+extern "C" void *g53h_alloc(size_t bytes)
+{
+    if (g53h_ready()) return nullptr;
+    void *p = nullptr;
+    if (g53h_check(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc", __FILE__, __LINE__)) return nullptr;
+    return p;
+}
+
+extern "C" int g53h_free(void *p)
+{
+    if (!p) return 0;
+    G53_TRY(hipFree(p));
+    return 0;
+}
+
+extern "C" void *g53h_host_alloc(size_t bytes)
+{
+    if (g53h_ready()) return nullptr;
+    void *p = nullptr;
+    if (g53h_check(hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc",
+                   __FILE__, __LINE__))
+        return nullptr;
+    return p;
+}
+
+extern "C" int g53h_host_free(void *p)
+{
+    if (!p) return 0;
+    G53_TRY(hipHostFree(p));
+    return 0;
+}
+
+extern "C" int g53h_h2d(void *dst, const void *src, size_t n)
+{
+    if (g53h_ready()) return -1;
+    if (!n) return 0;
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_stream));
+    G53_TRY(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+extern "C" int g53h_d2h(void *dst, const void *src, size_t n)
+{
+    if (g53h_ready()) return -1;
+    if (!n) return 0;
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_stream));
+    G53_TRY(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+extern "C" int g53h_d2d(void *dst, const void *src, size_t n)
+{
+    if (g53h_ready()) return -1;
+    if (!n) return 0;
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, g_stream));
+    return 0;
+}
+
+extern "C" int g53h_memset(void *dst, int v, size_t n)
+{
+    if (g53h_ready()) return -1;
+    if (!n) return 0;
+    G53_TRY(hipMemsetAsync(dst, v, n, g_stream));
+    return 0;
+}
+
+extern "C" int g53h_is_device_ptr(const void *p)
+{
+    if (!p || g53h_ready()) return 0;
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();                 /* unknown pointer: plain host memory */
+        return 0;
+    }
+    return a.type == hipMemoryTypeDevice;
+}
+
+extern "C" int g53h_mark(void)
+{
+    if (g53h_ready()) return -1;
+    G53_TRY(hipEventRecord(g_ev[g_ev_next], g_stream));
+    g_ev_next ^= 1;
+    return 0;
+}
+
+extern "C" float g53h_elapsed_ms(void)
+{
+    /* g_ev_next now points at the older mark */
+    hipEvent_t a = g_ev[g_ev_next], b = g_ev[g_ev_next ^ 1];
+    if (hipEventSynchronize(b) != hipSuccess) return -1.0f;
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, a, b) != hipSuccess) return -1.0f;
+    return ms;
+}
+
+extern "C" int g53h_mem_info(size_t *free_b, size_t *total_b)
+{
+    if (g53h_ready()) return -1;
+    G53_TRY(hipMemGetInfo(free_b, total_b));
+    return 0;
+}
+
+void *g53h_workspace(size_t bytes)
+{
+    if (bytes <= g_ws_bytes) return g_ws;
+    if (g_ws) {
+        if (g53h_check(hipStreamSynchronize(g_stream), "hipStreamSynchronize", __FILE__, __LINE__))
+            return nullptr;
+        (void)hipFree(g_ws);
+        g_ws = nullptr;
+        g_ws_bytes = 0;
+    }
+    size_t want = bytes + (bytes >> 2);
+    want = (want + 0xfffff) & ~(size_t)0xfffff;
+    if (g53h_check(hipMalloc(&g_ws, want), "hipMalloc(workspace)", __FILE__, __LINE__)) return nullptr;
+    g_ws_bytes = want;
+    return g_ws;
+}
+
+/* ---------------------------------------------------------------- profiling ----
+ * Per-kernel timing with HIP events on the compute stream: when enabled, the layer code
+ * records an event after each kernel it launches, tagged with the kernel's id; collection
+ * attributes each interval between consecutive events to the tag of the later event. */
+#define G53_PROF_EVENTS 16384
+static int         g_prof_on = 0;
+static hipEvent_t  g_prof_ev[G53_PROF_EVENTS];
+static int         g_prof_tag[G53_PROF_EVENTS];
+static int         g_prof_n = 0, g_prof_made = 0;
+
+extern "C" int g53h_prof_enable(int on)
+{
+    if (g53h_ready()) return -1;
+    if (on && !g_prof_made) {
+        for (int i = 0; i < G53_PROF_EVENTS; i++) G53_TRY(hipEventCreate(&g_prof_ev[i]));
+        g_prof_made = 1;
+    }
+    g_prof_on = on;
+    g_prof_n = 0;
+    return 0;
+}
+
+void g53h_prof_mark(int tag)
+{
+    if (!g_prof_on || g_prof_n >= G53_PROF_EVENTS) return;
+    if (hipEventRecord(g_prof_ev[g_prof_n], g_stream) != hipSuccess) return;
+    g_prof_tag[g_prof_n++] = tag;
+}
+
+extern "C" int g53h_prof_collect(float *ms, int *count, int ntags)
+{
+    if (g53h_ready()) return -1;
+    for (int t = 0; t < ntags; t++) { ms[t] = 0.0f; count[t] = 0; }
+    if (g_prof_n > 0) G53_TRY(hipEventSynchronize(g_prof_ev[g_prof_n - 1]));
+    for (int i = 1; i < g_prof_n; i++) {
+        const int tag = g_prof_tag[i];
+        if (tag <= 0 || tag >= ntags) continue;      /* tag 0 opens an interval only */
+        float e = 0.0f;
+        G53_TRY(hipEventElapsedTime(&e, g_prof_ev[i - 1], g_prof_ev[i]));
+        ms[tag] += e;
+        count[tag]++;
+    }
+    g_prof_n = 0;
+    return 0;
+}

@@ -1,0 +1,194 @@
+"""Seeded synthetic MoE layers on the host and in HBM.
+
+Every array is a pure function of (seed, stream); the streams below fix which stream each
+tensor draws from, so tests, golden fixtures, the bench and the CPU baseline all see the same
+inputs. Large expert weights are generated in HBM by the device generator; the host twin
+(g53h_synth_f8_host) yields the same bytes for the few experts a CPU check needs.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import G53hExpert, G53hMat, G53hMoeLayer, DevBuf, check, lib
+
+K_ROUTER, K_BIAS, K_X, K_EXPERT, K_SHARED = 1, 2, 3, 4, 5
+
+
+def stream(kind, layer=0, index=0):
+    return (layer << 40) | (kind << 32) | index
+
+
+@dataclass
+class LayerSpec:
+    E: int = 256
+    I: int = 128
+    NE: int = 16
+    K: int = 8
+    norm_topk: int = 1
+    routed_scale: float = 2.5
+    limit: float = 10.0
+    br: int = 128
+    bc: int = 128
+    router_sigma: float = 0.02
+    expert_sigma: float = 0.02
+    bias_a: float = 0.1
+    zipf_s: float | None = None      # Zipf exponent of the popularity skew, None = uniform
+    seed: int = 1
+    layer: int = 0
+    shared: bool = True
+
+    def expert_bytes(self):
+        """Codes + scales of one expert (BASELINE's 25,171,968 B at the released shapes)."""
+        sr = lambda r, c: ((r + self.br - 1) // self.br) * ((c + self.bc - 1) // self.bc) * 4
+        return 3 * self.E * self.I + 2 * sr(self.I, self.E) + sr(self.E, self.I)
+
+
+CONFIG1 = dict(E=256, I=128, NE=16, K=8, router_sigma=0.02)
+CONFIG2 = dict(E=4096, I=2048, NE=288, K=8, router_sigma=1.0 / 64.0)
+
+
+def spec(config, **kw):
+    base = {1: CONFIG1, 2: CONFIG2, 3: CONFIG2, 4: CONFIG2, 5: CONFIG2}[config]
+    d = dict(base)
+    if config == 3:
+        d["zipf_s"] = 1.1
+    d.update(kw)
+    return LayerSpec(**d)
+
+
+# ------------------------------------------------------------------------ host ----
+def normal_host(n, seed, strm, sigma, bf16):
+    out = np.empty(n, np.float32)
+    lib().g53h_synth_normal_host(out.ctypes.data, n, seed, strm, C.c_float(sigma), int(bf16))
+    return out
+
+
+def router_host(sp: LayerSpec):
+    """Router [NE][E] fp32 holding bf16 values (the checkpoint's router is bf16)."""
+    return normal_host(sp.NE * sp.E, sp.seed, stream(K_ROUTER, sp.layer), sp.router_sigma, True).reshape(sp.NE, sp.E)
+
+
+def bias_host(sp: LayerSpec):
+    """Selection bias [NE]: U(-a, a), or for a Zipf(s) popularity -0.1*(s/1.1)*ln(rank) over a
+    seeded permutation of ranks (calibrated so that top-8 selection frequency falls as rank^-s)."""
+    if sp.zipf_s is None:
+        out = np.empty(sp.NE, np.float32)
+        lib().g53h_synth_uniform_host(out.ctypes.data, sp.NE, sp.seed, stream(K_BIAS, sp.layer),
+                                      C.c_float(sp.bias_a))
+        return out
+    rng = np.random.default_rng(sp.seed * 1000003 + sp.layer)
+    rank = rng.permutation(sp.NE) + 1
+    return (-0.1 * (sp.zipf_s / 1.1) * np.log(rank)).astype(np.float32)
+
+
+def x_host(sp: LayerSpec, T, batch=0):
+    """Activations [T][E], bf16 values N(0, 1), as fp32."""
+    return normal_host(T * sp.E, sp.seed, stream(K_X, sp.layer, batch), 1.0, True).reshape(T, sp.E)
+
+
+def _mat_shapes(sp):
+    return [(sp.I, sp.E), (sp.I, sp.E), (sp.E, sp.I)]
+
+
+def expert_host(sp: LayerSpec, e):
+    """Expert e (or the shared expert for e == 'shared') as [(codes, scales)] x 3 on the host."""
+    mats = []
+    for m, (r, c) in enumerate(_mat_shapes(sp)):
+        strm = stream(K_SHARED, sp.layer, m) if e == "shared" else stream(K_EXPERT, sp.layer, e * 3 + m)
+        w = np.empty(r * c, np.uint8)
+        s = np.empty(((r + sp.br - 1) // sp.br) * ((c + sp.bc - 1) // sp.bc), np.float32)
+        lib().g53h_synth_f8_host(w.ctypes.data, s.ctypes.data, r, c, sp.br, sp.bc, sp.seed, strm,
+                                 C.c_float(sp.expert_sigma))
+        mats.append((w, s))
+    return mats
+
+
+# ---------------------------------------------------------------------- device ----
+def _align(v, a=256):
+    return (v + a - 1) // a * a
+
+
+@dataclass
+class DeviceLayer:
+    """One MoE layer resident in HBM: router (bf16), bias, every expert in a slot of one arena
+    (codes of gate, up, down, then their scales, as the reference's expert slot), the shared
+    expert, and the device table of expert descriptors."""
+    sp: LayerSpec
+    arena: DevBuf = None
+    slot_bytes: int = 0
+    router: DevBuf = None
+    bias: DevBuf = None
+    table: DevBuf = None
+    experts: list = field(default_factory=list)
+    layer: G53hMoeLayer = None
+    router_f32: np.ndarray = None
+    bias_f32: np.ndarray = None
+
+    @classmethod
+    def build(cls, sp: LayerSpec, n_experts_present=None):
+        self = cls(sp)
+        E, I, NE = sp.E, sp.I, sp.NE
+        shapes = _mat_shapes(sp)
+        code_off, sc_off, off = [], [], 0
+        for r, c in shapes:
+            code_off.append(off)
+            off = _align(off + r * c)
+        for r, c in shapes:
+            sc_off.append(off)
+            off = _align(off + ((r + sp.br - 1) // sp.br) * ((c + sp.bc - 1) // sp.bc) * 4)
+        self.slot_bytes = _align(off, 4096)
+        nslots = NE + (1 if sp.shared else 0)
+        self.arena = DevBuf(self.slot_bytes * nslots)
+        L = lib()
+        descs = (G53hExpert * (NE + 1))()
+        for i in range(nslots):
+            base = self.arena.ptr + i * self.slot_bytes
+            mats = []
+            for m, (r, c) in enumerate(shapes):
+                strm = stream(K_SHARED, sp.layer, m) if i == NE else stream(K_EXPERT, sp.layer, i * 3 + m)
+                w, s = base + code_off[m], base + sc_off[m]
+                check(L.g53h_synth_f8(w, s, r, c, sp.br, sp.bc, sp.seed, strm, C.c_float(sp.expert_sigma)),
+                      "g53h_synth_f8")
+                mats.append(G53hMat(w, s, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, 0))
+            descs[i] = G53hExpert(*mats)
+        self.experts = descs
+        self.table = DevBuf.from_array(np.frombuffer(bytes(descs), np.uint8))
+        self.router_f32 = router_host(sp)
+        rb = (self.router_f32.view(np.uint32) >> 16).astype(np.uint16)
+        self.router = DevBuf.from_array(rb)
+        self.bias_f32 = bias_host(sp)
+        self.bias = DevBuf.from_array(self.bias_f32)
+        self.layer = G53hMoeLayer(
+            hidden=E, inter=I, n_experts=NE, topk=sp.K, norm_topk=sp.norm_topk,
+            routed_scale=sp.routed_scale, swiglu_limit=sp.limit, router=self.router.ptr, router_dt=1,
+            bias=self.bias.ptr, experts=self.table.ptr,
+            shared=(self.table.ptr + NE * C.sizeof(G53hExpert)) if sp.shared else None,
+            block_c=sp.bc)
+        check(L.g53h_sync(), "g53h_sync")
+        return self
+
+    def fetch_expert(self, e):
+        """[(codes, scales)] x 3 of expert e (or 'shared') copied back from HBM."""
+        d = self.experts[self.sp.NE if e == "shared" else e]
+        out = []
+        for m in (d.gate, d.up, d.down):
+            w = np.empty(m.rows * m.cols, np.uint8)
+            s = np.empty(((m.rows + m.br - 1) // m.br) * m.scols, np.float32)
+            check(lib().g53h_d2h(w.ctypes.data, m.w, w.nbytes), "d2h")
+            check(lib().g53h_d2h(s.ctypes.data, m.s, s.nbytes), "d2h")
+            out.append((w, s))
+        return out
+
+    def forward(self, out: DevBuf, x: DevBuf, T, idx: DevBuf = None, w: DevBuf = None):
+        check(lib().g53h_moe(out.ptr, x.ptr, T, C.byref(self.layer), idx.ptr if idx else None,
+                             w.ptr if w else None), "g53h_moe")
+
+    def algorithmic_bytes(self, n_unique_routed):
+        """HBM bytes one layer call must read: each unique routed expert and the shared expert
+        once, the bf16 router and the bias."""
+        sp = self.sp
+        return (n_unique_routed + (1 if sp.shared else 0)) * sp.expert_bytes() + sp.NE * sp.E * 2 + sp.NE * 4

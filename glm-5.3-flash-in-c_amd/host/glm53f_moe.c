@@ -1,0 +1,543 @@
+/* glm53f_moe.c - the reference's expert-path entry points, served by the gfx950 kernels.
+ *
+ * Same signatures and the same observable behaviour as src/core/glm53f_ops.c of the
+ * reference: routing, the expert order, the drop path, the hint/prefetch protocol of
+ * moe_chunk (src/core/glm53f_ops.c:1144-1342) and the abort-on-error convention. The
+ * arithmetic runs on the GPU through g53h.h; this file only moves operands, drives the expert
+ * source and keeps weights resident.
+ *
+ * Host weights (router, bias, shared expert, host expert views) are uploaded to HBM once
+ * and found again by their host address in a small open-addressing table; a pointer that is
+ * already HBM is used as is. Host expert views (an Glm53fExpertSrc that serves host memory)
+ * are copied per call into staging slots instead, since a source may reuse its memory after
+ * release().
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "g53h.h"
+#include "g53h_core.h"
+#include "glm53f.h"
+
+long glm53f_expert_drops = 0;
+int  glm53f_quiet = 0;
+
+#define G53_MOE_CHUNK 64                /* reference chunk (src/core/glm53f_ops.c:988) */
+
+static void g53_die(const char *what)
+{
+    fprintf(stderr, "glm53f: FATAL, %s: %s\n", what, g53h_error());
+    abort();
+}
+
+/* ------------------------------------------------------------ resident weights ---- */
+typedef struct { const void *h; size_t n; void *d; int dt; } G53Res;
+static G53Res *g_res = NULL;
+static size_t g_res_cap = 0, g_res_n = 0;
+
+static size_t res_hash(const void *p, size_t cap)
+{
+    uint64_t v = (uint64_t)(uintptr_t)p;
+    v ^= v >> 33; v *= 0xff51afd7ed558ccdull; v ^= v >> 33;
+    return (size_t)(v & (cap - 1));
+}
+
+static G53Res *res_find(const void *h)
+{
+    if (!g_res_cap) return NULL;
+    for (size_t i = res_hash(h, g_res_cap);; i = (i + 1) & (g_res_cap - 1)) {
+        if (g_res[i].h == h) return &g_res[i];
+        if (!g_res[i].h) return NULL;
+    }
+}
+
+static G53Res *res_insert(const void *h)
+{
+    if (2 * (g_res_n + 1) > g_res_cap) {
+        const size_t ncap = g_res_cap ? 2 * g_res_cap : 256;
+        G53Res *nt = (G53Res *)calloc(ncap, sizeof *nt);
+        if (!nt) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
+        for (size_t i = 0; i < g_res_cap; i++) {
+            if (!g_res[i].h) continue;
+            size_t j = res_hash(g_res[i].h, ncap);
+            while (nt[j].h) j = (j + 1) & (ncap - 1);
+            nt[j] = g_res[i];
+        }
+        free(g_res);
+        g_res = nt;
+        g_res_cap = ncap;
+    }
+    size_t j = res_hash(h, g_res_cap);
+    while (g_res[j].h) j = (j + 1) & (g_res_cap - 1);
+    g_res[j].h = h;
+    g_res_n++;
+    return &g_res[j];
+}
+
+/* HBM copy of n host bytes at h (or h itself when it is HBM). */
+static const void *resident(const void *h, size_t n)
+{
+    if (!h) return NULL;
+    if (g53h_is_device_ptr(h)) return h;
+    G53Res *r = res_find(h);
+    if (r && r->n >= n) return r->d;
+    void *d = g53h_alloc(n);
+    if (!d || g53h_h2d(d, h, n)) g53_die("uploading a weight to HBM");
+    if (!r) r = res_insert(h);
+    else g53h_free(r->d);
+    r->n = n; r->d = d; r->dt = -1;
+    return d;
+}
+
+/* The router as resident: fp32 rows whose values are all bf16-representable (the released
+ * checkpoint stores the router in bf16 and the engine widens it) are kept as bf16, half the
+ * bytes for the same exact values. *dt receives 0 (fp32) or 1 (bf16). */
+static const void *resident_router(const float *h, size_t n, int *dt)
+{
+    if (g53h_is_device_ptr(h)) { *dt = 0; return h; }
+    G53Res *r = res_find(h);
+    if (r && r->dt >= 0 && r->n >= n * (r->dt ? 2 : 4)) { *dt = r->dt; return r->d; }
+    int bf = 1;
+    for (size_t i = 0; i < n && bf; i++) if (g53_fbits(h[i]) & 0xffffu) bf = 0;
+    void *d;
+    size_t bytes;
+    if (bf) {
+        uint16_t *tmp = (uint16_t *)malloc(n * 2);
+        if (!tmp) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
+        for (size_t i = 0; i < n; i++) tmp[i] = (uint16_t)(g53_fbits(h[i]) >> 16);
+        bytes = n * 2;
+        d = g53h_alloc(bytes);
+        if (!d || g53h_h2d(d, tmp, bytes)) g53_die("uploading the router");
+        free(tmp);
+    } else {
+        bytes = n * 4;
+        d = g53h_alloc(bytes);
+        if (!d || g53h_h2d(d, h, bytes)) g53_die("uploading the router");
+    }
+    if (!r) r = res_insert(h);
+    else g53h_free(r->d);
+    r->n = bytes; r->d = d; r->dt = bf;
+    *dt = bf;
+    return d;
+}
+
+void glm53f_forget_host_weights(void)
+{
+    for (size_t i = 0; i < g_res_cap; i++) if (g_res[i].h) g53h_free(g_res[i].d);
+    free(g_res);
+    g_res = NULL;
+    g_res_cap = g_res_n = 0;
+}
+
+static size_t mat_code_bytes(const Glm53fMat *m) { return (size_t)m->rows * (size_t)m->cols; }
+static size_t mat_scale_bytes(const Glm53fMat *m)
+{
+    return (size_t)((m->rows + m->br - 1) / m->br) * (size_t)m->scols * sizeof(float);
+}
+
+static void check_f8(const Glm53fMat *m, const char *what)
+{
+    if (!m->w) { fprintf(stderr, "glm53f: FATAL, multiply through an unbound matrix (%s)\n", what); abort(); }
+    if (m->dt != GLM53F_WF8) {
+        fprintf(stderr, "glm53f: FATAL, %s has storage type %d; the MI355X expert path multiplies "
+                        "FP8 E4M3 matrices only\n", what, m->dt);
+        abort();
+    }
+    if (m->br <= 0 || m->bc <= 0 || m->scols != (m->cols + m->bc - 1) / m->bc) {
+        fprintf(stderr, "glm53f: FATAL, %s has block %dx%d and %d scale columns for %d columns\n",
+                what, m->br, m->bc, m->scols, m->cols);
+        abort();
+    }
+}
+
+static G53hMat dev_mat_resident(const Glm53fMat *m, const char *what)
+{
+    check_f8(m, what);
+    G53hMat d;
+    memset(&d, 0, sizeof d);
+    d.w = (const uint8_t *)resident(m->w, mat_code_bytes(m));
+    d.s = (const float *)resident(m->s, mat_scale_bytes(m));
+    d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    return d;
+}
+
+static G53hMat view_mat_f8(const Glm53fMat *m)
+{
+    G53hMat d;
+    memset(&d, 0, sizeof d);
+    d.w = (const uint8_t *)m->w; d.s = m->s;
+    d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    return d;
+}
+
+/* ---------------------------------------------------------- staging buffers ---- */
+typedef struct { void *d; size_t n; } G53Buf;
+
+static void *buf_get(G53Buf *b, size_t n)
+{
+    if (n <= b->n) return b->d;
+    if (b->d && (g53h_sync() || g53h_free(b->d))) g53_die("freeing a staging buffer");
+    b->d = g53h_alloc(n);
+    if (!b->d) g53_die("allocating a staging buffer");
+    b->n = n;
+    return b->d;
+}
+
+static G53Buf g_xin, g_out, g_idx, g_w, g_flag, g_table, g_pred, g_tmp, g_contrib;
+
+/* Host operand -> HBM (or the operand itself when it is HBM already). */
+static const float *stage_in(G53Buf *b, const float *h, size_t n)
+{
+    if (g53h_is_device_ptr(h)) return h;
+    float *d = (float *)buf_get(b, n * sizeof(float));
+    if (g53h_h2d(d, h, n * sizeof(float))) g53_die("staging an operand");
+    return d;
+}
+
+static void ensure_device(void)
+{
+    if (g53h_init(0)) g53_die("initialising the GPU");
+}
+
+/* ------------------------------------------------------------ unit operations ---- */
+float glm53f_e4m3f(uint8_t b) { return g53_e4m3_to_f32(b); }
+
+/* A matrix passed to the unit operations is copied per call (its memory may be reused by the
+ * caller for another matrix); MoE weights are the ones kept resident. */
+static G53Buf g_mat[3];
+static G53hMat dev_mat_staged(const Glm53fMat *m, G53Buf *b, const char *what)
+{
+    check_f8(m, what);
+    if (g53h_is_device_ptr(m->w)) return view_mat_f8(m);
+    const size_t cb = mat_code_bytes(m), sb = mat_scale_bytes(m);
+    uint8_t *d = (uint8_t *)buf_get(b, ((cb + 255) & ~(size_t)255) + sb);
+    if (g53h_h2d(d, m->w, cb) || g53h_h2d(d + ((cb + 255) & ~(size_t)255), m->s, sb)) g53_die(what);
+    G53hMat r = view_mat_f8(m);
+    r.w = d;
+    r.s = (const float *)(d + ((cb + 255) & ~(size_t)255));
+    return r;
+}
+
+void glm53f_mm_batch(float *y, const float *x, int T, const Glm53fMat *m)
+{
+    if (T < 1) return;
+    ensure_device();
+    const G53hMat d = dev_mat_staged(m, &g_mat[0], "glm53f_mm");
+    const float *xd = stage_in(&g_xin, x, (size_t)T * m->cols);
+    const int yd_dev = g53h_is_device_ptr(y);
+    float *yd = yd_dev ? y : (float *)buf_get(&g_out, (size_t)T * m->rows * sizeof(float));
+    if (g53h_mm_f8(yd, xd, T, &d)) g53_die("glm53f_mm");
+    if (!yd_dev && g53h_d2h(y, yd, (size_t)T * m->rows * sizeof(float))) g53_die("glm53f_mm");
+    if (yd_dev && g53h_sync()) g53_die("glm53f_mm");
+}
+
+void glm53f_mm(float *y, const float *x, const Glm53fMat *m) { glm53f_mm_batch(y, x, 1, m); }
+
+void glm53f_swiglu_clamp(float *y, const float *gu, int n, float limit)
+{
+    if (n < 1) return;
+    ensure_device();
+    const float *gd = stage_in(&g_xin, gu, (size_t)2 * n);
+    const int ydev = g53h_is_device_ptr(y);
+    float *yd = ydev ? y : (float *)buf_get(&g_out, (size_t)n * sizeof(float));
+    if (g53h_swiglu(yd, gd, n, 1, limit)) g53_die("glm53f_swiglu_clamp");
+    if (!ydev && g53h_d2h(y, yd, (size_t)n * sizeof(float))) g53_die("glm53f_swiglu_clamp");
+    if (ydev && g53h_sync()) g53_die("glm53f_swiglu_clamp");
+}
+
+size_t glm53f_mlp_scratch(const Glm53fCfg *c)
+{
+    const int I = c->dense_inter > c->moe_inter * c->n_shared ? c->dense_inter : c->moe_inter * c->n_shared;
+    return (size_t)3 * I;
+}
+
+void glm53f_mlp(float *out, const float *x, const Glm53fMat *gate, const Glm53fMat *up,
+                const Glm53fMat *down, float limit, float *scratch)
+{
+    (void)scratch;
+    ensure_device();
+    const G53hMat g = dev_mat_staged(gate, &g_mat[0], "mlp gate"), u = dev_mat_staged(up, &g_mat[1], "mlp up");
+    const G53hMat dn = dev_mat_staged(down, &g_mat[2], "mlp down");
+    const int I = gate->rows, E = down->rows;
+    const float *xd = stage_in(&g_xin, x, (size_t)gate->cols);
+    float *tmp = (float *)buf_get(&g_tmp, (size_t)3 * I * sizeof(float));
+    const int odev = g53h_is_device_ptr(out);
+    float *od = odev ? out : (float *)buf_get(&g_out, (size_t)E * sizeof(float));
+    if (g53h_mm_f8(tmp, xd, 1, &g) || g53h_mm_f8(tmp + I, xd, 1, &u) ||
+        g53h_swiglu(tmp + 2 * I, tmp, I, 1, limit) || g53h_mm_f8(od, tmp + 2 * I, 1, &dn))
+        g53_die("glm53f_mlp");
+    if (!odev && g53h_d2h(out, od, (size_t)E * sizeof(float))) g53_die("glm53f_mlp");
+    if (odev && g53h_sync()) g53_die("glm53f_mlp");
+}
+
+/* ------------------------------------------------------------------ router ---- */
+static void route_dev(int *idx_d, float *w_d, const float *xd, int T, const Glm53fMoeW *m,
+                      const Glm53fCfg *c)
+{
+    int dt = 0;
+    const void *gate = resident_router(m->gate, (size_t)c->n_experts * c->hidden, &dt);
+    const float *bias = (const float *)resident(m->bias, (size_t)c->n_experts * sizeof(float));
+    int *flag = (int *)buf_get(&g_flag, 256);
+    if (g53h_memset(flag, 0, sizeof(int)) ||
+        g53h_router(idx_d, w_d, xd, T, gate, dt, bias, c->n_experts, c->hidden, c->topk, c->norm_topk,
+                    c->routed_scale, flag))
+        g53_die("glm53f_router");
+    int bad = 0;
+    if (g53h_d2h(&bad, flag, sizeof bad)) g53_die("glm53f_router");
+    if (bad) {
+        fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) found no candidate\n");
+        abort();
+    }
+}
+
+void glm53f_router(int *idx, float *w, const float *x, const Glm53fMoeW *m, const Glm53fCfg *c)
+{
+    ensure_device();
+    if (c->n_experts > 1024) {
+        fprintf(stderr, "glm53f: FATAL, routed experts is %d, above the limit of 1024.\n", c->n_experts);
+        abort();
+    }
+    const int K = c->topk;
+    const float *xd = stage_in(&g_xin, x, (size_t)c->hidden);
+    int *idx_d = (int *)buf_get(&g_idx, (size_t)K * sizeof(int));
+    float *w_d = (float *)buf_get(&g_w, (size_t)K * sizeof(float));
+    route_dev(idx_d, w_d, xd, 1, m, c);
+    if (g53h_d2h(idx, idx_d, (size_t)K * sizeof(int)) || g53h_d2h(w, w_d, (size_t)K * sizeof(float)))
+        g53_die("glm53f_router");
+}
+
+/* ---------------------------------------------------------------------- MoE ---- */
+size_t glm53f_moe_scratch(const Glm53fCfg *c, int T)
+{
+    const size_t n = (size_t)(T < G53_MOE_CHUNK ? T : G53_MOE_CHUNK);
+    const size_t E = (size_t)c->hidden, K = (size_t)c->topk;
+    return n * K * E + n * K * 2 + (size_t)3 * c->moe_inter + E + glm53f_mlp_scratch(c) + E +
+           n * (2 * E + 3 * (size_t)c->moe_inter);
+}
+
+/* Host expert views are copied into these per-call staging slots (one per unique expert). */
+typedef struct { G53Buf b; } G53Slot;
+static G53Slot *g_hslots = NULL;
+static int g_nhslots = 0;
+
+static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off)
+{
+    G53hMat d;
+    memset(&d, 0, sizeof d);
+    const size_t cb = mat_code_bytes(m), sb = mat_scale_bytes(m);
+    uint8_t *w = dst + *off;
+    *off += (cb + 255) & ~(size_t)255;
+    uint8_t *s = dst + *off;
+    *off += (sb + 255) & ~(size_t)255;
+    if (g53h_h2d(w, m->w, cb) || g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
+    d.w = w; d.s = (const float *)s;
+    d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    return d;
+}
+
+static void check_expert_shape(const Glm53fExpertQ *q, const Glm53fCfg *c, int layer, int e)
+{
+    const Glm53fMat *ms[3] = {&q->gate, &q->up, &q->down};
+    const int rows[3] = {c->moe_inter, c->moe_inter, c->hidden}, cols[3] = {c->hidden, c->hidden, c->moe_inter};
+    for (int i = 0; i < 3; i++) {
+        check_f8(ms[i], "a routed expert matrix");
+        if (ms[i]->rows != rows[i] || ms[i]->cols != cols[i]) {
+            fprintf(stderr, "glm53f: FATAL, layer %d expert %d matrix %d is %dx%d, expected %dx%d\n",
+                    layer, e, i, ms[i]->rows, ms[i]->cols, rows[i], cols[i]);
+            abort();
+        }
+    }
+}
+
+/* Next-layer prediction for the hint protocol (src/core/glm53f_ops.c:1190-1228). */
+static int predict_next(int *pred, const float *x_host, const float *xd, const Glm53fMoeW *w,
+                        const Glm53fCfg *c, int T)
+{
+    (void)x_host;
+    const int NE = c->n_experts, E = c->hidden;
+    int per = w->prefetch_n;
+    if (per > 2 * GLM53F_MAX_TOPK) per = 2 * GLM53F_MAX_TOPK;
+    if (per <= 0) return 0;
+    int dt = 0;
+    const void *gate = resident_router(w->next_gate, (size_t)NE * E, &dt);
+    const float *bias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
+    int *pd = (int *)buf_get(&g_pred, (size_t)2 * GLM53F_MAX_TOPK * sizeof(int));
+    if (T == 1) {
+        if (g53h_route_topn(pd, per, xd, gate, dt, bias, NE, E) || g53h_d2h(pred, pd, (size_t)per * sizeof(int)))
+            g53_die("next-layer prediction");
+        return per;
+    }
+    if (!w->prefill_next) return 0;
+    /* prefill: per-token votes, most-voted first, ties in first-seen order */
+    int *votes = (int *)calloc((size_t)NE, sizeof(int)), *order = (int *)malloc((size_t)NE * sizeof(int));
+    int tmp[2 * GLM53F_MAX_TOPK], no = 0;
+    if (!votes || !order) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
+    for (int t = 0; t < T; t++) {
+        if (g53h_route_topn(pd, per, xd + (size_t)t * E, gate, dt, bias, NE, E) ||
+            g53h_d2h(tmp, pd, (size_t)per * sizeof(int)))
+            g53_die("next-layer prediction");
+        for (int j = 0; j < per; j++) {
+            if (!votes[tmp[j]]) order[no++] = tmp[j];
+            votes[tmp[j]]++;
+        }
+    }
+    for (int i = 1; i < no; i++) {
+        const int v = order[i];
+        int j = i - 1;
+        while (j >= 0 && votes[order[j]] < votes[v]) { order[j + 1] = order[j]; j--; }
+        order[j + 1] = v;
+    }
+    memcpy(pred, order, (size_t)no * sizeof(int));
+    free(votes);
+    free(order);
+    return no;
+}
+
+static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T,
+                     int with_shared)
+{
+    if (T < 1) return;
+    ensure_device();
+    const int E = c->hidden, K = c->topk, NE = c->n_experts;
+    if (NE > 1024) {
+        fprintf(stderr, "glm53f: FATAL, routed experts is %d, above the limit of 1024.\n", NE);
+        abort();
+    }
+    const float *xd = stage_in(&g_xin, x, (size_t)T * E);
+    int *idx_d = (int *)buf_get(&g_idx, (size_t)T * K * sizeof(int));
+    float *w_d = (float *)buf_get(&g_w, (size_t)T * K * sizeof(float));
+    route_dev(idx_d, w_d, xd, T, w, c);
+    int *ids = (int *)malloc((size_t)T * K * sizeof(int));
+    int *uniq = (int *)malloc((size_t)T * K * sizeof(int));
+    unsigned char *seen = (unsigned char *)calloc((size_t)NE, 1);
+    G53hExpert *table = (G53hExpert *)calloc((size_t)NE, sizeof(G53hExpert));
+    unsigned char *got = (unsigned char *)calloc((size_t)NE, 1);
+    if (!ids || !uniq || !seen || !table || !got) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
+    if (g53h_d2h(ids, idx_d, (size_t)T * K * sizeof(int))) g53_die("glm53f_moe routing");
+    int nu = 0;
+    for (int i = 0; i < T * K; i++)
+        if (!seen[ids[i]]) { seen[ids[i]] = 1; uniq[nu++] = ids[i]; }
+
+    Glm53fExpertSrc *src = w->src;
+    const int prefetch = w->prefetch_n > 0 && src->hint != NULL;
+    if (prefetch) {
+        src->hint(src, w->layer, uniq, nu);
+        if (w->next_gate) {
+            int pred[64 * 2 * GLM53F_MAX_TOPK];
+            const int np = predict_next(pred, x, xd, w, c, T);
+            if (np > 0) src->hint(src, w->layer + 1, pred, np);
+        }
+    }
+
+    /* Fetch the unique experts in first-seen order, in batches of at most topk so that a
+     * cache of topk+1 slots (the reference's minimum) never has more pinned at once; each
+     * batch is multiplied and then released. Contributions are kept per (token, slot) and
+     * combined in top-k order at the end, so the batching does not change the result. */
+    const int B = K < 16 ? K : 16;
+    if (g_nhslots < B) {
+        G53Slot *ns = (G53Slot *)realloc(g_hslots, (size_t)B * sizeof *ns);
+        if (!ns) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
+        memset(ns + g_nhslots, 0, (size_t)(B - g_nhslots) * sizeof *ns);
+        g_hslots = ns;
+        g_nhslots = B;
+    }
+    const int nslots = K + (with_shared ? 1 : 0);
+    G53hExpert *table_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
+    float *contrib = (float *)buf_get(&g_contrib, (size_t)T * nslots * E * sizeof(float));
+    G53hMoeLayer L;
+    memset(&L, 0, sizeof L);
+    L.hidden = E; L.inter = c->moe_inter; L.n_experts = NE; L.topk = K; L.norm_topk = c->norm_topk;
+    L.routed_scale = c->routed_scale; L.swiglu_limit = c->swiglu_limit;
+    L.experts = table_d;
+    int *held = (int *)malloc((size_t)B * sizeof(int));
+    if (!held) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
+    for (int b0 = 0; b0 < nu || (b0 == 0 && with_shared); b0 += B) {
+        const int bn = (nu - b0) < B ? (nu - b0) : B;
+        int nh = 0, block_c = 128;
+        memset(table, 0, (size_t)NE * sizeof(G53hExpert));
+        if (bn > 0 && !prefetch && src->getmany) src->getmany(src, w->layer, uniq + b0, bn);
+        for (int u = b0; u < b0 + bn; u++) {
+            const int e = uniq[u];
+            Glm53fExpertQ q;
+            memset(&q, 0, sizeof q);
+            if (src->get(src, w->layer, e, &q) != 0) {
+                glm53f_expert_drops++;
+                fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this output is CORRUPT\n",
+                        w->layer, e);
+                table[e].gate.pad_ = 1;           /* dropped: its contributions are zero */
+                continue;
+            }
+            held[nh++] = e;
+            check_expert_shape(&q, c, w->layer, e);
+            if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128) block_c = 0;
+            if (g53h_is_device_ptr(q.gate.w)) {
+                table[e].gate = view_mat_f8(&q.gate);
+                table[e].up = view_mat_f8(&q.up);
+                table[e].down = view_mat_f8(&q.down);
+            } else {
+                const size_t need = 3 * ((size_t)E * c->moe_inter + 256) + 3 * (mat_scale_bytes(&q.down) + 512);
+                uint8_t *dst = (uint8_t *)buf_get(&g_hslots[u - b0].b, need);
+                size_t off = 0;
+                table[e].gate = stage_mat(&q.gate, dst, &off);
+                table[e].up = stage_mat(&q.up, dst, &off);
+                table[e].down = stage_mat(&q.down, dst, &off);
+            }
+        }
+        L.shared = NULL;
+        if (with_shared && b0 == 0) {             /* the shared expert rides with the first batch */
+            G53hExpert sh;
+            sh.gate = dev_mat_resident(&w->sh_gate, "shared gate");
+            sh.up = dev_mat_resident(&w->sh_up, "shared up");
+            sh.down = dev_mat_resident(&w->sh_down, "shared down");
+            if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128) block_c = 0;
+            if (g53h_h2d(table_d + NE, &sh, sizeof sh)) g53_die("glm53f_moe");
+            L.shared = table_d + NE;
+        }
+        if (g53h_h2d(table_d, table, (size_t)NE * sizeof(G53hExpert))) g53_die("glm53f_moe");
+        L.block_c = block_c;
+        if (L.shared) {
+            if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
+        } else {
+            /* a layout with the shared slot still has K+1 slots per token */
+            G53hExpert none;
+            memset(&none, 0, sizeof none);
+            if (with_shared) {
+                if (g53h_h2d(table_d + NE, &none, sizeof none)) g53_die("glm53f_moe");
+                L.shared = table_d + NE;
+            }
+            if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
+        }
+        /* the kernels that read this batch have finished: release it */
+        if (g53h_sync()) g53_die("glm53f_moe");
+        if (src->release)
+            for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
+    }
+    free(held);
+    L.shared = with_shared ? table_d + NE : NULL;
+    const int odev = g53h_is_device_ptr(out);
+    float *od = odev ? out : (float *)buf_get(&g_out, (size_t)T * E * sizeof(float));
+    if (g53h_moe_combine(od, contrib, w_d, T, &L)) g53_die("glm53f_moe");
+    if (!odev) {
+        if (g53h_d2h(out, od, (size_t)T * E * sizeof(float))) g53_die("glm53f_moe");
+    } else if (g53h_sync()) {
+        g53_die("glm53f_moe");
+    }
+    free(ids); free(uniq); free(seen); free(table); free(got);
+}
+
+void glm53f_moe(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T,
+                float *scratch)
+{
+    (void)scratch;
+    moe_impl(out, x, w, c, T, 1);
+}
+
+void glm53f_moe_routed(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T,
+                       float *scratch)
+{
+    (void)scratch;
+    moe_impl(out, x, w, c, T, 0);
+}

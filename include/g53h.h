@@ -1,0 +1,147 @@
+/* g53h.h - the thin C ABI between the C host code of the expert path and the gfx950 HIP
+ * kernels. Plain pointers and sizes only; every pointer named *_d or documented as device
+ * is HBM of the current device. All calls are issued on the library's compute stream and
+ * are asynchronous unless stated; g53h_sync() waits. Return value 0 = success, -1 = error
+ * (g53h_error() then holds the message).
+ *
+ * The reference has no device code for this path (its CUDA backend sends routed experts
+ * back to the CPU, src/gpu/glm53f_gpu.c:1023-1041); each entry point below replaces a CPU
+ * function of src/core/glm53f_ops.c, cited per declaration.
+ */
+#ifndef G53H_H
+#define G53H_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ runtime ---- */
+int         g53h_init(int device);          /* select device, create streams; idempotent */
+int         g53h_device_count(void);
+const char *g53h_error(void);               /* last error message ("" if none)           */
+int         g53h_sync(void);                /* wait for the compute and copy streams     */
+void       *g53h_alloc(size_t bytes);       /* HBM, 256-byte aligned; NULL on failure    */
+int         g53h_free(void *p);
+void       *g53h_host_alloc(size_t bytes);  /* pinned host memory                        */
+int         g53h_host_free(void *p);
+int         g53h_h2d(void *dst_d, const void *src_h, size_t bytes);   /* synchronous */
+int         g53h_d2h(void *dst_h, const void *src_d, size_t bytes);   /* synchronous */
+int         g53h_d2d(void *dst_d, const void *src_d, size_t bytes);   /* stream-ordered */
+int         g53h_memset(void *dst_d, int value, size_t bytes);        /* stream-ordered */
+int         g53h_is_device_ptr(const void *p);   /* 1 = HBM of a device, 0 = host      */
+/* Timing on the compute stream: the elapsed time between the two most recent marks. */
+int         g53h_mark(void);
+float       g53h_elapsed_ms(void);
+/* Per-kernel timing of the layer entry points: with profiling on, each kernel launch is
+ * followed by an event; g53h_prof_collect waits and returns, per tag (1 router, 2 gate/up,
+ * 3 down+combine, 4 generic path, 5 grouped path), the summed milliseconds and the number
+ * of launches since the last collect. */
+int         g53h_prof_enable(int on);
+int         g53h_prof_collect(float *ms, int *count, int ntags);
+/* HBM size and free bytes of the current device. */
+int         g53h_mem_info(size_t *free_b, size_t *total_b);
+
+/* -------------------------------------------------------------- FP8 matrices ---- */
+/* One FP8 E4M3 matrix in HBM: codes w [rows][cols] row-major, fp32 block scales s
+ * [ceil(rows/br)][scols], scols = ceil(cols/bc). Field order mirrors Glm53fMat. */
+typedef struct {
+    const uint8_t *w;
+    const float   *s;
+    int rows, cols, br, bc, scols;
+    int pad_;
+} G53hMat;
+
+/* One expert: gate [I][E], up [I][E], down [E][I]. A NULL gate.w marks an expert that
+ * is not there: with gate.pad_ == 1 it could not be loaded (its contributions are zero, as
+ * the reference's drop path); otherwise it is outside the current batch (g53h_moe_partial). */
+typedef struct {
+    G53hMat gate, up, down;
+} G53hExpert;
+
+/* y[T][rows] = M . x[T][cols], bit-exact with glm53f_mm per token
+ * (replaces src/core/glm53f_ops.c:185-228 matmul_f8 and :376-444 matmul_f8_batch). */
+int g53h_mm_f8(float *y_d, const float *x_d, int T, const G53hMat *m);
+
+/* y[T][n] = swiglu_clamp(gu[T][2n]) (replaces src/core/glm53f_ops.c:486-494). */
+int g53h_swiglu(float *y_d, const float *gu_d, int n, int T, float limit);
+
+/* Router for T tokens (replaces src/core/glm53f_ops.c:945-976 glm53f_router): idx [T][K],
+ * w [T][K]. gate is [n_experts][hidden] fp32 (gate_dt 0) or bf16 bits (gate_dt 1). A token
+ * whose selection finds no finite candidate sets *nan_flag_d (int, device) to 1. */
+int g53h_router(int *idx_d, float *w_d, const float *x_d, int T, const void *gate_d,
+                int gate_dt, const float *bias_d, int n_experts, int hidden, int topk,
+                int norm_topk, float routed_scale, int *nan_flag_d);
+
+/* Next-layer prediction (replaces src/core/glm53f_ops.c:1021-1042 route_topn): the n best
+ * experts of sigmoid(W x) + bias for one token, strict order, lowest index on ties. */
+int g53h_route_topn(int *idx_d, int n, const float *x_d, const void *gate_d, int gate_dt,
+                    const float *bias_d, int n_experts, int hidden);
+
+/* ---------------------------------------------------------------- MoE layer ---- */
+typedef struct {
+    int   hidden, inter, n_experts, topk, norm_topk;
+    float routed_scale, swiglu_limit;
+    const void       *router;       /* device [n_experts][hidden], fp32 or bf16            */
+    int               router_dt;    /* 0 fp32, 1 bf16                                      */
+    const float      *bias;         /* device [n_experts]                                  */
+    const G53hExpert *experts;      /* device array [n_experts] of expert descriptors      */
+    const G53hExpert *shared;       /* device pointer to one descriptor, or NULL           */
+    int               block_c;      /* FP8 column block of every expert matrix (128 takes the
+                                       tiled kernels; any other value the generic ones)     */
+} G53hMoeLayer;
+
+/* Whole MoE layer on the device (replaces src/core/glm53f_ops.c:1144-1342 moe_chunk with
+ * src/core/glm53f_ops.c:1344-1362 glm53f_moe / _routed): route, run the chosen experts and
+ * the shared expert, combine in double in top-k order. out, x: device [T][hidden].
+ * idx_d / w_d (device [T][topk]) receive the routing when non-NULL. No host round trip. */
+int g53h_moe(float *out_d, const float *x_d, int T, const G53hMoeLayer *L, int *idx_d,
+             float *w_d);
+
+/* The same with the routing already done (idx_d / w_d given, device [T][topk]); used by the
+ * host drop-in, which routes first to fetch the experts through an Glm53fExpertSrc. */
+int g53h_moe_routed_given(float *out_d, const float *x_d, int T, const G53hMoeLayer *L,
+                          const int *idx_d, const float *w_d);
+
+/* Partial layer for a host driver that fetches experts in batches (the drop-in path):
+ * contributions of the slots whose expert descriptor is present go to contrib_d
+ * [T][topk + has_shared][hidden]; slots whose descriptor has gate.w == NULL are left
+ * untouched, except that a descriptor with gate.pad_ == 1 (a dropped expert) writes zeros.
+ * g53h_moe_combine then forms out = (float)(sum_j w_j contrib_j in double) (+ shared). */
+int g53h_moe_partial(float *contrib_d, const float *x_d, int T, const G53hMoeLayer *L,
+                     const int *idx_d);
+int g53h_moe_combine(float *out_d, const float *contrib_d, const float *w_d, int T,
+                     const G53hMoeLayer *L);
+
+/* -------------------------------------------------------- checks and inputs ---- */
+/* y[i] = expf(x[i]) by the device restatement of glibc's expf (for exhaustive checks). */
+int g53h_expf(float *y_d, const float *x_d, size_t n);
+/* y[i] = expf of the float whose bit pattern is base + i, i < n (no input buffer). */
+int g53h_expf_range(float *y_d, uint32_t base, size_t n);
+/* Host twin of the device expf restatement (the same source compiled for the CPU). */
+void g53h_expf_host(float *y, const float *x, size_t n);
+/* out[i] = E4M3 code[i] decoded by the gfx950 conversion instruction the kernels use. */
+int g53h_e4m3_decode(float *out_d, const uint8_t *codes_d, size_t n);
+
+/* Seeded synthetic FP8 matrix: element (i,j) ~ N(0, sigma^2) from (seed, stream, i*cols+j),
+ * quantised per br x bc block by the absmax rule. The host twin g53h_synth_f8_host gives the
+ * same bytes on the CPU. */
+int  g53h_synth_f8(uint8_t *w_d, float *s_d, int rows, int cols, int br, int bc,
+                   uint64_t seed, uint64_t stream, float sigma);
+void g53h_synth_f8_host(uint8_t *w, float *s, int rows, int cols, int br, int bc,
+                        uint64_t seed, uint64_t stream, float sigma);
+/* n values N(0, sigma^2) (host); as bf16 bit patterns widened to float when bf16 != 0. */
+void g53h_synth_normal_host(float *out, size_t n, uint64_t seed, uint64_t stream, float sigma,
+                            int bf16);
+/* q[i] = E4M3(clamp(x[i] * scale, +-448)), the generator's quantiser (host). */
+void g53h_quant_host(uint8_t *q, const float *x, size_t n, float scale);
+/* n values U(-a, a) (host). */
+void g53h_synth_uniform_host(float *out, size_t n, uint64_t seed, uint64_t stream, float a);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* G53H_H */

@@ -1,0 +1,105 @@
+/* ref_shim.c - a flat C entry layer over the reference's own expert path, for the tests.
+ *
+ * TEST INFRASTRUCTURE ONLY. Compiled together with the reference's unmodified sources
+ * (src/core/glm53f_ops.c, src/core/glm53f_dsa.c, read where they lie under /root/reference)
+ * into oracle/_ref/libglm53f_ref.so by oracle/Makefile. The reference's header types are
+ * used as the reference declares them. Experts are served from caller memory through an
+ * in-memory Glm53fExpertSrc (get returns views, release does nothing; a NULL gate marks a
+ * failed load), which is the seam the reference's own docs name for faking the source.
+ */
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "glm53f.h"
+
+typedef struct {
+    const uint8_t *gw, *uw, *dw;
+    const float   *gs, *us, *ds;
+} RefExpert;
+
+typedef struct {
+    Glm53fExpertSrc src;              /* first member: the MoE passes &src back */
+    const RefExpert *ex;
+    int E, I, br, bc;
+} MemSrc;
+
+static void fill(Glm53fMat *m, const uint8_t *w, const float *s, int rows, int cols, int br, int bc)
+{
+    memset(m, 0, sizeof *m);
+    m->w = w; m->s = s; m->dt = GLM53F_WF8;
+    m->rows = rows; m->cols = cols; m->br = br; m->bc = bc; m->scols = (cols + bc - 1) / bc;
+}
+
+static int mem_get(Glm53fExpertSrc *self, int layer, int e, Glm53fExpertQ *q)
+{
+    (void)layer;
+    MemSrc *m = (MemSrc *)self;
+    const RefExpert *x = &m->ex[e];
+    if (!x->gw) return -1;
+    fill(&q->gate, x->gw, x->gs, m->I, m->E, m->br, m->bc);
+    fill(&q->up, x->uw, x->us, m->I, m->E, m->br, m->bc);
+    fill(&q->down, x->dw, x->ds, m->E, m->I, m->br, m->bc);
+    return 0;
+}
+
+static void cfg_of(Glm53fCfg *c, int E, int I, int NE, int K, int br, int bc, int norm_topk,
+                   float routed_scale, float limit)
+{
+    memset(c, 0, sizeof *c);
+    c->hidden = E; c->moe_inter = I; c->n_experts = NE; c->topk = K; c->n_shared = 1;
+    c->routed_scale = routed_scale; c->norm_topk = norm_topk; c->swiglu_limit = limit;
+    c->fp8_block_r = br; c->fp8_block_c = bc; c->n_layers = 1;
+}
+
+long ref_moe(float *out, const float *x, int T, int E, int I, int NE, int K, int br, int bc,
+             int norm_topk, float routed_scale, float limit, const float *gate, const float *bias,
+             const RefExpert *experts, const RefExpert *shared)
+{
+    Glm53fCfg c;
+    cfg_of(&c, E, I, NE, K, br, bc, norm_topk, routed_scale, limit);
+    MemSrc src;
+    memset(&src, 0, sizeof src);
+    src.src.get = mem_get;
+    src.src.ctx = &src;
+    src.ex = experts; src.E = E; src.I = I; src.br = br; src.bc = bc;
+    Glm53fMoeW w;
+    memset(&w, 0, sizeof w);
+    w.gate = gate; w.bias = bias; w.src = &src.src; w.layer = 0;
+    if (shared) {
+        fill(&w.sh_gate, shared->gw, shared->gs, I, E, br, bc);
+        fill(&w.sh_up, shared->uw, shared->us, I, E, br, bc);
+        fill(&w.sh_down, shared->dw, shared->ds, E, I, br, bc);
+    }
+    float *scratch = (float *)malloc(glm53f_moe_scratch(&c, T) * sizeof(float));
+    if (!scratch) return -1;
+    const long drops0 = glm53f_expert_drops;
+    if (shared) glm53f_moe(out, x, &w, &c, T, scratch);
+    else glm53f_moe_routed(out, x, &w, &c, T, scratch);
+    free(scratch);
+    return glm53f_expert_drops - drops0;
+}
+
+void ref_router(int *idx, float *wt, const float *x, int E, int NE, int K, int norm_topk,
+                float routed_scale, const float *gate, const float *bias)
+{
+    Glm53fCfg c;
+    cfg_of(&c, E, 1, NE, K, 128, 128, norm_topk, routed_scale, 10.0f);
+    Glm53fMoeW w;
+    memset(&w, 0, sizeof w);
+    w.gate = gate; w.bias = bias;
+    glm53f_router(idx, wt, x, &w, &c);
+}
+
+void ref_mm(float *y, const float *x, int T, const uint8_t *W, const float *S, int rows, int cols,
+            int br, int bc)
+{
+    Glm53fMat m;
+    fill(&m, W, S, rows, cols, br, bc);
+    if (T == 1) glm53f_mm(y, x, &m);
+    else glm53f_mm_batch(y, x, T, &m);
+}
+
+void ref_swiglu(float *y, const float *gu, int n, float limit) { glm53f_swiglu_clamp(y, gu, n, limit); }
+
+float ref_e4m3f(uint8_t b) { return glm53f_e4m3f(b); }

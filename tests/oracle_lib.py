@@ -1,0 +1,171 @@
+"""ctypes access to the checkers under oracle/ (the CPU restatement and, when built, the
+reference's own expert path). Test infrastructure: imported by tests/ and bench.py's
+cpu_baseline leg only."""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_LIB = os.path.join(ROOT, "oracle", "lib", "libg53_oracle.so")
+REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libglm53f_ref.so")
+
+
+class OrExpert(C.Structure):
+    _fields_ = [("gw", C.c_void_p), ("uw", C.c_void_p), ("dw", C.c_void_p),
+                ("gs", C.c_void_p), ("us", C.c_void_p), ("ds", C.c_void_p)]
+
+
+_or = None
+_ref = None
+
+
+def oracle():
+    global _or
+    if _or is None:
+        L = C.CDLL(ORACLE_LIB)
+        L.or_e4m3f.restype = C.c_float
+        L.or_e4m3f.argtypes = [C.c_uint8]
+        L.or_mm_f8.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                               C.c_int, C.c_int]
+        L.or_swiglu.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_float]
+        L.or_router.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                                C.c_int, C.c_int, C.c_float]
+        L.or_route_topn.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.or_moe.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                             C.c_int, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                             C.c_void_p, C.c_void_p]
+        L.or_expf_mismatches.restype = C.c_long
+        L.or_expf_mismatches.argtypes = [C.c_void_p, C.c_uint32, C.c_long, C.POINTER(C.c_long)]
+        L.or_expf.argtypes = [C.c_void_p, C.c_void_p, C.c_long]
+        _or = L
+    return _or
+
+
+def have_ref():
+    return os.path.exists(REF_LIB)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        L = C.CDLL(REF_LIB)
+        L.ref_moe.restype = C.c_long
+        L.ref_moe.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                              C.c_int, C.c_int, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_void_p,
+                              C.c_void_p]
+        L.ref_router.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                 C.c_float, C.c_void_p, C.c_void_p]
+        L.ref_mm.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
+                             C.c_int, C.c_int]
+        L.ref_swiglu.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_float]
+        L.ref_e4m3f.restype = C.c_float
+        L.ref_e4m3f.argtypes = [C.c_uint8]
+        _ref = L
+    return _ref
+
+
+def _p(a):
+    return a.ctypes.data if a is not None else None
+
+
+def mm_f8(lib, x, w, s, rows, cols, br, bc):
+    """y[T][rows] by the oracle (lib=oracle()) or the reference (lib=ref())."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, cols)
+    T = x.shape[0]
+    y = np.empty((T, rows), np.float32)
+    f = lib.or_mm_f8 if hasattr(lib, "or_mm_f8") else lib.ref_mm
+    f(y.ctypes.data, x.ctypes.data, T, w.ctypes.data, s.ctypes.data, rows, cols, br, bc)
+    return y
+
+
+def expert_table(mats_by_e, NE):
+    """OrExpert[NE] from {e: [(w, s)] x 3} (missing e: a failed load)."""
+    tab = (OrExpert * NE)()
+    keep = []
+    for e, mats in mats_by_e.items():
+        (gw, gs), (uw, us), (dw, ds) = mats
+        keep += [gw, gs, uw, us, dw, ds]
+        tab[e] = OrExpert(gw.ctypes.data, uw.ctypes.data, dw.ctypes.data, gs.ctypes.data, us.ctypes.data,
+                          ds.ctypes.data)
+    return tab, keep
+
+
+def moe(lib, x, sp, router, bias, mats_by_e, shared_mats):
+    """Layer output [T][E], idx [T][K], w [T][K] by the oracle or the reference."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, sp.E)
+    T = x.shape[0]
+    out = np.zeros((T, sp.E), np.float32)
+    tab, keep = expert_table(mats_by_e, sp.NE)
+    sh = None
+    if shared_mats is not None:
+        sht, keep2 = expert_table({0: shared_mats}, 1)
+        keep += keep2
+        sh = C.byref(sht[0])
+    router = np.ascontiguousarray(router, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    if hasattr(lib, "or_moe"):
+        idx = np.zeros((T, sp.K), np.int32)
+        w = np.zeros((T, sp.K), np.float32)
+        rc = lib.or_moe(out.ctypes.data, x.ctypes.data, T, sp.E, sp.I, sp.NE, sp.K, sp.br, sp.bc, sp.norm_topk,
+                        sp.routed_scale, sp.limit, router.ctypes.data, bias.ctypes.data, C.addressof(tab),
+                        sh, idx.ctypes.data, w.ctypes.data)
+        assert rc == 0
+        return out, idx, w
+    lib.ref_moe(out.ctypes.data, x.ctypes.data, T, sp.E, sp.I, sp.NE, sp.K, sp.br, sp.bc, sp.norm_topk,
+                sp.routed_scale, sp.limit, router.ctypes.data, bias.ctypes.data, C.addressof(tab), sh)
+    return out, None, None
+
+
+def router(lib, x, sp, router_w, bias):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, sp.E)
+    T = x.shape[0]
+    idx = np.zeros((T, sp.K), np.int32)
+    w = np.zeros((T, sp.K), np.float32)
+    rw = np.ascontiguousarray(router_w, np.float32)
+    b = np.ascontiguousarray(bias, np.float32)
+    for t in range(T):
+        xt = np.ascontiguousarray(x[t])
+        if hasattr(lib, "or_router"):
+            rc = lib.or_router(idx[t].ctypes.data, w[t].ctypes.data, xt.ctypes.data, rw.ctypes.data, b.ctypes.data,
+                               sp.NE, sp.E, sp.K, sp.norm_topk, sp.routed_scale)
+            assert rc == 0
+        else:
+            lib.ref_router(idx[t].ctypes.data, w[t].ctypes.data, xt.ctypes.data, sp.E, sp.NE, sp.K, sp.norm_topk,
+                           sp.routed_scale, rw.ctypes.data, b.ctypes.data)
+    return idx, w
+
+
+def fp8_kat_cases():
+    """All five matvec cases of the reference's test_fp8 main() (tests/unit/test_fp8.c:150-157),
+    with the reference's own inputs (tests/unit/test_fp8.c:41-54): one LCG stream
+    (rng = rng*1664525 + 1013904223 from 12345, next() = rng >> 8) consumed in the reference's
+    order; codes are the element index for the first 256 and next() after, NaN codes (low seven
+    bits all ones) flipped unless the case keeps them; scales (next()%1000+1)*1e-6f; x
+    ((next()%20001) - 10000)*1e-4f."""
+    L = oracle()
+    L.or_lcg.argtypes = [C.POINTER(C.c_uint32), C.c_void_p, C.c_long]
+    state = C.c_uint32(12345)
+
+    def draw(n):
+        out = np.empty(max(n, 0), np.uint32)
+        if n > 0:
+            L.or_lcg(C.byref(state), out.ctypes.data, n)
+        return out
+
+    cases = []
+    for rows, cols, br, bc, with_nan in [(2048, 4096, 128, 128, 0), (4096, 2048, 128, 128, 0),
+                                         (37, 1021, 16, 128, 0), (9, 13, 4, 4, 0), (64, 256, 128, 64, 1)]:
+        srows, scols = (rows + br - 1) // br, (cols + bc - 1) // bc
+        n = rows * cols
+        w = np.arange(n, dtype=np.uint64)
+        w[256:] = draw(n - 256)
+        w = (w & 0xff).astype(np.uint8)
+        if not with_nan:
+            nan = (w & 0x7f) == 0x7f
+            w[nan] ^= 1
+        s = (draw(srows * scols) % 1000 + 1).astype(np.float32) * np.float32(1e-6)
+        x = ((draw(cols) % 20001).astype(np.int64) - 10000).astype(np.float32) * np.float32(1e-4)
+        cases.append(dict(rows=rows, cols=cols, br=br, bc=bc, with_nan=with_nan, w=w, s=s.astype(np.float32),
+                          x=x.astype(np.float32)))
+    return cases
