@@ -1,0 +1,224 @@
+/* g53h_gemv.h - device building blocks of the bit-exact FP8 GEMV kernels (decode path). */
+#ifndef G53H_GEMV_H
+#define G53H_GEMV_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "g53h.h"
+#include "g53h_core.h"
+
+/* Block-lane layout. Lane i of a wave owns 128-column block i % NBLK of row i / NBLK, so one
+ * wave instruction reads 64 consecutive 16-byte pieces spaced 128 bytes apart, and the eight
+ * loads of a block cover 64 * 128 consecutive bytes of HBM: a wave streams 8 KB of contiguous
+ * codes per step. Every lane computes the reference's sum of its block (eight fp32 FMA chains
+ * over columns l, l+8, ..., the double tree, times the block scale) and writes that double
+ * to LDS; the row's double sum over blocks, which the reference takes in block order, is then
+ * formed by one lane per row reading the row's terms in order. */
+typedef float g53_f2 __attribute__((ext_vector_type(2)));
+
+/* Expert pointers come from a descriptor in memory, so the compiler cannot tell they are
+ * global and would emit flat loads, which also count against the LDS wait counter. Loads
+ * through the global address space keep the two counters apart. */
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __attribute__((address_space(1))) const uint4 g53_gu4;
+typedef __attribute__((address_space(1))) const float g53_gf;
+#else
+typedef const uint4 g53_gu4;
+typedef const float g53_gf;
+#endif
+
+__device__ __forceinline__ void g53_ld_blk(uint4 (&c)[8], const uint8_t *p)
+{
+    g53_gu4 *q = (g53_gu4 *)p;
+#pragma unroll
+    for (int k = 0; k < 8; k++) c[k] = q[k];
+}
+
+/* The block sum with x in LDS, stored swizzled: 16-byte chunk q of block b sits at chunk
+ * q ^ (b & 31) of the block, so the lanes of different blocks read different banks. */
+__device__ __forceinline__ double g53_blk_lds(const uint4 (&c)[8], const float *xb, int b)
+{
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t d[4] = {c[k].x, c[k].y, c[k].z, c[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = 4 * k + i, e = 4 * q, l = e & 7;
+            const float4 xq = *(const float4 *)(xb + 4 * (q ^ (b & 31)));
+            const g53_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[i], false);
+            const g53_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[i], true);
+            a[l + 0] = __builtin_fmaf(lo[0], xq.x, a[l + 0]);
+            a[l + 1] = __builtin_fmaf(lo[1], xq.y, a[l + 1]);
+            a[l + 2] = __builtin_fmaf(hi[0], xq.z, a[l + 2]);
+            a[l + 3] = __builtin_fmaf(hi[1], xq.w, a[l + 3]);
+        }
+    }
+    return (((double)a[0] + a[4]) + ((double)a[2] + a[6]))
+         + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
+}
+
+/* Copy a vector of n floats (n a multiple of 128) into LDS with the block swizzle. */
+__device__ __forceinline__ void g53_vec_to_lds(float *dst, const float *src, int n, int tid, int nthr)
+{
+    for (int c = tid; c < n / 4; c += nthr) {
+        const int e = 4 * c, blk = e / 128, q = (e % 128) / 4;
+        *(float4 *)(dst + blk * 128 + 4 * (q ^ (blk & 31))) = *(const float4 *)(src + e);
+    }
+}
+
+/* Gate and up products with the SwiGLU. Wave w of the grid owns n_o consecutive values of o of
+ * one slot: it streams the n_o gate rows (RPW = 64/NBLK rows per step, one 128-column block
+ * per lane, 8 KB of consecutive HBM bytes per step), then the n_o up rows. Each lane writes its
+ * block's scaled double term to LDS; at the end lane r < 2*n_o adds the terms of buffered row
+ * r in block order (the reference's sequential double sum), and lane r < n_o pairs gate row
+ * r with up row n_o + r for the SwiGLU. n_o = G53GuShape<NBLK>::NO. Grid:
+ * (ceil(nslots * I / n_o / 4), T), 256 threads. */
+
+/* Agent-scope relaxed accesses: coherent across the XCDs' L2 caches (the compiler emits the
+ * sc1 cache policy) without the L2 writeback / invalidate of a release / acquire fence. Used
+ * for the few values one workgroup hands to another inside a kernel. */
+__device__ __forceinline__ void g53_st_agent(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float g53_ld_agent(const float *p)
+{
+    return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int g53_ld_agent_i(const int *p)
+{
+    return __hip_atomic_load((int *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* ----------------------------------------------------------------- router ---- */
+/* Dot products in double. Every product of two floats is exact in double, so the only
+ * rounding is in the additions; the reference adds sequentially, this adds per lane and
+ * then across the wave. The double sums agree whenever the additions are exact (always
+ * for bf16-valued router and input rows of ordinary range) and otherwise differ in the last
+ * double bits, which changes the float score only if it lies within that distance of a
+ * float rounding boundary. */
+__device__ __forceinline__ float g53_router_dot(const void *gate, int dt, int e, int E, const float *x, int lane)
+{
+    double acc = 0.0;
+    if (dt == 1 && E % 512 == 0) {
+        /* bf16 rows: each lane takes E/64 consecutive weights, read 16 bytes at a time */
+        const int per = E / 64;
+        const uint16_t *row = (const uint16_t *)gate + (size_t)e * E + lane * per;
+        const float *xl = x + lane * per;
+        for (int i = 0; i < per; i += 8) {
+            const uint4 q = *(const uint4 *)(row + i);
+            const float4 x0 = *(const float4 *)(xl + i), x1 = *(const float4 *)(xl + i + 4);
+            const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                acc += (double)g53_bitsf(d[k] << 16) * (double)xv[2 * k];
+                acc += (double)g53_bitsf(d[k] & 0xffff0000u) * (double)xv[2 * k + 1];
+            }
+        }
+    } else if (dt == 1) {
+        const uint16_t *row = (const uint16_t *)gate + (size_t)e * E;
+        for (int i = lane; i < E; i += 64)
+            acc += (double)g53_bitsf((uint32_t)row[i] << 16) * (double)x[i];
+    } else {
+        const float *row = (const float *)gate + (size_t)e * E;
+        for (int i = lane; i < E; i += 64) acc += (double)row[i] * (double)x[i];
+    }
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    return (float)acc;
+}
+
+
+
+/* Loads of values another workgroup wrote in this kernel: a buffer load with the sc1 cache
+ * policy (coherent across the XCDs), 16 bytes per lane. base must stay valid for the offset. */
+__device__ __forceinline__ float4 g53_ld4_agent(const float *base, int byte_off)
+{
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff,
+                                                                       0x00020000);
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+}
+
+/* Total order of floats as unsigned keys (larger float -> larger key; +0 and -0 equal). */
+__device__ __forceinline__ uint32_t g53_fkey(float f)
+{
+    if (f == 0.0f) f = 0.0f;
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* Top-k of choice[0..NE) by one wave, equal to the reference's k rounds of "first strictly
+ * greater" argmax (src/core/glm53f_ops.c:957-969): larger value first, the lower index first
+ * among equal values, NaN and -inf never chosen. sel_out[0..K) receives the indices in that
+ * order (-1 where fewer than K experts are selectable). NE <= 1024, K <= 64. The threshold
+ * (the K-th largest key) is found by a binary search over keys with wave ballots, then the
+ * chosen K are ranked among themselves. Must be called by all 64 lanes of one wave. */
+__device__ __forceinline__ void g53_topk_wave(const float *choice, int NE, int K, int *sel_out,
+                                              uint32_t *kbuf, int *ebuf)
+{
+    const int lane = threadIdx.x & 63;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint32_t key[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int e = lane + 64 * v;
+        const float f = e < NE ? choice[e] : -INFINITY;
+        key[v] = (f > -INFINITY) ? g53_fkey(f) : 0u;       /* 0: not selectable */
+    }
+    /* tau = the largest key with at least K keys >= tau (1 if fewer than K are selectable) */
+    uint32_t lo = 1u, hi = 0xffffffffu;
+    while (lo < hi) {
+        const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+        int c = 0;
+#pragma unroll
+        for (int v = 0; v < 16; v++) c += __popcll(__ballot(key[v] >= mid));
+        if (c >= K) lo = mid; else hi = mid - 1;
+    }
+    const uint32_t tau = lo;
+    int gt = 0;
+#pragma unroll
+    for (int v = 0; v < 16; v++) gt += __popcll(__ballot(key[v] > tau));
+    int need = K - gt;                                    /* ties at tau, lowest index first */
+    int pos = 0;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        bool chosen = key[v] > tau;
+        const uint64_t tm = __ballot(key[v] == tau && key[v] != 0u);
+        if (need > 0 && tm) {
+            uint64_t take = tm;
+            const int n = __popcll(tm);
+            if (n > need) {                                /* keep the lowest `need` lanes */
+                uint64_t m = tm;
+                for (int i = 0; i < need; i++) m &= m - 1;  /* drop the lowest `need` bits ... */
+                take = tm & ~m;                             /* ... what was dropped is taken  */
+            }
+            chosen = chosen || ((take >> lane) & 1ull);
+            need -= __popcll(take);
+        }
+        const uint64_t cm = __ballot(chosen);
+        if (chosen) {
+            const int p = pos + __popcll(cm & lt);
+            kbuf[p] = key[v];
+            ebuf[p] = lane + 64 * v;
+        }
+        pos += __popcll(cm);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < K) sel_out[lane] = -1;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < pos) {
+        const uint32_t kv = kbuf[lane];
+        const int ev = ebuf[lane];
+        int rank = 0;
+        for (int j = 0; j < pos; j++) rank += (kbuf[j] > kv) || (kbuf[j] == kv && ebuf[j] < ev);
+        sel_out[rank] = ev;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+}
+
+#endif /* G53H_GEMV_H */

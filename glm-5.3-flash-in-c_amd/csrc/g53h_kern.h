@@ -12,6 +12,13 @@ int g53h_slot_mm_generic(float *y, const float *x, int T, int K, int nslots,
                          const G53hExpert *experts, const int *idx, const G53hExpert *shared,
                          int which, int rows, int cols, int x_per_slot);
 int g53h_combine_into(float *out, const float *contrib, const float *wts, int T, int E, int K, int nslots);
+int g53h_resolve_slots(G53hExpert *slots, const G53hExpert *experts, const int *idx, const G53hExpert *shared,
+                       int T, int K);
+int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate, int gate_dt,
+                     const float *bias, int NE, int E, int K, int norm_topk, float routed_scale,
+                     int *nan_flag, float *scratch, const G53hExpert *experts, const G53hExpert *shared,
+                     G53hExpert *slots);
+int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out);
 int g53h_swiglu_split(float *y, const float *g, const float *u, long m, float limit);
 
 #endif /* G53H_KERN_H */

@@ -25,249 +25,161 @@
 #include "g53h_kern.h"
 #include "g53h_runtime.h"
 
-#define G53_WG 256
-#define G53_PASS (G53_WG * 128)        /* bytes of codes per pass: one block per thread */
-#define G53_MAXPASS 4                  /* passes per workgroup */
-
 typedef float g53_f2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void *g53_lds_ptr;
 
-/* One 16-byte direct HBM->LDS load per lane (global_load_lds_dwordx4): lane i's bytes land at
- * LDS offset lds_base + 16*i. Issued as inline assembly so that the compiler's wait-count
- * pass does not treat every LDS read as dependent on every pending copy (it then waits for
- * all of them and the double buffer never overlaps); the kernels wait explicitly with
- * g53_wait_vm_keep8 / g53_wait_vm_all and publish with g53_barrier. M0 carries the LDS base;
- * nothing else in these kernels uses M0. */
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void g53_dma16(const void *src, uint32_t lds_base)
-{
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(src), "s"(lds_base) : "memory", "m0");
-}
-#pragma clang diagnostic pop
+#include "g53h_gemv.h"
 
-__device__ __forceinline__ uint32_t g53_lds_addr(const void *p)
-{
-    return (uint32_t)(uintptr_t)(g53_lds_ptr)p;
-}
+/* Work is spread over the whole GPU in grid-stride order: at step j, wave w takes chunk
+ * j * nwaves + w, so the waves running together read one contiguous sweep of HBM (regularly
+ * strided per-wave ranges make many waves hit the same HBM channels at once). A chunk is 64
+ * lanes x one 128-column block = 8 KB of consecutive codes per matrix stream. Each lane writes
+ * its block's scaled double term to LDS; after its last step every lane takes one buffered
+ * row and adds its terms in block order (the reference's sequential double sum). */
 
-/* Stage one pass of codes into LDS. The pass is RP rows of NBLK*128 bytes; row lr of the
- * pass starts at rowptr(lr). Chunk c (16 B) of the pass lands at LDS offset 16*c and holds
- * block b = (c/8) % NBLK, 16-byte piece k = (c%8) ^ (b&7) of row lr = c / (8*NBLK). Each wave
- * instruction covers 64 consecutive chunks, i.e. 1 KB of consecutive HBM bytes. */
-template <int NBLK, typename RowPtr>
-__device__ __forceinline__ void g53_stage(uint8_t *lds, RowPtr rowptr)
-{
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t base = g53_lds_addr(lds);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int ci = (wave * 8 + i) * 64;          /* first chunk of this wave instruction */
-        const int c = ci + lane;
-        const int lr = c / (8 * NBLK);
-        const int b = (c >> 3) % NBLK;
-        const int k = (c & 7) ^ (b & 7);
-        const uint8_t *src = rowptr(lr) + b * 128 + k * 16;
-        g53_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)ci * 16));
-    }
-}
-
-/* Workgroup barrier that publishes LDS writes, without the compiler's fence (which would also
- * drain the in-flight HBM->LDS copies of the next pass). */
-__device__ __forceinline__ void g53_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-/* The reference's block sum for the thread's (row, block): codes from LDS, x from registers. */
+/* Gate and up products with the SwiGLU. A chunk is OPS = 32/NBLK consecutive values of o of
+ * one slot; lane l of a step holds block l % NBLK of row l / NBLK, rows alternating gate o,
+ * up o, gate o+1, up o+1, ... Dynamic LDS: x (swizzled), the slot table, and the term buffer
+ * of 4 waves x steps*64/NBLK rows. Grid: (nwaves / 4, T), 256 threads. */
 template <int NBLK>
-__device__ __forceinline__ double g53_block_sum(const uint8_t *lds, int lr, int b, const float (&xr)[128])
+__global__ void __launch_bounds__(256, 2)
+k_gateup(float *__restrict__ act, const float *__restrict__ x, int E, int I, int nslots,
+         const G53hExpert *__restrict__ slots, float limit, int nwaves, int steps)
 {
-    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    const uint8_t *base = lds + (size_t)(lr * NBLK + b) * 128;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const uint4 q = *(const uint4 *)(base + 16 * (k ^ (b & 7)));
-        const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int h = 0; h < 2; h++) {                /* column step 2k + h, columns 16k+8h+l */
-            const g53_f2 w0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[2 * h], false);
-            const g53_f2 w1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[2 * h], true);
-            const g53_f2 w2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[2 * h + 1], false);
-            const g53_f2 w3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[2 * h + 1], true);
-            const int e = 16 * k + 8 * h;
-            a[0] = __builtin_fmaf(w0[0], xr[e + 0], a[0]);
-            a[1] = __builtin_fmaf(w0[1], xr[e + 1], a[1]);
-            a[2] = __builtin_fmaf(w1[0], xr[e + 2], a[2]);
-            a[3] = __builtin_fmaf(w1[1], xr[e + 3], a[3]);
-            a[4] = __builtin_fmaf(w2[0], xr[e + 4], a[4]);
-            a[5] = __builtin_fmaf(w2[1], xr[e + 5], a[5]);
-            a[6] = __builtin_fmaf(w3[0], xr[e + 6], a[6]);
-            a[7] = __builtin_fmaf(w3[1], xr[e + 7], a[7]);
-        }
+    constexpr int RPW = 64 / NBLK, OPS = RPW / 2, PST = NBLK + 1;
+    extern __shared__ __attribute__((aligned(16))) double dyn_gu[];
+    float *xs = (float *)dyn_gu;                              /* NBLK*128 floats        */
+    G53hExpert *st = (G53hExpert *)(xs + NBLK * 128);         /* nslots descriptors     */
+    double *pball = (double *)(st + nslots);                  /* [4][steps*RPW*PST]     */
+    const int t = blockIdx.y;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = blockIdx.x * 4 + w;
+    const int b = lane % NBLK, rw = lane / NBLK, ol = rw >> 1, up = rw & 1;
+    const int cps = I / OPS, total = nslots * cps;            /* chunks per slot, chunks */
+    {
+        const int words = nslots * (int)(sizeof(G53hExpert) / 4);
+        const int *src = (const int *)(slots + (size_t)t * nslots);
+        for (int q = threadIdx.x; q < words; q += 256) ((int *)st)[q] = src[q];
     }
-    return (((double)a[0] + a[4]) + ((double)a[2] + a[6]))
-         + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
-}
-
-__device__ __forceinline__ void g53_load_x(float (&xr)[128], const float *x)
-{
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const float4 v = *(const float4 *)(x + 4 * i);
-        xr[4 * i + 0] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
-    }
-}
-
-__device__ __forceinline__ void g53_wait_vm_keep8() { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); }
-__device__ __forceinline__ void g53_wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-__device__ __forceinline__ const G53hExpert *g53_slot_expert(const G53hExpert *experts, const int *idx,
-                                                             const G53hExpert *shared, int K, int t, int s)
-{
-    return s < K ? &experts[idx[(size_t)t * K + s]] : shared;
-}
-
-/* act[t][s][o] = swiglu(gate_s x_t, up_s x_t) for o in this workgroup's rows.
- * Grid: (I / (HALF*npass), nslots, T); HALF = RP/2 rows of gate and of up per pass. */
-template <int NBLK>
-__global__ void __launch_bounds__(G53_WG, 2)
-k_gateup(float *__restrict__ act, const float *__restrict__ x, int E, int I, int K, int nslots,
-         const G53hExpert *__restrict__ experts, const int *__restrict__ idx,
-         const G53hExpert *__restrict__ shared, int npass, float limit)
-{
-    constexpr int RP = G53_WG / NBLK, HALF = RP / 2;
-    __shared__ __attribute__((aligned(16))) uint8_t codes[2][G53_PASS];
-    __shared__ double pbuf[2][G53_WG];
-    __shared__ float sct[G53_MAXPASS][G53_WG];
-    const int s = blockIdx.y, t = blockIdx.z;
-    const G53hExpert *ex = g53_slot_expert(experts, idx, shared, K, t, s);
-    const uint8_t *gw = ex->gate.w, *uw = ex->up.w;
-    if (!gw) return;                                   /* dropped expert: down writes zeros */
-    const float *gs = ex->gate.s, *us = ex->up.s;
-    const int br = ex->gate.br, scols = ex->gate.scols;
-    const int tid = threadIdx.x, lr = tid / NBLK, b = tid % NBLK;
-    const int o_first = blockIdx.x * HALF * npass;
-
-    float xr[128];
-    g53_load_x(xr, x + (size_t)t * E + b * 128);
-
-    auto rowptr_of = [&](int p) {
-        return [=](int r) -> const uint8_t * {
-            const int o = o_first + p * HALF + (r < HALF ? r : r - HALF);
-            return (r < HALF ? gw : uw) + (size_t)o * E;
-        };
-    };
-    for (int p = 0; p < npass; p++) {                 /* this thread's block scales, per pass */
-        const int o = o_first + p * HALF + (lr < HALF ? lr : lr - HALF);
-        sct[p][tid] = (lr < HALF ? gs : us)[(size_t)(o / br) * scols + b];
-    }
-    g53_stage<NBLK>(codes[0], rowptr_of(0));
-#pragma unroll 1
-    for (int p = 0; p < npass; p++) {
-        const int cur = p & 1;
-        if (p + 1 < npass) {
-            g53_stage<NBLK>(codes[cur ^ 1], rowptr_of(p + 1));
-            g53_wait_vm_keep8();
-        } else {
-            g53_wait_vm_all();
-        }
-        const float sc = sct[p][tid];
-        g53_barrier();
-        const double bs = g53_block_sum<NBLK>(codes[cur], lr, b, xr);
-        pbuf[cur][tid] = bs * (double)sc;
-        g53_barrier();
-        if (tid < HALF) {
-            double ag = 0.0, au = 0.0;
-#pragma unroll 4
-            for (int j = 0; j < NBLK; j++) ag = ag + pbuf[cur][tid * NBLK + j];
-#pragma unroll 4
-            for (int j = 0; j < NBLK; j++) au = au + pbuf[cur][(tid + HALF) * NBLK + j];
-            const int oo = o_first + p * HALF + tid;
-            act[((size_t)t * nslots + s) * I + oo] = g53_swiglu1((float)ag, (float)au, limit);
-        }
-    }
-}
-
-/* contrib[t][s][d] = down_s act[t][s] for this workgroup's rows; the last of the nslots
- * workgroups of a row tile then writes out[t][d] = (float)(sum_j w_j * contrib_j[d]) (+ the
- * shared slot). Grid: (E / (RP*npass), nslots, T). */
-template <int NBLK>
-__global__ void __launch_bounds__(G53_WG, 2)
-k_down_combine(float *__restrict__ out, float *__restrict__ contrib, const float *__restrict__ act,
-               int E, int I, int K, int nslots, const G53hExpert *__restrict__ experts,
-               const int *__restrict__ idx, const float *__restrict__ wts,
-               const G53hExpert *__restrict__ shared, int npass, int *__restrict__ counters, int fused)
-{
-    constexpr int RP = G53_WG / NBLK;
-    __shared__ __attribute__((aligned(16))) uint8_t codes[2][G53_PASS];
-    __shared__ double pbuf[2][G53_WG];
-    __shared__ float sct[G53_MAXPASS][G53_WG];
-    __shared__ int last;
-    const int s = blockIdx.y, t = blockIdx.z;
-    const G53hExpert *ex = g53_slot_expert(experts, idx, shared, K, t, s);
-    const uint8_t *dw = ex->down.w;
-    const int tid = threadIdx.x, lr = tid / NBLK, b = tid % NBLK;
-    const int d_first = blockIdx.x * RP * npass, rows = RP * npass;
-    float *crow = contrib + ((size_t)t * nslots + s) * E;
-
-    if (dw && ex->gate.w) {
-        const float *ds = ex->down.s;
-        const int br = ex->down.br, scols = ex->down.scols;
-        float xr[128];
-        g53_load_x(xr, act + ((size_t)t * nslots + s) * I + b * 128);
-        auto rowptr_of = [&](int p) {
-            return [=](int r) -> const uint8_t * { return dw + (size_t)(d_first + p * RP + r) * I; };
-        };
-        for (int p = 0; p < npass; p++)
-            sct[p][tid] = ds[(size_t)((d_first + p * RP + lr) / br) * scols + b];
-        g53_stage<NBLK>(codes[0], rowptr_of(0));
-#pragma unroll 1
-        for (int p = 0; p < npass; p++) {
-            const int cur = p & 1;
-            if (p + 1 < npass) {
-                g53_stage<NBLK>(codes[cur ^ 1], rowptr_of(p + 1));
-                g53_wait_vm_keep8();
-            } else {
-                g53_wait_vm_all();
-            }
-            const float sc = sct[p][tid];
-            g53_barrier();
-            const double bs = g53_block_sum<NBLK>(codes[cur], lr, b, xr);
-            pbuf[cur][tid] = bs * (double)sc;
-            g53_barrier();
-            if (tid < RP) {
-                double acc = 0.0;
-#pragma unroll 4
-                for (int j = 0; j < NBLK; j++) acc = acc + pbuf[cur][tid * NBLK + j];
-                crow[d_first + p * RP + tid] = (float)acc;
-            }
-        }
-    } else if (ex->gate.pad_ == G53_DROPPED) {
-        for (int r = tid; r < rows; r += G53_WG) crow[d_first + r] = 0.0f;
-    }
-    if (!fused) return;
-
-    /* arrival: publish this slot's rows, and let the last slot of the tile combine */
-    __threadfence();
+    g53_vec_to_lds(xs, x + (size_t)t * E, E, threadIdx.x, 256);
     __syncthreads();
-    int *cnt = counters + (size_t)t * gridDim.x + blockIdx.x;
-    if (tid == 0) last = (atomicAdd(cnt, 1) == nslots - 1);
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const float *wt = wts + (size_t)t * K;
-    const float *ct = contrib + (size_t)t * nslots * E;
-    for (int r = tid; r < rows; r += G53_WG) {
-        const int d = d_first + r;
-        double acc = 0.0;
-        for (int j = 0; j < K; j++) {
-            const float c = __builtin_nontemporal_load(ct + (size_t)j * E + d);
-            acc = acc + (double)wt[j] * (double)c;
-        }
-        float o = (float)acc;
-        if (nslots > K) o = o + __builtin_nontemporal_load(ct + (size_t)K * E + d);
-        out[(size_t)t * E + d] = o;
+    const float *xb = xs + b * 128;
+    double *pw = pball + (size_t)w * steps * RPW * PST;
+    uint4 cur[8];
+    float sc = 0.0f;
+    int c = wave;
+    bool have = c < total && st[c / cps].gate.w != nullptr;
+    if (have) {
+        const int s = c / cps, o = (c % cps) * OPS + ol;
+        const G53hMat &m = up ? st[s].up : st[s].gate;
+        g53_ld_blk(cur, m.w + (size_t)o * E + b * 128);
+        sc = ((g53_gf *)m.s)[(size_t)(o / m.br) * m.scols + b];
     }
-    if (tid == 0) *cnt = 0;
+    for (int j = 0; j < steps; j++, c += nwaves) {
+        const int cn = c + nwaves;
+        const bool hn = j + 1 < steps && cn < total && st[cn / cps].gate.w != nullptr;
+        uint4 nxt[8];
+        float scn = 0.0f;
+        if (hn) {
+            const int s = cn / cps, o = (cn % cps) * OPS + ol;
+            const G53hMat &m = up ? st[s].up : st[s].gate;
+            g53_ld_blk(nxt, m.w + (size_t)o * E + b * 128);
+            scn = ((g53_gf *)m.s)[(size_t)(o / m.br) * m.scols + b];
+        }
+        if (have) pw[(j * RPW + rw) * PST + b] = g53_blk_lds(cur, xb, b) * (double)sc;
+        have = hn;
+        sc = scn;
+#pragma unroll
+        for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);                      /* lgkmcnt(0): the term writes */
+    __builtin_amdgcn_wave_barrier();
+    /* lane r sums buffered row r: step r / RPW, row r % RPW of that step */
+    const int jr = lane / RPW, rr = lane % RPW, cr = wave + jr * nwaves;
+    const bool mine = lane < steps * RPW && cr < total && st[cr / cps].gate.w != nullptr;
+    float v = 0.0f;
+    if (mine) {
+        double accd = 0.0;
+        const double *pr = pw + lane * PST;
+        for (int bb = 0; bb < NBLK; bb++) accd = accd + pr[bb];
+        v = (float)accd;
+    }
+    const float u = __shfl_down(v, 1);                        /* up row of the same o */
+    if (mine && !(rr & 1)) {
+        const int s = cr / cps, o = (cr % cps) * OPS + (rr >> 1);
+        act[((size_t)t * nslots + s) * I + o] = g53_swiglu1(v, u, limit);
+    }
+}
+
+/* Down products: contrib[t][s][d] = (down_s act[t][s])[d] for the present slots (zeros for a
+ * dropped expert, nothing for an absent one). A chunk is RPW = 64/NBLK consecutive rows of one
+ * slot. Every slot's activation sits in LDS (swizzled). Dynamic LDS: activations, the slot
+ * table, the term buffer of nw waves x steps*RPW rows. Grid: (nwaves / nw, T), 64*nw threads. */
+template <int NBLK>
+__global__ void __launch_bounds__(1024)
+k_down(float *__restrict__ contrib, const float *__restrict__ act, int E, int I, int nslots,
+       const G53hExpert *__restrict__ slots, int nwaves, int steps)
+{
+    constexpr int RPW = 64 / NBLK, PST = NBLK + 1;
+    extern __shared__ __attribute__((aligned(16))) double dyn_dn[];
+    const int nw = blockDim.x >> 6, nthr = blockDim.x;
+    float *as = (float *)dyn_dn;                              /* [nslots][I]            */
+    G53hExpert *st = (G53hExpert *)(as + (size_t)nslots * I);
+    double *pball = (double *)(st + nslots);                  /* [nw][steps*RPW*PST]    */
+    const int t = blockIdx.y;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = blockIdx.x * nw + w;
+    const int b = lane % NBLK, rw = lane / NBLK;
+    const int cps = E / RPW, total = nslots * cps;
+    {
+        const int words = nslots * (int)(sizeof(G53hExpert) / 4);
+        const int *src = (const int *)(slots + (size_t)t * nslots);
+        for (int q = threadIdx.x; q < words; q += nthr) ((int *)st)[q] = src[q];
+    }
+    for (int sl = 0; sl < nslots; sl++)
+        g53_vec_to_lds(as + (size_t)sl * I, act + ((size_t)t * nslots + sl) * I, I, threadIdx.x, nthr);
+    __syncthreads();
+    double *pw = pball + (size_t)w * steps * RPW * PST;
+    uint4 cur[8];
+    float sc = 0.0f;
+    int c = wave;
+    bool have = c < total && st[c / cps].gate.w != nullptr;
+    if (have) {
+        const G53hMat &m = st[c / cps].down;
+        const int d = (c % cps) * RPW + rw;
+        g53_ld_blk(cur, m.w + (size_t)d * I + b * 128);
+        sc = ((g53_gf *)m.s)[(size_t)(d / m.br) * m.scols + b];
+    }
+    for (int j = 0; j < steps; j++, c += nwaves) {
+        const int cn = c + nwaves;
+        const bool hn = j + 1 < steps && cn < total && st[cn / cps].gate.w != nullptr;
+        uint4 nxt[8];
+        float scn = 0.0f;
+        if (hn) {
+            const G53hMat &m = st[cn / cps].down;
+            const int d = (cn % cps) * RPW + rw;
+            g53_ld_blk(nxt, m.w + (size_t)d * I + b * 128);
+            scn = ((g53_gf *)m.s)[(size_t)(d / m.br) * m.scols + b];
+        }
+        if (have) pw[(j * RPW + rw) * PST + b] = g53_blk_lds(cur, as + (size_t)(c / cps) * I + b * 128, b) * (double)sc;
+        have = hn;
+        sc = scn;
+#pragma unroll
+        for (int k = 0; k < 8; k++) cur[k] = nxt[k];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const int jr = lane / RPW, rr = lane % RPW, cr = wave + jr * nwaves;
+    if (lane < steps * RPW && cr < total) {
+        const int s = cr / cps, d = (cr % cps) * RPW + rr;
+        if (st[s].gate.w) {
+            double accd = 0.0;
+            const double *pr = pw + lane * PST;
+            for (int bb = 0; bb < NBLK; bb++) accd = accd + pr[bb];
+            contrib[((size_t)t * nslots + s) * E + d] = (float)accd;
+        } else if (st[s].gate.pad_ == G53_DROPPED) {
+            contrib[((size_t)t * nslots + s) * E + d] = 0.0f;
+        }
+    }
 }
 
 /* Generic combine for the fallback path (any shape): contrib [T][nslots][E]. */
@@ -286,65 +198,80 @@ __global__ void k_combine(float *__restrict__ out, const float *__restrict__ con
 }
 
 /* ------------------------------------------------------------------ dispatch ---- */
-static int g53_pow2_le(int v, int lim) { return v >= 1 && v <= lim && (v & (v - 1)) == 0; }
-
-/* The tiled kernels need 128-column blocks, column counts that are powers of two multiples
- * of 128, and row counts that fill whole passes. */
-static int g53_fast_ok(const G53hMoeLayer *L, int *np_gu, int *np_dn)
+/* Allow a kernel more than the default 64 KB of dynamic LDS (gfx950 has 160 KB per CU). */
+static int g53_lds_attr(const void *fn, size_t bytes)
 {
-    const int E = L->hidden, I = L->inter;
-    if (L->block_c != 128 || E % 128 || I % 128) return 0;
-    const int nbe = E / 128, nbi = I / 128;
-    if (!g53_pow2_le(nbe, 128) || !g53_pow2_le(nbi, 128)) return 0;
-    const int half = (G53_WG / nbe) / 2, rp = G53_WG / nbi;
-    if (half < 1 || I % half || E % rp) return 0;
-    int a = I / half, c = E / rp;                     /* passes per slot */
-    int pg = G53_MAXPASS, pd = G53_MAXPASS;
-    while (pg > 1 && a % pg) pg >>= 1;
-    while (pd > 1 && c % pd) pd >>= 1;
-    *np_gu = pg;
-    *np_dn = pd;
-    return 1;
+    if (bytes <= 65536) return 0;
+    G53_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    return 0;
 }
 
-/* Expert descriptors must describe 128x128-block FP8 matrices of the layer's shape for the
- * tiled path; the host drop-in checks this per expert, g53h_moe trusts the caller. */
-static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+static int g53_pow2_le(int v, int lim) { return v >= 1 && v <= lim && (v & (v - 1)) == 0; }
 
-int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate, int dt,
-                     const float *bias, int NE, int E, int K, int norm_topk, float scale,
-                     int *nan_flag, float *scratch);
+/* The block-lane kernels need 128-column blocks and 2 to 32 blocks per row of gate/up and 1
+ * to 32 per row of down (powers of two), whole chunks of rows, at most 64 slots and every
+ * slot's activation within LDS. */
+static int g53_fast_ok(const G53hMoeLayer *L)
+{
+    const int E = L->hidden, I = L->inter, nslots = L->topk + (L->shared ? 1 : 0);
+    if (L->block_c != 128 || E % 128 || I % 128 || nslots > 64) return 0;
+    const int nbe = E / 128, nbi = I / 128;
+    if (!g53_pow2_le(nbe, 32) || nbe < 2 || !g53_pow2_le(nbi, 32)) return 0;
+    if ((size_t)nslots * I * 4 > 100 * 1024) return 0;
+    return I % (32 / nbe) == 0 && E % (64 / nbi) == 0;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 /* fused != 0: every slot's expert is present or dropped, and the layer output is combined in
  * the same launch. fused == 0: contributions of the present slots only go to contrib (slots
  * whose descriptor is absent are left as they are), for the caller to combine later. */
 static int g53_layer_body(float *out, const float *x, int T, const G53hMoeLayer *L, const int *idx,
-                          const float *wts, char *ws, float *contrib, int fused)
+                          const float *wts, char *ws, float *contrib, int fused, const G53hExpert *slots)
 {
     const int E = L->hidden, I = L->inter, K = L->topk;
     const int nslots = K + (L->shared ? 1 : 0);
     float *act = (float *)ws;
     hipStream_t st = g53h_stream();
-    int np_gu = 0, np_dn = 0;
-    if (g53_fast_ok(L, &np_gu, &np_dn)) {
+    if (g53_fast_ok(L)) {
         const int nbe = E / 128, nbi = I / 128;
-        const int half = (G53_WG / nbe) / 2, rp = G53_WG / nbi;
-        const int tiles = E / (rp * np_dn);
-        int *counters = g53h_counters();
-        if ((long)T * tiles > 4096) return g53h_fail("g53h_moe: %d tokens x %d tiles exceed the counters", T, tiles);
-        dim3 g1(I / (half * np_gu), nslots, T), g2(tiles, nslots, T);
-#define G53_GU(N) case N: hipLaunchKernelGGL(k_gateup<N>, g1, dim3(G53_WG), 0, st, act, x, E, I, K, nslots, \
-                                             L->experts, idx, L->shared, np_gu, L->swiglu_limit); break
-#define G53_DN(N) case N: hipLaunchKernelGGL(k_down_combine<N>, g2, dim3(G53_WG), 0, st, out, contrib, act, E, I, \
-                                             K, nslots, L->experts, idx, wts, L->shared, np_dn, counters, fused); break
-        switch (nbe) { G53_GU(1); G53_GU(2); G53_GU(4); G53_GU(8); G53_GU(16); G53_GU(32); G53_GU(64); G53_GU(128); }
+        const int rpw_e = 64 / nbe, rpw_i = 64 / nbi, cus = g53h_num_cus();
+        /* gate/up: about 8 waves per CU in grid-stride order; each wave buffers at most 64 rows */
+        const int tot_gu = nslots * (I / (rpw_e / 2));
+        int nw_gu = 8 * cus;
+        if (nw_gu > tot_gu) nw_gu = tot_gu;
+        int st_gu = (tot_gu + nw_gu - 1) / nw_gu;
+        while (st_gu * rpw_e > 64) { nw_gu *= 2; st_gu = (tot_gu + nw_gu - 1) / nw_gu; }
+        nw_gu = (nw_gu + 3) / 4 * 4;
+        const size_t lds1 = (size_t)nbe * 128 * 4 + (size_t)nslots * sizeof(G53hExpert) +
+                            (size_t)4 * st_gu * rpw_e * (nbe + 1) * 8;
+        /* down: one workgroup of 16 waves per CU, every slot's activation in its LDS */
+        const int tot_dn = nslots * (E / rpw_i);
+        int wpg = 16, nw_dn = wpg * cus;
+        if (nw_dn > tot_dn) { nw_dn = (tot_dn + wpg - 1) / wpg * wpg; }
+        int st_dn = (tot_dn + nw_dn - 1) / nw_dn;
+        while (st_dn * rpw_i > 64) { nw_dn *= 2; st_dn = (tot_dn + nw_dn - 1) / nw_dn; }
+        const size_t lds2 = (size_t)nslots * I * 4 + (size_t)nslots * sizeof(G53hExpert) +
+                            (size_t)wpg * st_dn * rpw_i * (nbi + 1) * 8;
+        if (lds2 > 160 * 1024) return g53h_fail("g53h_moe: %zu bytes of LDS for the down kernel", lds2);
+        dim3 g1(nw_gu / 4, T), g2(nw_dn / wpg, T);
+#define G53_GU(N) case N: if (g53_lds_attr((const void *)k_gateup<N>, lds1)) return -1; \
+                          hipLaunchKernelGGL(k_gateup<N>, g1, dim3(256), lds1, st, act, x, E, I, nslots, slots, \
+                                             L->swiglu_limit, nw_gu, st_gu); break
+#define G53_DN(N) case N: if (g53_lds_attr((const void *)k_down<N>, lds2)) return -1; \
+                          hipLaunchKernelGGL(k_down<N>, g2, dim3(64 * wpg), lds2, st, contrib, act, E, I, nslots, \
+                                             slots, nw_dn, st_dn); break
+        switch (nbe) { G53_GU(2); G53_GU(4); G53_GU(8); G53_GU(16); G53_GU(32); }
         G53_LAUNCHED("k_gateup");
         g53h_prof_mark(G53_PROF_GATEUP);
-        switch (nbi) { G53_DN(1); G53_DN(2); G53_DN(4); G53_DN(8); G53_DN(16); G53_DN(32); G53_DN(64); G53_DN(128); }
-        G53_LAUNCHED("k_down_combine");
+        switch (nbi) { G53_DN(1); G53_DN(2); G53_DN(4); G53_DN(8); G53_DN(16); G53_DN(32); }
+        G53_LAUNCHED("k_down");
         g53h_prof_mark(G53_PROF_DOWN);
 #undef G53_GU
 #undef G53_DN
+        if (!fused) return 0;
+        if (g53h_combine_into(out, contrib, wts, T, E, K, nslots)) return -1;
+        g53h_prof_mark(G53_PROF_COMBINE);
         return 0;
     }
     /* any other shape: one thread per (token, slot, row), same arithmetic */
@@ -370,14 +297,18 @@ int g53h_combine_into(float *out, const float *contrib, const float *wts, int T,
 
 static size_t g53_layer_ws_bytes(const G53hMoeLayer *L, int T)
 {
-    const int E = L->hidden, I = L->inter, K = L->topk, nslots = K + (L->shared ? 1 : 0);
-    (void)E;
+    const int I = L->inter, K = L->topk, nslots = K + (L->shared ? 1 : 0);
     return align256((size_t)T * nslots * I * 4) + align256((size_t)2 * T * nslots * I * 4);
 }
 
 static size_t g53_contrib_bytes(const G53hMoeLayer *L, int T)
 {
     return align256((size_t)T * (L->topk + (L->shared ? 1 : 0)) * L->hidden * 4);
+}
+
+static size_t g53_slots_bytes(const G53hMoeLayer *L, int T)
+{
+    return align256((size_t)T * (L->topk + (L->shared ? 1 : 0)) * sizeof(G53hExpert));
 }
 
 static int g53_check_layer(const G53hMoeLayer *L, int T)
@@ -396,9 +327,12 @@ extern "C" int g53h_moe_routed_given(float *out, const float *x, int T, const G5
 {
     if (g53h_ready() || g53_check_layer(L, T)) return -1;
     if (T == 0) return 0;
-    char *ws = (char *)g53h_workspace(g53_contrib_bytes(L, T) + g53_layer_ws_bytes(L, T));
+    const size_t ssz = g53_slots_bytes(L, T), csz = g53_contrib_bytes(L, T);
+    char *ws = (char *)g53h_workspace(ssz + csz + g53_layer_ws_bytes(L, T));
     if (!ws) return -1;
-    return g53_layer_body(out, x, T, L, idx, wts, ws + g53_contrib_bytes(L, T), (float *)ws, 1);
+    G53hExpert *slots = (G53hExpert *)ws;
+    if (g53h_resolve_slots(slots, L->experts, idx, L->shared, T, L->topk)) return -1;
+    return g53_layer_body(out, x, T, L, idx, wts, ws + ssz + csz, (float *)(ws + ssz), 1, slots);
 }
 
 extern "C" int g53h_moe_partial(float *contrib, const float *x, int T, const G53hMoeLayer *L,
@@ -406,9 +340,12 @@ extern "C" int g53h_moe_partial(float *contrib, const float *x, int T, const G53
 {
     if (g53h_ready() || g53_check_layer(L, T)) return -1;
     if (T == 0) return 0;
-    char *ws = (char *)g53h_workspace(g53_layer_ws_bytes(L, T));
+    const size_t ssz = g53_slots_bytes(L, T);
+    char *ws = (char *)g53h_workspace(ssz + g53_layer_ws_bytes(L, T));
     if (!ws) return -1;
-    return g53_layer_body(nullptr, x, T, L, idx, nullptr, ws, contrib, 0);
+    G53hExpert *slots = (G53hExpert *)ws;
+    if (g53h_resolve_slots(slots, L->experts, idx, L->shared, T, L->topk)) return -1;
+    return g53_layer_body(nullptr, x, T, L, idx, nullptr, ws + ssz, contrib, 0, slots);
 }
 
 extern "C" int g53h_moe_combine(float *out, const float *contrib, const float *wts, int T,
@@ -425,17 +362,23 @@ extern "C" int g53h_moe(float *out, const float *x, int T, const G53hMoeLayer *L
     if (g53h_ready() || g53_check_layer(L, T)) return -1;
     if (T == 0) return 0;
     if (!L->router || !L->bias) return g53h_fail("g53h_moe: no router");
+    if (T == 1) {                                    /* single-token decode: one fused launch */
+        const int r = g53h_decode_fused(out, x, L, idx_out, w_out);
+        if (r <= 0) return r;
+    }
     const int K = L->topk, NE = L->n_experts;
     const size_t rsz = align256((size_t)2 * T * NE * 4), isz = align256((size_t)T * K * 4);
-    const size_t csz = g53_contrib_bytes(L, T);
-    char *ws = (char *)g53h_workspace(rsz + 2 * isz + csz + g53_layer_ws_bytes(L, T));
+    const size_t ssz = g53_slots_bytes(L, T), csz = g53_contrib_bytes(L, T);
+    char *ws = (char *)g53h_workspace(rsz + 2 * isz + ssz + csz + g53_layer_ws_bytes(L, T));
     if (!ws) return -1;
     int *idx = idx_out ? idx_out : (int *)(ws + rsz);
     float *w = w_out ? w_out : (float *)(ws + rsz + isz);
+    G53hExpert *slots = (G53hExpert *)(ws + rsz + 2 * isz);
     g53h_prof_mark(G53_PROF_START);
     if (g53h_router_into(idx, w, x, T, L->router, L->router_dt, L->bias, NE, L->hidden, K, L->norm_topk,
-                         L->routed_scale, nullptr, (float *)ws))
+                         L->routed_scale, nullptr, (float *)ws, L->experts, L->shared, slots))
         return -1;
     g53h_prof_mark(G53_PROF_ROUTER);
-    return g53_layer_body(out, x, T, L, idx, w, ws + rsz + 2 * isz + csz, (float *)(ws + rsz + 2 * isz), 1);
+    return g53_layer_body(out, x, T, L, idx, w, ws + rsz + 2 * isz + ssz + csz,
+                          (float *)(ws + rsz + 2 * isz + ssz), 1, slots);
 }

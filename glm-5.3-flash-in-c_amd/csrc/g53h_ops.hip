@@ -142,39 +142,17 @@ int g53h_swiglu_split(float *y, const float *g, const float *u, long m, float li
     return 0;
 }
 
-/* ----------------------------------------------------------------- router ---- */
-/* Dot products in double. Every product of two floats is exact in double, so the only
- * rounding is in the additions; the reference adds sequentially, this adds per lane and
- * then across the wave. The double sums agree whenever the additions are exact (always
- * for bf16-valued router and input rows of ordinary range) and otherwise differ in the last
- * double bits, which changes the float score only if it lies within that distance of a
- * float rounding boundary. */
-__device__ float g53_router_dot(const void *gate, int dt, int e, int E, const float *x, int lane)
-{
-    double acc = 0.0;
-    if (dt == 1) {
-        const uint16_t *row = (const uint16_t *)gate + (size_t)e * E;
-        for (int i = lane; i < E; i += 64)
-            acc += (double)g53_bitsf((uint32_t)row[i] << 16) * (double)x[i];
-    } else {
-        const float *row = (const float *)gate + (size_t)e * E;
-        for (int i = lane; i < E; i += 64) acc += (double)row[i] * (double)x[i];
-    }
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-    return (float)acc;
-}
+#include "g53h_gemv.h"
 
-/* scores[t][e] = sigmoid(dot); choice[t][e] = score + bias[e]. One wave per (token, expert). */
-__global__ void __launch_bounds__(256) k_router_scores(float *__restrict__ score,
-                                                       float *__restrict__ choice,
-                                                       const float *__restrict__ x, int T,
-                                                       const void *__restrict__ gate, int dt,
-                                                       const float *__restrict__ bias, int NE, int E)
+/* scores[t][e] = sigmoid(dot); choice[t][e] = score + bias[e]. One wave per (token, expert),
+ * one wave per workgroup so the experts spread over every CU. */
+__global__ void __launch_bounds__(64) k_router_scores(float *__restrict__ score, float *__restrict__ choice,
+                                                      const float *__restrict__ x, int T,
+                                                      const void *__restrict__ gate, int dt,
+                                                      const float *__restrict__ bias, int NE, int E)
 {
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int t = blockIdx.y;
-    if (e >= NE) return;
+    const int lane = threadIdx.x;
+    const int e = blockIdx.x, t = blockIdx.y;
     const float d = g53_router_dot(gate, dt, e, E, x + (size_t)t * E, lane);
     if (lane == 0) {
         const float s = g53_sigmoidf(d);
@@ -183,50 +161,40 @@ __global__ void __launch_bounds__(256) k_router_scores(float *__restrict__ score
     }
 }
 
-/* Lane-local and wave-wide argmax with the reference's rule: strictly greater wins, so the
- * lowest index among equal maxima; NaN never wins; -inf is never selected. */
-__device__ inline void g53_argmax_merge(float &bv, int &bi, float ov, int oi)
+/* Top-k by rank, equal to the reference's k rounds of "first strictly greater" argmax: an
+ * expert's rank is the number of experts with a larger choice, plus those with an equal choice
+ * and a lower index; rank j goes to slot j. NaN and -inf are never selected (the reference's
+ * scan starts from -inf and only moves on a strict >); a token with fewer than k selectable
+ * experts sets *nan_flag. Then the weights: the unbiased scores of the chosen experts,
+ * renormalised in double if norm_topk, times routed_scale. When experts != NULL the chosen
+ * experts' descriptors (and the shared expert's, if any) are copied to slots[t][*], so the
+ * expert kernels find their matrices with one load. One workgroup per token. */
+__global__ void __launch_bounds__(1024) k_router_select(int *__restrict__ idx, float *__restrict__ w,
+                                                        const float *__restrict__ score,
+                                                        const float *__restrict__ choice, int NE, int K,
+                                                        int norm_topk, float routed_scale,
+                                                        int *__restrict__ nan_flag,
+                                                        const G53hExpert *__restrict__ experts,
+                                                        const G53hExpert *__restrict__ shared,
+                                                        G53hExpert *__restrict__ slots)
 {
-    if (oi < 0) return;
-    if (bi < 0 || ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-}
-
-#define G53_SEL_PER_LANE 16   /* up to 1024 experts per wave */
-
-__global__ void __launch_bounds__(64) k_router_select(int *__restrict__ idx, float *__restrict__ w,
-                                                      const float *__restrict__ score,
-                                                      const float *__restrict__ choice, int NE, int K,
-                                                      int norm_topk, float routed_scale,
-                                                      int *__restrict__ nan_flag)
-{
-    const int t = blockIdx.x, lane = threadIdx.x;
-    float c[G53_SEL_PER_LANE];
-    for (int k = 0; k < G53_SEL_PER_LANE; k++) {
-        const int e = lane + 64 * k;
-        c[k] = e < NE ? choice[(size_t)t * NE + e] : -INFINITY;
-    }
+    __shared__ __attribute__((aligned(16))) float c[1024];
+    __shared__ int sel[GLM53F_MAX_TOPK_DEV];
     __shared__ float sw[GLM53F_MAX_TOPK_DEV];
-    __shared__ int si[GLM53F_MAX_TOPK_DEV];
-    for (int j = 0; j < K; j++) {
-        float bv = -INFINITY;
-        int bi = -1;
-        for (int k = 0; k < G53_SEL_PER_LANE; k++)          /* ascending expert index */
-            if (c[k] > bv) { bv = c[k]; bi = lane + 64 * k; }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            g53_argmax_merge(bv, bi, ov, oi);
-        }
-        for (int k = 0; k < G53_SEL_PER_LANE; k++)
-            if (lane + 64 * k == bi) c[k] = -INFINITY;
-        if (lane == 0) si[j] = bi;
-    }
+    __shared__ uint32_t kbuf[GLM53F_MAX_TOPK_DEV];
+    __shared__ int ebuf[GLM53F_MAX_TOPK_DEV];
+    const int t = blockIdx.x, i = threadIdx.x;
+    const int NE4 = (NE + 3) & ~3;
+    const float *ct = choice + (size_t)t * NE;
+    for (int e = i; e < NE4; e += blockDim.x) c[e] = e < NE ? ct[e] : -INFINITY;
     __syncthreads();
-    if (lane == 0) {
+    if (i < 64) g53_topk_wave(c, NE, K, sel, kbuf, ebuf);
+    __syncthreads();
+    if (i == 0) {
         int bad = 0;
         for (int j = 0; j < K; j++) {
-            if (si[j] < 0) { bad = 1; si[j] = 0; }
-            sw[j] = score[(size_t)t * NE + si[j]];
+            if (sel[j] < 0) { bad = 1; sel[j] = 0; }
+            sw[j] = score[(size_t)t * NE + sel[j]];
         }
         if (bad && nan_flag) atomicOr(nan_flag, 1);
         if (norm_topk) {
@@ -235,24 +203,61 @@ __global__ void __launch_bounds__(64) k_router_select(int *__restrict__ idx, flo
             for (int j = 0; j < K; j++) sw[j] = (float)((double)sw[j] / (s + 1e-20));
         }
         for (int j = 0; j < K; j++) {
-            idx[(size_t)t * K + j] = si[j];
+            idx[(size_t)t * K + j] = sel[j];
             w[(size_t)t * K + j] = sw[j] * routed_scale;
+        }
+    }
+    if (experts) {
+        __syncthreads();
+        const int nslots = K + (shared ? 1 : 0);
+        const int words = (int)(sizeof(G53hExpert) / 4);
+        for (int q = i; q < nslots * words; q += blockDim.x) {
+            const int j = q / words, k = q % words;
+            const G53hExpert *src = j < K ? &experts[sel[j]] : shared;
+            ((int *)&slots[(size_t)t * nslots + j])[k] = ((const int *)src)[k];
         }
     }
 }
 
+/* slots[t][j] = experts[idx[t][j]] (j < K), slots[t][K] = *shared: the descriptor table of
+ * the expert kernels, for callers that route elsewhere. */
+__global__ void k_resolve_slots(G53hExpert *__restrict__ slots, const G53hExpert *__restrict__ experts,
+                                const int *__restrict__ idx, const G53hExpert *__restrict__ shared, int T,
+                                int K, int nslots)
+{
+    const int words = (int)(sizeof(G53hExpert) / 4);
+    const long q = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (long)T * nslots * words) return;
+    const int k = (int)(q % words), j = (int)((q / words) % nslots), t = (int)(q / ((long)words * nslots));
+    const G53hExpert *src = j < K ? &experts[idx[(size_t)t * K + j]] : shared;
+    ((int *)&slots[(size_t)t * nslots + j])[k] = ((const int *)src)[k];
+}
+
+int g53h_resolve_slots(G53hExpert *slots, const G53hExpert *experts, const int *idx, const G53hExpert *shared,
+                       int T, int K)
+{
+    const int nslots = K + (shared ? 1 : 0);
+    const long n = (long)T * nslots * (long)(sizeof(G53hExpert) / 4);
+    hipLaunchKernelGGL(k_resolve_slots, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, g53h_stream(), slots,
+                       experts, idx, shared, T, K, nslots);
+    G53_LAUNCHED("k_resolve_slots");
+    return 0;
+}
+
 int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate, int gate_dt,
                      const float *bias, int NE, int E, int K, int norm_topk, float routed_scale,
-                     int *nan_flag, float *scratch)
+                     int *nan_flag, float *scratch, const G53hExpert *experts, const G53hExpert *shared,
+                     G53hExpert *slots)
 {
-    if (NE < 1 || NE > 64 * G53_SEL_PER_LANE) return g53h_fail("g53h_router: %d experts (max 1024)", NE);
+    if (NE < 1 || NE > 1024) return g53h_fail("g53h_router: %d experts (max 1024)", NE);
     if (K < 1 || K > NE || K > GLM53F_MAX_TOPK_DEV) return g53h_fail("g53h_router: topk %d", K);
     float *score = scratch, *choice = scratch + (size_t)T * NE;
-    hipLaunchKernelGGL(k_router_scores, dim3((NE + 3) / 4, T), dim3(256), 0, g53h_stream(), score,
-                       choice, x, T, gate, gate_dt, bias, NE, E);
+    hipLaunchKernelGGL(k_router_scores, dim3(NE, T), dim3(64), 0, g53h_stream(), score, choice, x, T, gate,
+                       gate_dt, bias, NE, E);
     G53_LAUNCHED("k_router_scores");
-    hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), 0, g53h_stream(), idx, w, score, choice,
-                       NE, K, norm_topk, routed_scale, nan_flag);
+    const int nthr = NE < 64 ? 64 : (NE > 1024 ? 1024 : (NE + 63) / 64 * 64);
+    hipLaunchKernelGGL(k_router_select, dim3(T), dim3(nthr), 0, g53h_stream(), idx, w, score, choice, NE, K,
+                       norm_topk, routed_scale, nan_flag, experts, shared, slots);
     G53_LAUNCHED("k_router_select");
     return 0;
 }
@@ -266,7 +271,17 @@ extern "C" int g53h_router(int *idx, float *w, const float *x, int T, const void
     float *ws = (float *)g53h_workspace((size_t)2 * T * (NE > 0 ? NE : 1) * sizeof(float));
     if (!ws) return -1;
     return g53h_router_into(idx, w, x, T, gate, gate_dt, bias, NE, E, K, norm_topk, routed_scale,
-                            nan_flag, ws);
+                            nan_flag, ws, nullptr, nullptr, nullptr);
+}
+
+#define G53_SEL_PER_LANE 16   /* up to 1024 experts per wave */
+
+/* Wave-wide argmax with the reference's rule: strictly greater wins, so the lowest index among
+ * equal maxima; an empty candidate (index < 0) never wins. */
+__device__ inline void g53_argmax_merge(float &bv, int &bi, float ov, int oi)
+{
+    if (oi < 0) return;
+    if (bi < 0 || ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
 }
 
 /* route_topn (src/core/glm53f_ops.c:1021-1042): the scan starts from expert 0, so a NaN at
@@ -313,8 +328,8 @@ extern "C" int g53h_route_topn(int *idx, int n, const float *x, const void *gate
     if (NE < 1 || NE > 64 * G53_SEL_PER_LANE) return g53h_fail("g53h_route_topn: %d experts", NE);
     float *ws = (float *)g53h_workspace((size_t)2 * NE * sizeof(float));
     if (!ws) return -1;
-    hipLaunchKernelGGL(k_router_scores, dim3((NE + 3) / 4, 1), dim3(256), 0, g53h_stream(), ws + NE,
-                       ws, x, 1, gate, gate_dt, bias, NE, E);
+    hipLaunchKernelGGL(k_router_scores, dim3(NE, 1), dim3(64), 0, g53h_stream(), ws + NE, ws, x, 1, gate,
+                       gate_dt, bias, NE, E);
     G53_LAUNCHED("k_router_scores");
     hipLaunchKernelGGL(k_route_topn, dim3(1), dim3(64), 0, g53h_stream(), idx, n, ws, NE);
     G53_LAUNCHED("k_route_topn");

@@ -33,7 +33,7 @@ int        *g53h_counters(void);
 /* Kernel timing marks (no-ops unless g53h_prof_enable(1)): tag 0 opens an interval, the
  * tags below close the interval since the previous mark. */
 enum { G53_PROF_START = 0, G53_PROF_ROUTER = 1, G53_PROF_GATEUP = 2, G53_PROF_DOWN = 3,
-       G53_PROF_GENERIC = 4, G53_PROF_GROUPED = 5, G53_PROF_NTAGS = 8 };
+       G53_PROF_GENERIC = 4, G53_PROF_GROUPED = 5, G53_PROF_COMBINE = 6, G53_PROF_FUSED = 7, G53_PROF_NTAGS = 8 };
 void        g53h_prof_mark(int tag);
 
 #endif /* G53H_RUNTIME_H */

@@ -132,6 +132,10 @@ _SIGS = {
                                    C.c_void_p]),
     "g53h_moe_combine": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                                    C.POINTER(G53hMoeLayer)]),
+    "g53h_set_fused_decode": (C.c_int, [C.c_int]),
+    "g53h_decode_errors": (C.c_int, []),
+    "g53h_decode_grid": (C.c_int, []),
+    "g53h_set_decode_trace": (C.c_int, [C.c_void_p]),
     "g53h_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_expf_range": (C.c_int, [C.c_void_p, C.c_uint32, C.c_size_t]),
     "g53h_expf_host": (None, [C.c_void_p, C.c_void_p, C.c_size_t]),

@@ -115,6 +115,19 @@ int g53h_moe_partial(float *contrib_d, const float *x_d, int T, const G53hMoeLay
 int g53h_moe_combine(float *out_d, const float *contrib_d, const float *w_d, int T,
                      const G53hMoeLayer *L);
 
+/* Single-token decode runs as one persistent launch when the layer has the released shapes
+ * (hidden 4096, inter 2048, 128x128 blocks, topk <= 16); g53h_set_fused_decode(0) selects the
+ * multi-kernel path instead (returns the previous setting). g53h_decode_errors waits for the
+ * stream and returns, then clears, the fused kernel's error flags (1: a grid wait timed out,
+ * 2: a token had fewer than topk selectable experts), 0 if none. g53h_decode_grid returns the
+ * fused kernel's workgroup count (0: unavailable, -1: not yet sized). */
+int g53h_set_fused_decode(int on);
+int g53h_decode_errors(void);
+int g53h_decode_grid(void);
+/* Diagnostics: with dev_buf != NULL (device, grid x 8 uint64), the fused kernel's workgroups
+ * record 100 MHz timestamps at their phase boundaries; NULL turns it off. */
+int g53h_set_decode_trace(void *dev_buf);
+
 /* -------------------------------------------------------- checks and inputs ---- */
 /* y[i] = expf(x[i]) by the device restatement of glibc's expf (for exhaustive checks). */
 int g53h_expf(float *y_d, const float *x_d, size_t n);

@@ -137,21 +137,40 @@ def test_layer_config1(L):
     assert same(out, GOLD["c1b_routed_out"])
 
 
-def test_layer_config2_decode(L, c2layer):
-    sp = c2layer.sp
-    x = S.x_host(sp, 64, batch=0)
-    say("config 2 decode token 0 vs golden")
-    out, idx, _ = run_layer(c2layer, x[:1], 1)
-    assert np.array_equal(idx[0], GOLD["c2r_idx"][0])
-    assert same(out[0], GOLD["c2_out"])
-    for t in (1, 2, 3):
-        say("config 2 decode token", t, "vs oracle")
-        out, idx, w = run_layer(c2layer, x[t:t + 1], 1)
-        mats = {int(e): c2layer.fetch_expert(int(e)) for e in idx[0]}
-        want, wi, ww = O.moe(O.oracle(), x[t:t + 1], sp, c2layer.router_f32, c2layer.bias_f32, mats,
-                             c2layer.fetch_expert("shared"))
-        assert np.array_equal(idx, wi) and same(w, ww)
-        assert same(out, want)
+@pytest.mark.parametrize("fused", [1, 0])
+def test_layer_config2_decode(L, c2layer, fused):
+    """Single-token decode at the released shapes, through the one-launch persistent kernel
+    (fused=1) and through the multi-kernel path (fused=0)."""
+    prev = L.g53h_set_fused_decode(fused)
+    try:
+        sp = c2layer.sp
+        x = S.x_host(sp, 64, batch=0)
+        say("config 2 decode token 0 vs golden, fused", fused)
+        out, idx, _ = run_layer(c2layer, x[:1], 1)
+        assert L.g53h_decode_errors() == 0
+        assert np.array_equal(idx[0], GOLD["c2r_idx"][0])
+        assert same(out[0], GOLD["c2_out"])
+        for t in (1, 2, 3):
+            say("config 2 decode token", t, "vs oracle, fused", fused, "grid", L.g53h_decode_grid())
+            out, idx, w = run_layer(c2layer, x[t:t + 1], 1)
+            assert L.g53h_decode_errors() == 0
+            mats = {int(e): c2layer.fetch_expert(int(e)) for e in idx[0]}
+            want, wi, ww = O.moe(O.oracle(), x[t:t + 1], sp, c2layer.router_f32, c2layer.bias_f32, mats,
+                                 c2layer.fetch_expert("shared"))
+            assert np.array_equal(idx, wi) and same(w, ww)
+            assert same(out, want)
+        say("config 2: 64 decode tokens back to back, routing vs golden")
+        xd = DevBuf.from_array(x)
+        outs = DevBuf(64 * sp.E * 4)
+        idxs = DevBuf(64 * sp.K * 4)
+        for t in range(64):
+            check(L.g53h_moe(outs.ptr + t * sp.E * 4, xd.ptr + t * sp.E * 4, 1, C.byref(c2layer.layer),
+                             idxs.ptr + t * sp.K * 4, None), "g53h_moe")
+        glm53h.sync()
+        assert L.g53h_decode_errors() == 0
+        assert np.array_equal(idxs.download(np.int32).reshape(64, sp.K), GOLD["c2r_idx"])
+    finally:
+        L.g53h_set_fused_decode(prev)
 
 
 def test_layer_config2_small_batch(L, c2layer):
