@@ -58,13 +58,10 @@ __constant__ static const uint64_t g53_exp2_tab_dev[32] = G53_EXP2_TAB;
 #endif
 static const uint64_t g53_exp2_tab_host[32] = G53_EXP2_TAB;
 
-G53_HD float g53_expf(float x)
+/* The exponential with the table passed in (kernels keep a copy of it in LDS, so that the
+ * per-lane lookup is an LDS read rather than a global load). */
+G53_HD float g53_expf_tab(float x, const uint64_t *tab)
 {
-#if defined(__HIP_DEVICE_COMPILE__)
-    const uint64_t *tab = g53_exp2_tab_dev;
-#else
-    const uint64_t *tab = g53_exp2_tab_host;
-#endif
     const uint32_t ix = g53_fbits(x);
     const uint32_t abstop = (ix >> 20) & 0x7ff;
     if (abstop >= 0x42b) {                       /* |x| >= 88, inf or nan */
@@ -95,23 +92,40 @@ G53_HD float g53_expf(float x)
     return (float)y;
 }
 
-/* 1 / (1 + e^-x) in float, operation for operation as the reference's sigmoidf_. */
-G53_HD float g53_sigmoidf(float x)
+G53_HD float g53_expf(float x)
 {
-    const float e = g53_expf(-x);
+#if defined(__HIP_DEVICE_COMPILE__)
+    return g53_expf_tab(x, g53_exp2_tab_dev);
+#else
+    return g53_expf_tab(x, g53_exp2_tab_host);
+#endif
+}
+
+/* 1 / (1 + e^-x) in float, operation for operation as the reference's sigmoidf_. */
+G53_HD float g53_sigmoidf_tab(float x, const uint64_t *tab)
+{
+    const float e = g53_expf_tab(-x, tab);
     const float d = 1.0f + e;
     return 1.0f / d;
 }
 
 /* SwiGLU with the clamp: the gate only from above, the up projection both ways
  * (reference src/core/glm53f_ops.c:486-494). */
-G53_HD float g53_swiglu1(float g, float u, float limit)
+G53_HD float g53_swiglu1_tab(float g, float u, float limit, const uint64_t *tab)
 {
     const float gi = g > limit ? limit : g;
     const float ui = u > limit ? limit : (u < -limit ? -limit : u);
-    const float sg = gi * g53_sigmoidf(gi);
+    const float sg = gi * g53_sigmoidf_tab(gi, tab);
     return sg * ui;
 }
+
+#if defined(__HIP_DEVICE_COMPILE__)
+#define G53_EXP_TAB g53_exp2_tab_dev
+#else
+#define G53_EXP_TAB g53_exp2_tab_host
+#endif
+G53_HD float g53_sigmoidf(float x) { return g53_sigmoidf_tab(x, G53_EXP_TAB); }
+G53_HD float g53_swiglu1(float g, float u, float limit) { return g53_swiglu1_tab(g, u, limit, G53_EXP_TAB); }
 
 /* E4M3FN: sign, 4-bit exponent (bias 7), 3-bit mantissa, no infinities, 0x7f/0xff NaN. */
 G53_HD float g53_e4m3_to_f32(uint8_t b)

@@ -59,6 +59,50 @@ __device__ __forceinline__ double g53_blk_lds(const uint4 (&c)[8], const float *
          + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
 }
 
+/* Padded block layout: 128-column block b of a vector starts at float b * G53_PADB, so that
+ * the 8 lanes of one ds_read_b128 phase, each reading chunk q of a different block, hit
+ * different LDS banks, and a lane's 32 chunk reads are one base address plus immediate
+ * offsets. */
+#define G53_PADB 132
+
+__device__ __forceinline__ double g53_blk_pad(const uint4 (&c)[8], const float *xb)
+{
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t d[4] = {c[k].x, c[k].y, c[k].z, c[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = 4 * k + i, e = 4 * q, l = e & 7;
+            const float4 xq = *(const float4 *)(xb + 4 * q);
+            const g53_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[i], false);
+            const g53_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[i], true);
+            a[l + 0] = __builtin_fmaf(lo[0], xq.x, a[l + 0]);
+            a[l + 1] = __builtin_fmaf(lo[1], xq.y, a[l + 1]);
+            a[l + 2] = __builtin_fmaf(hi[0], xq.z, a[l + 2]);
+            a[l + 3] = __builtin_fmaf(hi[1], xq.w, a[l + 3]);
+        }
+    }
+    return (((double)a[0] + a[4]) + ((double)a[2] + a[6]))
+         + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
+}
+
+/* Copy a vector of N floats (N a multiple of 4 * NTHR) into LDS in the padded block layout,
+ * every load issued before the first store. */
+template <int N, int NTHR>
+__device__ __forceinline__ void g53_vec_to_lds_pad(float *dst, const float *src, int tid)
+{
+    constexpr int PER = N / 4 / NTHR;
+    float4 v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) v[k] = *(const float4 *)(src + 4 * (tid + k * NTHR));
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int e = 4 * (tid + k * NTHR);
+        *(float4 *)(dst + (e / 128) * G53_PADB + (e % 128)) = v[k];
+    }
+}
+
 /* Copy a vector of n floats (n a multiple of 128) into LDS with the block swizzle. */
 __device__ __forceinline__ void g53_vec_to_lds(float *dst, const float *src, int n, int tid, int nthr)
 {

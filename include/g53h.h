@@ -124,7 +124,7 @@ int g53h_moe_combine(float *out_d, const float *contrib_d, const float *w_d, int
 int g53h_set_fused_decode(int on);
 int g53h_decode_errors(void);
 int g53h_decode_grid(void);
-/* Diagnostics: with dev_buf != NULL (device, grid x 8 uint64), the fused kernel's workgroups
+/* Diagnostics: with dev_buf != NULL (device, grid x 32 uint64), the fused kernel's workgroups
  * record 100 MHz timestamps at their phase boundaries; NULL turns it off. */
 int g53h_set_decode_trace(void *dev_buf);
 
