@@ -146,27 +146,36 @@ __device__ __forceinline__ double g53_router_row(const uint4 (&c)[8], const floa
     return acc;
 }
 
-/* The sum, in lane order, of the doubles held by lanes base .. base+n-1 (base = lane rounded
- * down to a multiple of n), valid in lane base: the reference's sequential sum over a row's
- * blocks. The terms travel by lane shuffles, so no LDS is needed. */
+/* The sum, in lane order, of the doubles held by lanes base .. base+N-1 (base = lane rounded
+ * down to a multiple of N), valid in lane base: the reference's sequential sum over a row's
+ * blocks. The terms pass through pt, 64 doubles of LDS private to the wave. */
 template <int N>
-__device__ __forceinline__ double g53_row_sum(double t, int lane)
+__device__ __forceinline__ double g53_row_sum(double t, double *pt, int lane)
 {
-    const int base = lane & ~(N - 1);
+    pt[lane] = t;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
     double s = 0.0;
+    if ((lane & (N - 1)) == 0) {
 #pragma unroll
-    for (int k = 0; k < N; k++) s = s + __shfl(t, base + k);
+        for (int k = 0; k < N; k += 2) {
+            const double2 q = *(const double2 *)(pt + lane + k);
+            s = s + q.x;
+            s = s + q.y;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
     return s;
 }
 
 /* One gate/up row pair (lanes 0-31 gate blocks, 32-63 up blocks) with x in LDS: the two row
  * sums in block order and the SwiGLU, valid in lane 0. */
-__device__ __forceinline__ float g53_gateup_pair(const uint4 (&c)[8], float sc, const float *xs,
+__device__ __forceinline__ float g53_gateup_pair(const uint4 (&c)[8], float sc, const float *xs, double *pt,
                                                  float limit, const uint64_t *etab, int lane)
 {
     const int bb = lane & 31;
     const double t = g53_blk_pad(c, xs + bb * G53_PADB) * (double)sc;
-    const float v = (float)g53_row_sum<32>(t, lane);
+    const float v = (float)g53_row_sum<32>(t, pt, lane);
     const float u = __shfl(v, 32);
     return g53_swiglu1_tab(v, u, limit, etab);
 }
@@ -379,6 +388,7 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
 {
     __shared__ __attribute__((aligned(16))) float xs[G53_DEC_NBE * G53_PADB];        /* padded x   */
     __shared__ __attribute__((aligned(16))) float actl[G53_DEC_NENT][G53_DEC_NBI * G53_PADB];
+    __shared__ __attribute__((aligned(16))) double pw[4][64];                         /* row terms  */
     __shared__ G53hExpert st[G53_DEC_MAXK + 1];
     __shared__ float sw[16];
     __shared__ int sidx[16];
@@ -452,7 +462,7 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
         G53_TRACE(14);
     }
 
-    g53_u64 tw_act = 0, tw_comp = 0, n_items = 0, n_stale = 0;
+    g53_u64 tw_act = 0, tw_comp = 0, n_items = 0, n_stale = 0, n_stale2 = 0;
     auto claim = [&]() -> int {
         int i = 0;
         if (lane == 0) i = g53_lds_add(&qctr, 1);
@@ -463,7 +473,7 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
     auto compute = [&](const G53Item &it, const uint4 (&c)[8], float sc, bool loaded) {
         if (it.kind == G53_IT_G) {
             if (!loaded) return;                             /* expert not there */
-            const float v = g53_gateup_pair(c, sc, xs, a.limit, etab, lane);
+            const float v = g53_gateup_pair(c, sc, xs, pw[w], a.limit, etab, lane);
             if (lane == 0) g53_st_tag(a.act + (size_t)it.s * G53_DEC_I + it.r, g53_tag(a.epoch, v));
             return;
         }
@@ -477,19 +487,28 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
                 if (lane == 0) g53_lds_add(&ent_ver[e], 1);
                 return;
             }
-            g53_u64 v[8][2];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                v[k][0] = ((g53_u64)c[k].y << 32) | c[k].x;
-                v[k][1] = ((g53_u64)c[k].w << 32) | c[k].z;
-            }
+            /* value 2k of this lane: c[k].x (value) / c[k].y (epoch); value 2k+1: c[k].z / c[k].w */
             uint32_t pending = 0;
 #pragma unroll
-            for (int k = 0; k < 16; k++)
-                if ((unsigned)(v[k >> 1][k & 1] >> 32) != a.epoch) pending |= 1u << k;
+            for (int k = 0; k < 8; k++) {
+                if (c[k].y != a.epoch) pending |= 1u << (2 * k);
+                if (c[k].w != a.epoch) pending |= 1u << (2 * k + 1);
+            }
+            if (use > 0 && !g53_wait_lds(&ent_used[e], use * l.n_rg) && lane == 0) g53_flag_err(a.err, 1);
+            const int i0 = it.r * 1024 + lane * 16;          /* 16 values within one block */
+            float *dst = actl[e] + (i0 >> 7) * G53_PADB + (i0 & 127);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                *(float4 *)(dst + 4 * k) = make_float4(__uint_as_float(c[2 * k].x), __uint_as_float(c[2 * k].z),
+                                                       __uint_as_float(c[2 * k + 1].x), __uint_as_float(c[2 * k + 1].z));
             if (__ballot(pending != 0)) {
+                /* stale values (read from a line this XCD's L2 took before they were written):
+                 * re-read them coherently until their epochs are current, and store each back
+                 * with a plain store, which refreshes the stale line for the workgroups of this
+                 * XCD that read it later (the value stored is the one already in memory) */
                 const g53_u64 t0 = __builtin_amdgcn_s_memrealtime();
                 n_stale += __popc(pending);
+                g53_u64 *src = a.act + (size_t)it.s * G53_DEC_I + it.r * 1024 + lane * 16;
                 const __amdgpu_buffer_rsrc_t rsrc = g53_rsrc(a.act + (size_t)it.s * G53_DEC_I + it.r * 1024);
                 int spins = 0;
                 while (__ballot(pending != 0)) {
@@ -503,21 +522,16 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
 #pragma unroll
                         for (int k = 0; k < 4; k++)
                             if ((pending & (1u << (h + k))) && (unsigned)(t[k] >> 32) == a.epoch) {
-                                v[(h + k) >> 1][(h + k) & 1] = t[k];
+                                dst[h + k] = __uint_as_float((uint32_t)t[k]);
+                                src[h + k] = t[k];
                                 pending &= ~(1u << (h + k));
                             }
                     }
+                    if (spins == 1) n_stale2 += __popc(pending);
                     if (__ballot(pending != 0)) g53_backoff();
                 }
                 tw_act += __builtin_amdgcn_s_memrealtime() - t0;
             }
-            if (use > 0 && !g53_wait_lds(&ent_used[e], use * l.n_rg) && lane == 0) g53_flag_err(a.err, 1);
-            const int i0 = it.r * 1024 + lane * 16;          /* 16 values within one block */
-            float *dst = actl[e] + (i0 >> 7) * G53_PADB + (i0 & 127);
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                *(float4 *)(dst + 4 * k) = make_float4(__uint_as_float((uint32_t)v[2 * k][0]), __uint_as_float((uint32_t)v[2 * k][1]),
-                                                       __uint_as_float((uint32_t)v[2 * k + 1][0]), __uint_as_float((uint32_t)v[2 * k + 1][1]));
             __builtin_amdgcn_s_waitcnt(0xc07f);
             __builtin_amdgcn_wave_barrier();
             G53_CBAR();
@@ -534,7 +548,7 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
                 tw_act += __builtin_amdgcn_s_memrealtime() - t0;
             }
             const int bb = lane & 15;
-            v = (float)g53_row_sum<16>(g53_blk_pad(c, actl[e] + bb * G53_PADB) * (double)sc, lane);
+            v = (float)g53_row_sum<16>(g53_blk_pad(c, actl[e] + bb * G53_PADB) * (double)sc, pw[w], lane);
         }
         if ((lane & 15) == 0) cvals[it.r - l.rg_lo][lane >> 4][it.s] = v;
         __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -606,7 +620,7 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
     G53_TRACE(2 + w);
     if (a.trace && lane == 0) {
         g53_u64 *tr = a.trace + (size_t)blockIdx.x * 32;
-        tr[16 + w] = n_stale; tr[20 + w] = tw_act; tr[24 + w] = tw_comp; tr[28 + w] = n_items;
+        tr[16 + w] = n_stale; tr[20 + w] = tw_act; tr[6] = n_stale2; tr[24 + w] = tw_comp; tr[28 + w] = n_items;
     }
 }
 
