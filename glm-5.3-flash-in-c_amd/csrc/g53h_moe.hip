@@ -366,6 +366,7 @@ extern "C" int g53h_moe(float *out, const float *x, int T, const G53hMoeLayer *L
         const int r = g53h_decode_fused(out, x, L, idx_out, w_out);
         if (r <= 0) return r;
     }
+    if (g53h_grouped_use(L, T)) return g53h_moe_grouped(out, x, T, L, idx_out, w_out);
     const int K = L->topk, NE = L->n_experts;
     const size_t rsz = align256((size_t)2 * T * NE * 4), isz = align256((size_t)T * K * 4);
     const size_t ssz = g53_slots_bytes(L, T), csz = g53_contrib_bytes(L, T);

@@ -161,6 +161,66 @@ __global__ void __launch_bounds__(64) k_router_scores(float *__restrict__ score,
     }
 }
 
+/* The same scores for many tokens on the FP64 matrix cores (v_mfma_f64_16x16x4f64). Every
+ * product (double)bf16 * (double)x is exact in double, as in k_router_scores; the instruction
+ * adds them with double FMAs. Wave w of a workgroup computes the 16 x 16 tile of experts
+ * e0 = 64 * blockIdx.x + 16 * w .. +15 and tokens t0 = 16 * blockIdx.y .. +15. Operands: lane l
+ * gives A[l % 16][l / 16] (an expert's weight) and B[l / 16][l % 16] (a token's x); step s of
+ * a 256-column chunk uses column 64 * (l / 16) + s, so each lane reads 128 consecutive router
+ * bytes per chunk. Result: lane l, register r holds C[4 * r + l / 16][l % 16]. x chunks are
+ * staged in LDS. bf16 router rows, E a multiple of 256. */
+typedef double g53_v4d __attribute__((ext_vector_type(4)));
+#define G53_RM_XST 260                                  /* LDS floats per token row       */
+__global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, float *__restrict__ choice,
+                                                     const float *__restrict__ x, int T,
+                                                     const uint16_t *__restrict__ gate,
+                                                     const float *__restrict__ bias, int NE, int E)
+{
+    __shared__ __attribute__((aligned(16))) float xs[16 * G53_RM_XST];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 64 + w * 16;
+    const int i = lane & 15, g = lane >> 4;
+    const int er = e0 + i < NE ? e0 + i : NE - 1;          /* rows past NE: discarded       */
+    const uint16_t *wrow = gate + (size_t)er * E + g * 64;
+    const float *xl = xs + i * G53_RM_XST + g * 64;
+    g53_v4d acc = {0.0, 0.0, 0.0, 0.0};
+    for (int k0 = 0; k0 < E; k0 += 256) {
+        uint4 wv[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) wv[q] = *(const uint4 *)(wrow + k0 + q * 8);
+        __syncthreads();
+        for (int q = threadIdx.x; q < 16 * 64; q += 256) {
+            const int tk = q >> 6, c = (q & 63) * 4;
+            const int tt = t0 + tk < T ? t0 + tk : T - 1;
+            *(float4 *)(xs + tk * G53_RM_XST + c) = *(const float4 *)(x + (size_t)tt * E + k0 + c);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const uint32_t d[4] = {wv[q].x, wv[q].y, wv[q].z, wv[q].w};
+            const float4 xa = *(const float4 *)(xl + q * 8), xb = *(const float4 *)(xl + q * 8 + 4);
+            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)g53_bitsf(d[k] << 16), (double)xv[2 * k], acc,
+                                                           0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)g53_bitsf(d[k] & 0xffff0000u),
+                                                           (double)xv[2 * k + 1], acc, 0, 0, 0);
+            }
+        }
+    }
+    const int t = t0 + i;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int e = e0 + 4 * r + g;
+        if (t < T && e < NE) {
+            const float s = g53_sigmoidf((float)acc[r]);
+            score[(size_t)t * NE + e] = s;
+            if (choice) choice[(size_t)t * NE + e] = s + bias[e];
+        }
+    }
+}
+
 /* Top-k by rank, equal to the reference's k rounds of "first strictly greater" argmax: an
  * expert's rank is the number of experts with a larger choice, plus those with an equal choice
  * and a lower index; rank j goes to slot j. NaN and -inf are never selected (the reference's
@@ -252,9 +312,15 @@ int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate
     if (NE < 1 || NE > 1024) return g53h_fail("g53h_router: %d experts (max 1024)", NE);
     if (K < 1 || K > NE || K > GLM53F_MAX_TOPK_DEV) return g53h_fail("g53h_router: topk %d", K);
     float *score = scratch, *choice = scratch + (size_t)T * NE;
-    hipLaunchKernelGGL(k_router_scores, dim3(NE, T), dim3(64), 0, g53h_stream(), score, choice, x, T, gate,
-                       gate_dt, bias, NE, E);
-    G53_LAUNCHED("k_router_scores");
+    if (T >= 2 && gate_dt == 1 && E % 256 == 0) {           /* batches: the matrix-core form */
+        hipLaunchKernelGGL(k_router_mfma, dim3((NE + 63) / 64, (T + 15) / 16), dim3(256), 0, g53h_stream(), score,
+                           choice, x, T, (const uint16_t *)gate, bias, NE, E);
+        G53_LAUNCHED("k_router_mfma");
+    } else {
+        hipLaunchKernelGGL(k_router_scores, dim3(NE, T), dim3(64), 0, g53h_stream(), score, choice, x, T, gate,
+                           gate_dt, bias, NE, E);
+        G53_LAUNCHED("k_router_scores");
+    }
     const int nthr = NE < 64 ? 64 : (NE > 1024 ? 1024 : (NE + 63) / 64 * 64);
     hipLaunchKernelGGL(k_router_select, dim3(T), dim3(nthr), 0, g53h_stream(), idx, w, score, choice, NE, K,
                        norm_topk, routed_scale, nan_flag, experts, shared, slots);

@@ -132,6 +132,12 @@ _SIGS = {
                                    C.c_void_p]),
     "g53h_moe_combine": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                                    C.POINTER(G53hMoeLayer)]),
+    "g53h_moe_grouped": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.POINTER(G53hMoeLayer), C.c_void_p,
+                                   C.c_void_p]),
+    "g53h_set_grouped": (C.c_int, [C.c_int]),
+    "g53h_grouped_ok": (C.c_int, [C.POINTER(G53hMoeLayer)]),
+    "g53h_grouped_errors": (C.c_int, []),
+    "g53h_set_grouped_trace": (C.c_int, [C.c_void_p]),
     "g53h_set_fused_decode": (C.c_int, [C.c_int]),
     "g53h_decode_errors": (C.c_int, []),
     "g53h_decode_grid": (C.c_int, []),

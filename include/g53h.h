@@ -115,6 +115,27 @@ int g53h_moe_partial(float *contrib_d, const float *x_d, int T, const G53hMoeLay
 int g53h_moe_combine(float *out_d, const float *contrib_d, const float *w_d, int T,
                      const G53hMoeLayer *L);
 
+/* Batched decode and prefill (T >= 2) as token-sorted grouped GEMMs on the FP8 matrix cores
+ * (replaces src/core/glm53f_ops.c:1144-1342 moe_chunk with :376-444 matmul_f8_batch for a chunk
+ * of tokens): every expert's weights are read once per call of up to 2048 tokens. Routing is the
+ * exact router's (top-k indices and weights bit-exact); the expert products run on
+ * v_mfma_scale_f32_32x32x64_f8f6f4 with the activations split into E4M3 planes, so outputs
+ * match the reference within 2e-3 relative + 1e-2 absolute rather than bit for bit. Layers need
+ * 128x128 blocks, hidden and inter multiples of 512 with power-of-two block counts up to 32,
+ * topk <= 16, at most 1024 experts and a finite positive SwiGLU limit (g53h_grouped_ok).
+ * g53h_moe takes this path for T >= 2 when g53h_set_grouped is on (the default; it returns the
+ * previous setting) and the layer qualifies; otherwise the exact per-token kernels.
+ * g53h_grouped_errors waits for the stream and returns, then clears, the grouped kernels' flags
+ * (1: a routed index out of range, 8: an expert descriptor without the 128x128 layout). */
+int g53h_moe_grouped(float *out_d, const float *x_d, int T, const G53hMoeLayer *L, int *idx_d,
+                     float *w_d);
+int g53h_set_grouped(int on);
+int g53h_grouped_ok(const G53hMoeLayer *L);
+int g53h_grouped_errors(void);
+/* Diagnostics: with dev_buf != NULL (device, at least gate/up grid x 8 uint64), the grouped
+ * gate/up kernel's workgroups record 100 MHz timestamps of their phases; NULL turns it off. */
+int g53h_set_grouped_trace(void *dev_buf);
+
 /* Single-token decode runs as one persistent launch when the layer has the released shapes
  * (hidden 4096, inter 2048, 128x128 blocks, topk <= 16); g53h_set_fused_decode(0) selects the
  * multi-kernel path instead (returns the previous setting). g53h_decode_errors waits for the

@@ -174,11 +174,16 @@ def test_layer_config2_decode(L, c2layer, fused):
 
 
 def test_layer_config2_small_batch(L, c2layer):
-    """Four tokens in one call: each token's output equals its decode output, bit for bit."""
+    """Four tokens in one call on the exact per-token kernels (grouped path off): each token's
+    output equals its decode output, bit for bit."""
     sp = c2layer.sp
     x = S.x_host(sp, 4, batch=9)
     say("config 2, T=4")
-    out4, _, _ = run_layer(c2layer, x, 4)
+    prev = L.g53h_set_grouped(0)
+    try:
+        out4, _, _ = run_layer(c2layer, x, 4)
+    finally:
+        L.g53h_set_grouped(prev)
     for t in range(4):
         out1, _, _ = run_layer(c2layer, x[t:t + 1], 1)
         assert same(out4[t], out1[0])
