@@ -1,0 +1,522 @@
+/* g53h_cache.hip - the routed-expert cache in HBM (include/glm53f_cache.h).
+ *
+ * Policy: g53h_lru.c, the reference's (src/cache/glm53f_cache.c). Data movement, MI355X style:
+ *   - a slot is one expert's FP8 codes and fp32 block scales in one HBM arena;
+ *   - a read is six hipMemcpyAsync from the store's host memory into the slot, on the demand
+ *     copy stream (get/getmany) or the prefetch copy stream (hint), followed by the slot's
+ *     `landed` event. The bookkeeping publishes the slot when the copies are issued: get()
+ *     makes the library's compute stream wait for `landed`, so no host thread blocks on a
+ *     read (the reference waits on a condition variable instead);
+ *   - release() records the slot's `used` event on the compute stream; a later read into
+ *     the slot first waits for `used` (and for the slot's previous `landed`, which may be on
+ *     the other copy stream), so a slot is never overwritten while a kernel still reads it;
+ *   - prefetch keeps at most n_io expert reads in flight on the prefetch stream; the queue
+ *     (ordered by layer, stale entries cancelled by later hints) feeds it whenever the cache is
+ *     called and earlier reads have landed.
+ * Every entry point takes one mutex, as the reference's. */
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+#include <vector>
+
+#include "g53h.h"
+#include "g53h_runtime.h"
+#include "glm53f.h"
+#include "glm53f_cache.h"
+extern "C" {
+#include "../host/g53h_lru.h"
+}
+
+namespace {
+
+struct Geom {                       /* slot layout, from the probe expert */
+    size_t off[6], bytes[6];        /* gate/up/down codes, then gate/up/down scales */
+    int rows[3], cols[3], br[3], bc[3], scols[3];
+};
+
+struct Copy {
+    hipEvent_t ev;
+    int layer, expert, background;
+};
+
+struct Impl {
+    G53hLru lru;
+    uint8_t *arena = nullptr;
+    Geom geo;
+    std::vector<hipEvent_t> landed, used;
+    std::vector<unsigned char> landed_ok, used_ok;
+    hipStream_t demand = nullptr, prefetch = nullptr;
+    std::vector<Copy> inflight;     /* copies not yet seen complete                         */
+    std::vector<hipEvent_t> pool;   /* spare events                                         */
+    std::mutex mu;
+};
+
+double now_s()
+{
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return t.tv_sec + t.tv_nsec * 1e-9;
+}
+
+size_t al(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+size_t scale_bytes(const Glm53fMat &m) { return (size_t)((m.rows + m.br - 1) / m.br) * m.scols * sizeof(float); }
+
+Impl *impl_of(const Glm53fCache *c) { return (Impl *)c->impl; }
+
+void sync_stats(Glm53fCache *c, const Impl *m)
+{
+    c->hits = m->lru.hits;
+    c->misses = m->lru.misses;
+    c->evictions = m->lru.evictions;
+    c->prefetch_reads = m->lru.prefetch_reads;
+    c->bg_reads = m->lru.bg_reads;
+    c->bg_used = m->lru.bg_used;
+}
+
+/* Copies seen complete hand their host bytes back to the store. */
+void poll(Glm53fCache *c, Impl *m)
+{
+    size_t k = 0;
+    for (size_t i = 0; i < m->inflight.size(); i++) {
+        Copy &cp = m->inflight[i];
+        if (hipEventQuery(cp.ev) == hipSuccess) {
+            if (c->st->done) c->st->done(c->st, cp.layer, cp.expert);
+            m->pool.push_back(cp.ev);
+        } else {
+            m->inflight[k++] = cp;
+        }
+    }
+    m->inflight.resize(k);
+}
+
+bool same_mat(const Glm53fMat &h, const Geom &g, int i)
+{
+    return h.dt == GLM53F_WF8 && h.w && h.s && h.rows == g.rows[i] && h.cols == g.cols[i] && h.br == g.br[i] &&
+           h.bc == g.bc[i] && h.scols == g.scols[i];
+}
+
+/* Read expert (layer, expert) into slot on stream s. Returns 1 on success. */
+int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t s, int background, int64_t *nread)
+{
+    *nread = 0;
+    Glm53fExpertQ h;
+    memset(&h, 0, sizeof h);
+    if (c->st->view(c->st, layer, expert, &h) != 0) return 0;
+    const Glm53fMat *mats[3] = {&h.gate, &h.up, &h.down};
+    for (int i = 0; i < 3; i++)
+        if (!same_mat(*mats[i], m->geo, i)) {
+            fprintf(stderr, "glm53f_cache: L%d expert %d does not have the slot's shape\n", layer, expert);
+            if (c->st->done) c->st->done(c->st, layer, expert);
+            return 0;
+        }
+    uint8_t *base = m->arena + (size_t)slot * (size_t)c->slot_bytes;
+    if (m->used_ok[slot] && hipStreamWaitEvent(s, m->used[slot], 0) != hipSuccess) return 0;
+    if (m->landed_ok[slot] && hipStreamWaitEvent(s, m->landed[slot], 0) != hipSuccess) return 0;
+    for (int i = 0; i < 3; i++) {
+        if (hipMemcpyAsync(base + m->geo.off[i], mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(base + m->geo.off[3 + i], mats[i]->s, m->geo.bytes[3 + i], hipMemcpyHostToDevice, s) !=
+                hipSuccess)
+            return 0;
+        *nread += (int64_t)(m->geo.bytes[i] + m->geo.bytes[3 + i]);
+    }
+    if (hipEventRecord(m->landed[slot], s) != hipSuccess) return 0;
+    m->landed_ok[slot] = 1;
+    hipEvent_t ev;
+    if (!m->pool.empty()) { ev = m->pool.back(); m->pool.pop_back(); }
+    else if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return 0;
+    if (hipEventRecord(ev, s) != hipSuccess) return 0;
+    m->inflight.push_back(Copy{ev, layer, expert, background});
+    return 1;
+}
+
+/* Start queued prefetch reads while fewer than n_io are in flight. */
+void pump(Glm53fCache *c, Impl *m)
+{
+    int busy = 0;
+    for (const Copy &cp : m->inflight) busy += cp.background;
+    while (busy < c->n_io) {
+        const int32_t key = g53_lru_pop(&m->lru);
+        if (key < 0) break;
+        const int slot = g53_lru_reserve(&m->lru, key);
+        if (slot < 0) continue;                       /* cache saturated: skip this hint */
+        int64_t nread = 0;
+        const int ok = issue(c, m, slot, key / c->n_experts, key % c->n_experts, m->prefetch, 1, &nread);
+        g53_lru_land(&m->lru, key, slot, ok, 1);
+        if (ok) { m->lru.bg_reads++; c->bg_bytes += (uint64_t)nread; busy++; }
+    }
+}
+
+void view_of(const Glm53fCache *c, const Impl *m, int slot, Glm53fExpertQ *q)
+{
+    uint8_t *base = m->arena + (size_t)slot * (size_t)c->slot_bytes;
+    Glm53fMat *mats[3] = {&q->gate, &q->up, &q->down};
+    for (int i = 0; i < 3; i++) {
+        Glm53fMat &v = *mats[i];
+        v.w = base + m->geo.off[i];
+        v.s = (const float *)(base + m->geo.off[3 + i]);
+        v.dt = GLM53F_WF8;
+        v.rows = m->geo.rows[i]; v.cols = m->geo.cols[i];
+        v.br = m->geo.br[i]; v.bc = m->geo.bc[i]; v.scols = m->geo.scols[i];
+    }
+}
+
+int cache_get(Glm53fExpertSrc *self, int layer, int expert, Glm53fExpertQ *out)
+{
+    Glm53fCache *c = (Glm53fCache *)self;
+    Impl *m = impl_of(c);
+    if (layer < 0 || layer >= c->n_layers || expert < 0 || expert >= c->n_experts) {
+        fprintf(stderr, "glm53f_cache: out of range L%d expert %d\n", layer, expert);
+        return -1;
+    }
+    const int32_t key = layer * c->n_experts + expert;
+    const double t0 = now_s();
+    std::lock_guard<std::mutex> g(m->mu);
+    poll(c, m);
+    int slot = g53_lru_hit(&m->lru, key);
+    if (slot < 0) {
+        m->lru.misses++;
+        const int s = g53_lru_reserve(&m->lru, key);
+        if (s < 0) {          /* every slot pinned: the caller holds more than the cache can */
+            fprintf(stderr, "glm53f_cache: all %d slots are pinned; cannot read L%d expert %d\n", c->nslot, layer,
+                    expert);
+            m->lru.misses--;
+            c->load_seconds += now_s() - t0;
+            return -1;
+        }
+        int64_t nread = 0;
+        const int ok = issue(c, m, s, layer, expert, m->demand, 0, &nread);
+        g53_lru_land(&m->lru, key, s, ok, 0);
+        if (!ok) {
+            fprintf(stderr, "glm53f_cache: short load of L%d expert %d\n", layer, expert);
+            sync_stats(c, m);
+            c->load_seconds += now_s() - t0;
+            return -1;
+        }
+        c->bytes_read += (uint64_t)nread;
+        slot = g53_lru_hit(&m->lru, key);
+        m->lru.hits--;                                /* the read, not a hit */
+    }
+    /* kernels on the compute stream after this point see the slot's bytes */
+    if (m->landed_ok[slot] && hipStreamWaitEvent(g53h_stream(), m->landed[slot], 0) != hipSuccess) {
+        g53_lru_release(&m->lru, key);
+        return -1;
+    }
+    view_of(c, m, slot, out);
+    pump(c, m);
+    sync_stats(c, m);
+    c->load_seconds += now_s() - t0;
+    return 0;
+}
+
+void cache_release(Glm53fExpertSrc *self, int layer, int expert)
+{
+    Glm53fCache *c = (Glm53fCache *)self;
+    Impl *m = impl_of(c);
+    if (layer < 0 || layer >= c->n_layers || expert < 0 || expert >= c->n_experts) return;
+    const int32_t key = layer * c->n_experts + expert;
+    std::lock_guard<std::mutex> g(m->mu);
+    const int slot = m->lru.slot_of[key];
+    if (slot >= 0 && m->lru.pins[slot] > 0) {
+        if (hipEventRecord(m->used[slot], g53h_stream()) == hipSuccess) m->used_ok[slot] = 1;
+        g53_lru_release(&m->lru, key);
+    }
+    poll(c, m);
+    pump(c, m);
+    sync_stats(c, m);
+}
+
+int cache_getmany(Glm53fExpertSrc *self, int layer, const int *ids, int n)
+{
+    Glm53fCache *c = (Glm53fCache *)self;
+    Impl *m = impl_of(c);
+    const double t0 = now_s();
+    std::lock_guard<std::mutex> g(m->mu);
+    poll(c, m);
+    int keys[GLM53F_MAX_TOPK], slots[GLM53F_MAX_TOPK], nw = 0;
+    for (int i = 0; i < n && nw < GLM53F_MAX_TOPK; i++) {
+        const int e = ids[i];
+        if (e < 0 || e >= c->n_experts || layer < 0 || layer >= c->n_layers) continue;
+        const int32_t key = layer * c->n_experts + e;
+        if (m->lru.slot_of[key] >= 0 || m->lru.inflight_of[key] >= 0) continue;
+        const int s = g53_lru_reserve(&m->lru, key);
+        if (s < 0) break;
+        keys[nw] = key; slots[nw] = s; nw++;
+    }
+    int ok_n = 0;
+    for (int k = 0; k < nw; k++) {
+        int64_t nread = 0;
+        const int ok = issue(c, m, slots[k], layer, keys[k] % c->n_experts, m->demand, 0, &nread);
+        g53_lru_land(&m->lru, keys[k], slots[k], ok, 0);
+        if (!ok) {
+            fprintf(stderr, "glm53f_cache: short prefetch of L%d expert %d; slot left empty\n", layer,
+                    keys[k] % c->n_experts);
+            continue;
+        }
+        c->bytes_read += (uint64_t)nread;
+        m->lru.prefetch_reads++;
+        ok_n++;
+    }
+    sync_stats(c, m);
+    c->load_seconds += now_s() - t0;
+    return ok_n;
+}
+
+void cache_hint(Glm53fExpertSrc *self, int layer, const int *ids, int n)
+{
+    Glm53fCache *c = (Glm53fCache *)self;
+    Impl *m = impl_of(c);
+    if (c->n_io <= 0 || layer < 0 || layer >= c->n_layers) return;
+    std::lock_guard<std::mutex> g(m->mu);
+    g53_lru_hint(&m->lru, layer, ids, n);
+    poll(c, m);
+    pump(c, m);
+    sync_stats(c, m);
+}
+
+} /* namespace */
+
+extern "C" int g53h_cache_is(const Glm53fExpertSrc *src) { return src && src->get == cache_get; }
+
+extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
+                                 int n_io, int i4)
+{
+    memset(c, 0, sizeof *c);
+    if (i4) {
+        fprintf(stderr, "glm53f_cache: int4 slots are not supported by the MI355X cache\n");
+        return -1;
+    }
+    if (!st || !st->view || !cfg) return -1;
+    if (g53h_ready()) {
+        fprintf(stderr, "glm53f_cache: %s\n", g53h_error());
+        return -1;
+    }
+    c->st = st;
+    c->cfg = cfg;
+    c->n_layers = cfg->n_layers + 1;       /* the MTP layer streams experts the same way */
+    c->n_experts = cfg->n_experts;
+    int probe = -1;
+    for (int L = 0; L < cfg->n_layers && L < GLM53F_MAX_LAYERS; L++)
+        if (!cfg->is_dense[L]) { probe = L; break; }
+    if (probe < 0) return 0;               /* no MoE layers: nothing to cache */
+    Glm53fExpertQ h;
+    memset(&h, 0, sizeof h);
+    if (st->view(st, probe, 0, &h) != 0) {
+        fprintf(stderr, "glm53f_cache: cannot resolve expert 0 of layer %d\n", probe);
+        return -1;
+    }
+    if (st->done) st->done(st, probe, 0);
+    Impl *m = new Impl();
+    const Glm53fMat *mats[3] = {&h.gate, &h.up, &h.down};
+    size_t off = 0;
+    for (int i = 0; i < 3; i++) {
+        if (mats[i]->dt != GLM53F_WF8) {
+            fprintf(stderr, "glm53f_cache: expert matrices must be FP8\n");
+            delete m;
+            return -1;
+        }
+        m->geo.rows[i] = mats[i]->rows; m->geo.cols[i] = mats[i]->cols;
+        m->geo.br[i] = mats[i]->br; m->geo.bc[i] = mats[i]->bc; m->geo.scols[i] = mats[i]->scols;
+        m->geo.off[i] = off;
+        m->geo.bytes[i] = (size_t)mats[i]->rows * (size_t)mats[i]->cols;
+        off = al(off + m->geo.bytes[i], 256);
+    }
+    for (int i = 0; i < 3; i++) {
+        m->geo.off[3 + i] = off;
+        m->geo.bytes[3 + i] = scale_bytes(*mats[i]);
+        off = al(off + m->geo.bytes[3 + i], 256);
+    }
+    c->slot_bytes = (int64_t)al(off, 4096);
+    c->nslot = (int)(budget_bytes / c->slot_bytes);
+    if (c->nslot < cfg->topk + 1) {
+        fprintf(stderr, "glm53f_cache: budget %.2f GB gives %d slots of %.2f MB; top-%d needs at least %d\n",
+                (double)budget_bytes / 1e9, c->nslot, (double)c->slot_bytes / 1e6, cfg->topk, cfg->topk + 1);
+        delete m;
+        return -1;
+    }
+    if (g53_lru_init(&m->lru, c->n_layers, c->n_experts, c->nslot, 64 * 4 * GLM53F_MAX_TOPK) != 0) {
+        delete m;
+        return -1;
+    }
+    m->arena = (uint8_t *)g53h_alloc((size_t)c->nslot * (size_t)c->slot_bytes);
+    if (!m->arena) {
+        fprintf(stderr, "glm53f_cache: cannot allocate a %.2f GB arena in HBM\n",
+                (double)c->nslot * (double)c->slot_bytes / 1e9);
+        g53_lru_free(&m->lru);
+        delete m;
+        return -1;
+    }
+    m->landed.resize(c->nslot);
+    m->used.resize(c->nslot);
+    m->landed_ok.assign(c->nslot, 0);
+    m->used_ok.assign(c->nslot, 0);
+    bool ok = true;
+    for (int i = 0; i < c->nslot && ok; i++)
+        ok = hipEventCreateWithFlags(&m->landed[i], hipEventDisableTiming) == hipSuccess &&
+             hipEventCreateWithFlags(&m->used[i], hipEventDisableTiming) == hipSuccess;
+    m->demand = g53h_copy_stream();
+    ok = ok && hipStreamCreateWithFlags(&m->prefetch, hipStreamNonBlocking) == hipSuccess;
+    c->impl = m;
+    if (!ok) {
+        fprintf(stderr, "glm53f_cache: cannot create the copy events and streams\n");
+        glm53f_cache_free(c);
+        return -1;
+    }
+    c->n_io = n_io > 0 ? n_io : 0;
+    c->src.get = cache_get;
+    c->src.release = cache_release;
+    c->src.getmany = cache_getmany;
+    c->src.hint = cache_hint;
+    c->src.ctx = c;
+    return 0;
+}
+
+extern "C" int glm53f_cache_sync(Glm53fCache *c)
+{
+    Impl *m = impl_of(c);
+    if (!m) return 0;
+    std::lock_guard<std::mutex> g(m->mu);
+    if (hipStreamSynchronize(m->demand) != hipSuccess || hipStreamSynchronize(m->prefetch) != hipSuccess) return -1;
+    poll(c, m);
+    return 0;
+}
+
+extern "C" void glm53f_cache_free(Glm53fCache *c)
+{
+    Impl *m = impl_of(c);
+    if (m) {
+        (void)hipDeviceSynchronize();
+        poll(c, m);
+        for (hipEvent_t e : m->landed) if (e) (void)hipEventDestroy(e);
+        for (hipEvent_t e : m->used) if (e) (void)hipEventDestroy(e);
+        for (hipEvent_t e : m->pool) (void)hipEventDestroy(e);
+        for (Copy &cp : m->inflight) (void)hipEventDestroy(cp.ev);
+        if (m->prefetch) (void)hipStreamDestroy(m->prefetch);
+        if (m->arena) g53h_free(m->arena);
+        g53_lru_free(&m->lru);
+        delete m;
+    }
+    memset(c, 0, sizeof *c);
+}
+
+extern "C" void glm53f_cache_reset_stats(Glm53fCache *c)
+{
+    Impl *m = impl_of(c);
+    if (!m) return;
+    std::lock_guard<std::mutex> g(m->mu);
+    m->lru.hits = m->lru.misses = m->lru.evictions = m->lru.prefetch_reads = 0;
+    m->lru.bg_reads = m->lru.bg_used = 0;
+    c->bytes_read = c->bg_bytes = 0;
+    c->load_seconds = 0.0;
+    sync_stats(c, m);
+}
+
+extern "C" void glm53f_cache_report(const Glm53fCache *c, const char *label)
+{
+    const Impl *m = impl_of(c);
+    if (!m || glm53f_quiet) return;
+    int resident = 0;
+    for (int i = 0; i < c->nslot; i++) if (m->lru.key_of[i] >= 0) resident++;
+    const uint64_t n = c->hits + c->misses;
+    const uint64_t served = c->hits > c->prefetch_reads ? c->hits - c->prefetch_reads : 0;
+    printf("expert cache [%s]\n", label ? label : "");
+    printf("  slots          : %d x %.2f MB = %.2f GB of HBM (%d resident), %d prefetch reads in flight\n",
+           c->nslot, (double)c->slot_bytes / 1e6, (double)c->nslot * c->slot_bytes / 1e9, resident, c->n_io);
+    printf("  requests       : %llu, resident when requested: %llu (%.1f%%)\n", (unsigned long long)n,
+           (unsigned long long)served, n ? 100.0 * served / n : 0.0);
+    printf("  foreground     : %.2f GB copied to HBM, %.3f s in get/getmany, %llu evictions\n",
+           (double)c->bytes_read / 1e9, c->load_seconds, (unsigned long long)c->evictions);
+    if (c->n_io)
+        printf("  prefetch       : %llu experts read ahead (%.2f GB), %llu of them used\n",
+               (unsigned long long)c->bg_reads, (double)c->bg_bytes / 1e9, (unsigned long long)c->bg_used);
+}
+
+/* ------------------------------------------------------- synthetic host store ---- */
+namespace {
+
+struct SynthStore {
+    int hidden, inter, n_layers, n_experts, n_pool;
+    uint8_t *pinned;                 /* n_pool experts: codes g, u, d, scales g, u, d */
+    size_t per, off[6];
+};
+
+int synth_view(const Glm53fSt *st, int layer, int expert, Glm53fExpertQ *h)
+{
+    const SynthStore *s = (const SynthStore *)st->ctx;
+    if (layer < 0 || layer >= s->n_layers || expert < 0 || expert >= s->n_experts) return -1;
+    const long key = (long)layer * s->n_experts + expert;
+    const uint8_t *b = s->pinned + (size_t)(key % s->n_pool) * s->per;
+    const int rows[3] = {s->inter, s->inter, s->hidden}, cols[3] = {s->hidden, s->hidden, s->inter};
+    Glm53fMat *mats[3] = {&h->gate, &h->up, &h->down};
+    for (int i = 0; i < 3; i++) {
+        Glm53fMat &m = *mats[i];
+        m.w = b + s->off[i];
+        m.s = (const float *)(b + s->off[3 + i]);
+        m.dt = GLM53F_WF8;
+        m.rows = rows[i]; m.cols = cols[i];
+        m.br = 128; m.bc = 128;
+        m.scols = (cols[i] + 127) / 128;
+    }
+    return 0;
+}
+
+} /* namespace */
+
+extern "C" int g53h_store_synth_init(Glm53fSt *st, int hidden, int inter, int n_layers, int n_experts, int n_pool,
+                                     uint64_t seed, float sigma)
+{
+    memset(st, 0, sizeof *st);
+    if (hidden <= 0 || inter <= 0 || n_layers <= 0 || n_experts <= 0 || n_pool <= 0) return -1;
+    if (g53h_ready()) return -1;
+    SynthStore *s = new SynthStore();
+    s->hidden = hidden; s->inter = inter; s->n_layers = n_layers; s->n_experts = n_experts; s->n_pool = n_pool;
+    const int rows[3] = {inter, inter, hidden}, cols[3] = {hidden, hidden, inter};
+    size_t off = 0;
+    for (int i = 0; i < 3; i++) { s->off[i] = off; off = al(off + (size_t)rows[i] * cols[i], 256); }
+    for (int i = 0; i < 3; i++) {
+        s->off[3 + i] = off;
+        off = al(off + (size_t)((rows[i] + 127) / 128) * ((cols[i] + 127) / 128) * 4, 256);
+    }
+    s->per = al(off, 4096);
+    s->pinned = (uint8_t *)g53h_host_alloc(s->per * (size_t)n_pool);
+    uint8_t *dev = (uint8_t *)g53h_alloc(s->per);
+    if (!s->pinned || !dev) {
+        if (s->pinned) g53h_host_free(s->pinned);
+        if (dev) g53h_free(dev);
+        delete s;
+        return g53h_fail("g53h_store_synth_init: cannot allocate %zu bytes of pinned host memory", s->per * (size_t)n_pool);
+    }
+    /* pool entry p is expert p of the synthetic layer 0: the streams of glm53h.synth */
+    for (int p = 0; p < n_pool; p++) {
+        for (int i = 0; i < 3; i++) {
+            const uint64_t strm = (4ull << 32) | (uint64_t)(p * 3 + i);
+            if (g53h_synth_f8(dev + s->off[i], (float *)(dev + s->off[3 + i]), rows[i], cols[i], 128, 128, seed, strm,
+                              sigma))
+                goto fail;
+        }
+        if (g53h_sync() || g53h_d2h(s->pinned + (size_t)p * s->per, dev, s->per)) goto fail;
+    }
+    g53h_free(dev);
+    st->view = synth_view;
+    st->done = nullptr;
+    st->ctx = s;
+    return 0;
+fail:
+    g53h_free(dev);
+    g53h_host_free(s->pinned);
+    delete s;
+    return -1;
+}
+
+extern "C" void g53h_store_synth_free(Glm53fSt *st)
+{
+    SynthStore *s = (SynthStore *)st->ctx;
+    if (s) {
+        g53h_host_free(s->pinned);
+        delete s;
+    }
+    memset(st, 0, sizeof *st);
+}

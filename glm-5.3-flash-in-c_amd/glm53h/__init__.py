@@ -96,6 +96,25 @@ class Glm53fMoeW(C.Structure):
                 ("prefill_next", C.c_int), ("layer", C.c_int)]
 
 
+VIEW_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(Glm53fExpertQ))
+DONE_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_int)
+
+
+class Glm53fSt(C.Structure):
+    """include/glm53f_cache.h: the store the HBM expert cache reads experts from."""
+    _fields_ = [("view", VIEW_FN), ("done", DONE_FN), ("ctx", C.c_void_p)]
+
+
+class Glm53fCache(C.Structure):
+    """include/glm53f_cache.h (src must stay first)."""
+    _fields_ = [("src", Glm53fExpertSrc), ("st", C.c_void_p), ("cfg", C.c_void_p),
+                ("n_layers", C.c_int), ("n_experts", C.c_int), ("slot_bytes", C.c_int64),
+                ("nslot", C.c_int), ("n_io", C.c_int), ("impl", C.c_void_p),
+                ("hits", C.c_uint64), ("misses", C.c_uint64), ("evictions", C.c_uint64),
+                ("bytes_read", C.c_uint64), ("prefetch_reads", C.c_uint64), ("load_seconds", C.c_double),
+                ("bg_reads", C.c_uint64), ("bg_bytes", C.c_uint64), ("bg_used", C.c_uint64)]
+
+
 # ------------------------------------------------------------------- loading ----
 _SIGS = {
     # runtime
@@ -170,6 +189,19 @@ _SIGS = {
     "glm53f_mlp": (None, [C.c_void_p, C.c_void_p, C.POINTER(Glm53fMat), C.POINTER(Glm53fMat),
                           C.POINTER(Glm53fMat), C.c_float, C.c_void_p]),
     "glm53f_forget_host_weights": (None, []),
+    # expert cache (glm53f_cache.h)
+    "glm53f_cache_init": (C.c_int, [C.POINTER(Glm53fCache), C.POINTER(Glm53fSt), C.POINTER(Glm53fCfg), C.c_int64,
+                                    C.c_int, C.c_int]),
+    "glm53f_cache_free": (None, [C.POINTER(Glm53fCache)]),
+    "glm53f_cache_reset_stats": (None, [C.POINTER(Glm53fCache)]),
+    "glm53f_cache_report": (None, [C.POINTER(Glm53fCache), C.c_char_p]),
+    "glm53f_cache_sync": (C.c_int, [C.POINTER(Glm53fCache)]),
+    "g53h_cache_is": (C.c_int, [C.POINTER(Glm53fExpertSrc)]),
+    "g53h_store_synth_init": (C.c_int, [C.POINTER(Glm53fSt), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.c_uint64, C.c_float]),
+    "g53h_store_synth_free": (None, [C.POINTER(Glm53fSt)]),
+    "g53h_lru_trace": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                                 C.c_void_p]),
 }
 
 

@@ -21,6 +21,7 @@
 #include "g53h.h"
 #include "g53h_core.h"
 #include "glm53f.h"
+#include "glm53f_cache.h"
 
 long glm53f_expert_drops = 0;
 int  glm53f_quiet = 0;
@@ -510,8 +511,11 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
             }
             if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
         }
-        /* the kernels that read this batch have finished: release it */
-        if (g53h_sync()) g53_die("glm53f_moe");
+        /* release the batch once the kernels that read it are done: the HBM cache orders that
+         * on the device (release records an event its next copy into the slot waits for); any
+         * other source, or a next batch that rewrites the descriptor table, waits for the
+         * stream to drain */
+        if ((!g53h_cache_is(src) || b0 + B < nu) && g53h_sync()) g53_die("glm53f_moe");
         if (src->release)
             for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
     }

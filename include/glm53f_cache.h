@@ -1,0 +1,102 @@
+/* glm53f_cache.h - the routed-expert cache, in HBM, with predictive prefetch from host memory.
+ *
+ * Drop-in for the reference's src/cache/glm53f_cache.h:99-103 (glm53f_cache_init/free/
+ * reset_stats/report) and its Glm53fCache whose first member is the Glm53fExpertSrc the MoE
+ * layer reads experts through (src/cache/glm53f_cache.h:45). Same policy as the reference
+ * (src/cache/glm53f_cache.c): LRU over fixed slots, a slot is never handed out while pinned
+ * (between get() and release()) or while a read into it is being set up; hint() queues the
+ * experts a layer will need, ordered by layer, and cancels stale entries; prefetch changes
+ * only what is resident when, never what get() returns.
+ *
+ * What is different on MI355X:
+ *   - the slots are HBM (a slot holds one expert's FP8 codes and block scales) and get()
+ *     returns DEVICE views: pass them to the library's kernels (glm53f_moe does);
+ *   - a missing expert is copied from the store's host memory (pinned for full PCIe speed) with
+ *     hipMemcpyAsync on a copy stream; the library's compute stream waits for that copy with
+ *     a stream event, so get() does not block the host;
+ *   - release() records an event on the compute stream; a later copy into the same slot waits
+ *     for it on the copy stream, so a slot is never overwritten while a kernel still reads it;
+ *   - n_io is the number of prefetch copies kept in flight (0 disables prefetch), instead of a
+ *     number of I/O threads;
+ *   - the store is any Glm53fSt below, e.g. experts kept in pinned host memory, or a reader of
+ *     the checkpoint (the reference's glm53f_expert_ref/glm53f_expert_load into a pinned
+ *     staging buffer);
+ *   - int4 slots (i4 != 0) are not supported: init returns -1.
+ */
+#ifndef GLM53F_CACHE_H
+#define GLM53F_CACHE_H
+
+#include <stdint.h>
+
+#include "glm53f.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Where the cache reads experts from. view() fills host views of the expert's three FP8
+ * matrices (codes and fp32 scales, GLM53F_WF8) and returns 0, or -1 when the expert cannot be
+ * read (get() then fails: a dropped expert). The bytes must stay valid until done() is called
+ * for that expert (when the copy to HBM has completed); done may be NULL for a store whose
+ * bytes never move. Calls come from the thread that calls the cache. */
+typedef struct Glm53fSt {
+    int  (*view)(const struct Glm53fSt *st, int layer, int expert, Glm53fExpertQ *host);
+    void (*done)(const struct Glm53fSt *st, int layer, int expert);
+    void *ctx;
+} Glm53fSt;
+
+typedef struct {
+    Glm53fExpertSrc  src;         /* MUST be first: pass &cache->src to Glm53fMoeW          */
+    const Glm53fSt  *st;
+    const Glm53fCfg *cfg;
+    int              n_layers, n_experts;
+    int64_t          slot_bytes;
+    int              nslot;
+    int              n_io;        /* prefetch copies in flight, 0 = prefetch disabled        */
+    void            *impl;        /* library state (slots in HBM, events, LRU bookkeeping)   */
+    /* statistics (reset by glm53f_cache_reset_stats), as the reference's */
+    uint64_t         hits, misses, evictions, bytes_read, prefetch_reads;
+    double           load_seconds;    /* host time spent in get()/getmany()              */
+    uint64_t         bg_reads, bg_bytes, bg_used;
+} Glm53fCache;
+
+/* budget_bytes is the HBM arena, rounded down to whole experts. The slot geometry comes from
+ * expert 0 of the first MoE layer (cfg->is_dense), as the reference probes it. Fails (-1) if
+ * fewer than topk+1 slots fit, if HBM cannot hold the arena, or for i4 != 0. */
+int  glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
+                       int n_io, int i4);
+void glm53f_cache_free(Glm53fCache *c);
+void glm53f_cache_reset_stats(Glm53fCache *c);
+void glm53f_cache_report(const Glm53fCache *c, const char *label);
+
+/* Wait until every copy the cache issued has landed (tests and benchmarks). */
+int  glm53f_cache_sync(Glm53fCache *c);
+/* 1 when src is the expert source of a cache made by glm53f_cache_init (its views are HBM and
+ * its release is ordered on the device), else 0. */
+int  g53h_cache_is(const Glm53fExpertSrc *src);
+
+/* A store of experts in pinned host memory built by the library: n_pool distinct experts
+ * generated from the seeded synthetic distribution (FP8 E4M3, N(0, sigma^2) absmax-quantised
+ * per 128 x 128 block) of the given shapes; expert (layer, e) is pool entry
+ * (layer * n_experts + e) % n_pool. For benchmarks and tests that need more experts than host
+ * memory holds distinct copies of. */
+int  g53h_store_synth_init(Glm53fSt *st, int hidden, int inter, int n_layers, int n_experts, int n_pool,
+                           uint64_t seed, float sigma);
+void g53h_store_synth_free(Glm53fSt *st);
+
+/* The LRU policy alone on a scripted trace (CPU, no device): ops are
+ *   1 L E        get          -> out: rc, was resident (1/0), slot
+ *   2 L E        release
+ *   3 L n e...   getmany      -> out: rc
+ *   4 L n e...   hint         -> out: queue length, then the queued keys
+ *   5 k          serve up to k queued hints as background reads -> out: (key, slot) per read, -1
+ * and stats receives hits, misses, evictions, prefetch_reads, bg_reads, bg_used. Returns the
+ * number of ints written to out, or -1. For checking the policy against the reference. */
+int  g53h_lru_trace(int n_layers, int n_experts, int nslot, const int *ops, int nops, int *out, int outcap,
+                    long long *stats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLM53F_CACHE_H */

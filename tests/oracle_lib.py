@@ -59,6 +59,10 @@ def ref():
         L.ref_mm.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int,
                              C.c_int, C.c_int]
         L.ref_swiglu.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_float]
+        if hasattr(L, "ref_cache_trace"):
+            L.ref_cache_trace.restype = C.c_int
+            L.ref_cache_trace.argtypes = [C.c_char_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                                          C.c_void_p, C.c_void_p, C.c_void_p]
         L.ref_e4m3f.restype = C.c_float
         L.ref_e4m3f.argtypes = [C.c_uint8]
         _ref = L
