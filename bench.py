@@ -14,7 +14,17 @@ roofline of the dominant kernel (k_dec_experts) measured live with HIP events on
 stream, and the reference CPU expert path (compiled from the reference's sources, oracle/_ref)
 timed on this host's cores on a bounded sample of the same workload.
 
+Other BASELINE configs (one JSON line each, same contract), with --workload:
+  3  batched decode: 64 tokens x top-8 over 288 experts with Zipf(1.1) popularity, one layer call
+     of 64 tokens per step (the grouped FP8-MFMA path); metric us per 64-token layer call
+  4  prefill: 2048 tokens, uniform routing, one layer call per step (grouped path); metric ms
+     per layer, with TFLOP/s against the FP8 dense peak and GB/s against the HBM floor
+  5  42-layer decode stack, 32 steps, through the drop-in glm53f_moe with the HBM expert cache
+     (200 GB of slots) filled from pinned host memory and next-layer prefetch; metric us per
+     layer, with hit rate and host-to-HBM GB/s
+
 Usage: python bench.py [--gpus 1] [--steps 400] [--warmup 50] [--no-cpu] [--cpu-seconds 10]
+       python bench.py --workload 3|4|5 [--steps K] [--warmup W] [--no-cpu]
        python bench.py --copy-calibration   (device-to-device copies of 256 MiB, for scaling
                                              rocprof's FETCH_SIZE / WRITE_SIZE counters)
 """
@@ -37,6 +47,7 @@ import glm53h.synth as S  # noqa: E402
 from glm53h import DevBuf, G53hExpert, G53hMoeLayer, check  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0      # MI355X HBM3E, vendor figure
+FP8_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 matrix peak, vendor figure
 NTOK = 64
 NCOPY = 12                  # router / shared-expert address copies used in turn
 
@@ -123,6 +134,265 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
 
 
+def prof_run(L, fn, n, tags):
+    """Per-kernel averages (us) over n calls of fn, from the library's HIP events."""
+    check(L.g53h_prof_enable(1), "prof")
+    for i in range(n):
+        fn(i)
+    tms = (C.c_float * 8)()
+    cnt = (C.c_int * 8)()
+    check(L.g53h_prof_collect(tms, cnt, 8), "collect")
+    check(L.g53h_prof_enable(0), "prof")
+    return {name: (round(tms[i] / cnt[i] * 1e3, 2) if cnt[i] else None) for i, name in tags}
+
+
+def cpu_grouped(layer, x, idx, seconds):
+    """The reference's glm53f_moe (oracle/_ref) on this host for the same token batch, experts in
+    host RAM: one call of all T tokens per sample (the reference splits them into 64-token
+    chunks itself), repeated for about `seconds`."""
+    import oracle_lib as O
+    if not O.have_ref():
+        return None
+    sp = layer.sp
+    mats = {int(e): layer.fetch_expert(int(e)) for e in np.unique(idx)}
+    sh = layer.fetch_expert("shared")
+    R = O.ref()
+    O.moe(R, x[:2], sp, layer.router_f32, layer.bias_f32, mats, sh)          # warm-up
+    times, t_end = [], time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 1:
+        t0 = time.perf_counter()
+        O.moe(R, x, sp, layer.router_f32, layer.bias_f32, mats, sh)
+        times.append(time.perf_counter() - t0)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    return statistics.median(times), len(times), threads
+
+
+def bench_grouped(a):
+    """BASELINE configs 3 and 4 on the grouped path (g53h_moe with T tokens)."""
+    L = glm53h.init(0)
+    cfg = a.workload
+    sp = S.spec(3 if cfg == 3 else 2)
+    T = 64 if cfg == 3 else 2048
+    steps = a.steps if a.steps != 400 else (200 if cfg == 3 else 30)
+    warm = a.warmup if a.warmup != 50 else 5
+    layer = S.DeviceLayer.build(sp)
+    nb = 4
+    xs = [S.x_host(sp, T, batch=b) for b in range(nb)]
+    xd = [DevBuf.from_array(x) for x in xs]
+    out = DevBuf(T * sp.E * 4)
+    idx = DevBuf(T * sp.K * 4)
+    uniq = []
+    for b in range(nb):
+        check(L.g53h_moe(out.ptr, xd[b].ptr, T, C.byref(layer.layer), idx.ptr, None), "g53h_moe")
+        uniq.append(len(np.unique(idx.download(np.int32))))
+    assert L.g53h_grouped_errors() == 0
+
+    def step(i):
+        check(L.g53h_moe(out.ptr, xd[i % nb].ptr, T, C.byref(layer.layer), None, None), "g53h_moe")
+
+    for i in range(warm):
+        step(i)
+    glm53h.sync()
+    check(L.g53h_mark(), "mark")
+    for i in range(steps):
+        step(i)
+    check(L.g53h_mark(), "mark")
+    ms = L.g53h_elapsed_ms() / steps
+    glm53h.sync()
+    per = prof_run(L, step, min(steps, 40), [(1, "k_router_mfma"), (5, "k_grp_plan+k_grp_xq"), (2, "k_grp_gateup"),
+                                              (3, "k_grp_down"), (6, "k_grp_combine")])
+    D = float(np.mean(uniq))
+    eb = sp.expert_bytes()
+    gu_bytes = (D + 1) * 2 * (sp.I * sp.E + (sp.I // 128) * (sp.E // 128) * 4)
+    layer_bytes = (D + 1) * eb + sp.NE * sp.E * 2 + sp.NE * 4 + T * sp.E * 4 * 2
+    flops = 2.0 * (T * sp.K + T) * 3 * sp.E * sp.I
+    gbps = layer_bytes / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    gu_gbps = gu_bytes / (per["k_grp_gateup"] * 1e-6) / 1e9
+    cpu = None
+    if not a.no_cpu:
+        r = cpu_grouped(layer, xs[0], _routing(L, layer, xd[0], T), a.cpu_seconds)
+        if r:
+            med, n, threads = r
+            cpu = {"value": round(med * (1e6 if cfg == 3 else 1e3), 1), "unit": "us/layer" if cfg == 3 else "ms/layer",
+                   "cores": threads, "kind": "reference",
+                   "sample": f"reference glm53f_moe (src/core/glm53f_ops.c, 64-token chunks) compiled -O3 -mavx2 "
+                             f"-mfma -fopenmp -ffp-contract=off, OpenMP threads {threads}; the same {T}-token batch "
+                             f"(batch 0), median of {n} call(s), experts in host RAM",
+                   "tflops": round(flops / med / 1e12, 3)}
+    name = "moe_batched_decode_layer_time" if cfg == 3 else "moe_prefill_layer_time"
+    line = {
+        "metric": name,
+        "value": round(ms * 1e3, 2) if cfg == 3 else round(ms, 4),
+        "unit": "us/layer" if cfg == 3 else "ms/layer",
+        "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(ms, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32 accumulate, fp8 MFMA",
+        "data": "synthetic (seeded FP8 E4M3 experts N(0,0.02) absmax-quantised per 128x128 block; bf16 x ~N(0,1))",
+        "config": {"workload": (f"BASELINE config 3: batched decode, {T} tokens x top-8, Zipf(1.1) popularity"
+                                if cfg == 3 else f"BASELINE config 4: prefill, {T} tokens, uniform routing, + shared"),
+                   "tokens": T, "token_batches_cycled": nb, "unique_routed_experts": D,
+                   "parallelism": "single GPU"},
+        "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "tflops": round(tflops, 2),
+        "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+        "hbm_GBps": round(gbps, 1),
+        "hbm_floor_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "algorithmic_bytes_per_layer": int(layer_bytes),
+        "kernels_us": per,
+        "roofline": {"bound": "hbm", "kernel": "k_grp_gateup", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_launch": int(gu_bytes), "avg_launch_us": per["k_grp_gateup"]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def _routing(L, layer, xd, T):
+    sp = layer.sp
+    idx, w = DevBuf(T * sp.K * 4), DevBuf(T * sp.K * 4)
+    check(L.g53h_router(idx.ptr, w.ptr, xd.ptr, T, layer.router.ptr, 1, layer.bias.ptr, sp.NE, sp.E, sp.K,
+                        sp.norm_topk, C.c_float(sp.routed_scale), None), "router")
+    return idx.download(np.int32).reshape(T, sp.K)
+
+
+def cpu_stack_layer(sp, W, b, x, sh, seconds):
+    """The reference's glm53f_moe for one layer of the stack (one token), experts already in host
+    RAM (the reference's cache would read misses from storage; that is not timed)."""
+    import oracle_lib as O
+    if not O.have_ref():
+        return None
+    idx, _ = O.router(O.oracle(), x[None, :], sp, W, b)
+    mats = {int(e): S.expert_host(sp, int(e)) for e in idx[0]}
+    R = O.ref()
+    xt = x[None, :]
+    O.moe(R, xt, sp, W, b, mats, sh)
+    times, t_end = [], time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 20:
+        t0 = time.perf_counter()
+        O.moe(R, xt, sp, W, b, mats, sh)
+        times.append(time.perf_counter() - t0)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    return {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/layer", "cores": threads,
+            "kind": "reference",
+            "sample": f"reference glm53f_moe, one stack layer (layer 0, one token), experts in host RAM (no storage "
+                      f"reads), OpenMP threads {threads}, median of {len(times)} calls"}
+
+
+def bench_stack(a):
+    """a 42-layer stack of routed-expert layers (config-2 shapes) in single-
+    token decode, 32 steps, each layer one glm53f_moe call (the drop-in, with the reference's
+    hint protocol: own experts, then the next layer's router on this input, prefetch_n 6). The
+    experts come through the HBM cache (200 GB of slots) from pinned host memory. Per-layer
+    routers are seeded bf16 with a Zipf(1.1) selection bias over a per-layer permutation; each
+    layer's input follows x <- 0.9 x + sqrt(1 - 0.81) z (bf16), which reuses about 70% of a
+    layer's experts from one token to the next. The cache starts holding the 189 most popular
+    experts of every layer (7,938 experts, what 200 GB holds), the steady state of a long run."""
+    L = glm53h.init(0)
+    NL, steps, warm = 42, (a.steps if a.steps != 400 else 32), (a.warmup if a.warmup != 50 else 2)
+    base = S.spec(3)
+    E, I, NE, K = base.E, base.I, base.NE, base.K
+    rho, pf, n_io = 0.9, 6, 4
+    cf = glm53h.Glm53fCfg()
+    cf.hidden, cf.n_layers, cf.n_experts, cf.topk, cf.n_shared, cf.moe_inter = E, NL, NE, K, 1, I
+    cf.routed_scale, cf.norm_topk, cf.swiglu_limit = base.routed_scale, base.norm_topk, base.limit
+    cf.fp8_block_r, cf.fp8_block_c = 128, 128
+    print(f"[bench] config 5: building the pinned host store ({NE} experts)", file=sys.stderr, flush=True)
+    st = glm53h.Glm53fSt()
+    check(L.g53h_store_synth_init(C.byref(st), E, I, NL + 1, NE, NE, base.seed, C.c_float(base.expert_sigma)), "store")
+    cache = glm53h.Glm53fCache()
+    budget = 200 * 10 ** 9
+    if L.glm53f_cache_init(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io, 0) != 0:
+        sys.exit("glm53f_cache_init failed")
+    specs = [S.spec(3, layer=l) for l in range(NL)]
+    W = [S.router_host(s_) for s_ in specs]
+    B = [S.bias_host(s_) for s_ in specs]
+    sh = S.expert_host(base, "shared")
+    per_layer = cache.nslot // NL
+    print(f"[bench] config 5: filling {per_layer} x {NL} slots of {cache.nslot}", file=sys.stderr, flush=True)
+    for l in range(NL):
+        ranked = np.argsort(-B[l], kind="stable")[:per_layer].astype(np.int32)
+        for c0 in range(0, len(ranked), 64):
+            ids = np.ascontiguousarray(ranked[c0:c0 + 64])
+            cache.src.getmany(C.byref(cache.src), l, ids.ctypes.data_as(C.POINTER(C.c_int)), len(ids))
+    check(L.glm53f_cache_sync(C.byref(cache)), "cache sync")
+    rng = np.random.default_rng(5)
+
+    def bf16(v):
+        return (np.asarray(v, np.float32).view(np.uint32) + 0x8000 & 0xFFFF0000).view(np.float32)
+
+    xs = [bf16(rng.standard_normal(E)) for _ in range(NL)]
+    ws = []
+    for l in range(NL):
+        w = glm53h.Glm53fMoeW()
+        w.gate, w.bias = W[l].ctypes.data, B[l].ctypes.data
+        (gw, gs), (uw, us), (dw, ds) = sh
+        w.sh_gate = glm53h.Glm53fMat(gw.ctypes.data, gs.ctypes.data, glm53h.GLM53F_WF8, I, E, 128, 128, E // 128)
+        w.sh_up = glm53h.Glm53fMat(uw.ctypes.data, us.ctypes.data, glm53h.GLM53F_WF8, I, E, 128, 128, E // 128)
+        w.sh_down = glm53h.Glm53fMat(dw.ctypes.data, ds.ctypes.data, glm53h.GLM53F_WF8, E, I, 128, 128, I // 128)
+        w.src = C.pointer(cache.src)
+        w.layer, w.prefetch_n = l, pf
+        if l + 1 < NL:
+            w.next_gate, w.next_bias = W[l + 1].ctypes.data, B[l + 1].ctypes.data
+        ws.append(w)
+    out = np.zeros((1, E), np.float32)
+    fn = L.glm53f_moe
+
+    def step():
+        for l in range(NL):
+            xs[l] = bf16(rho * xs[l] + np.sqrt(1 - rho * rho) * rng.standard_normal(E))
+            fn(out.ctypes.data, xs[l].ctypes.data, C.byref(ws[l]), C.byref(cf), 1, None)
+
+    print("[bench] config 5: warm-up", file=sys.stderr, flush=True)
+    for _ in range(warm):
+        step()
+    check(L.glm53f_cache_sync(C.byref(cache)), "cache sync")
+    L.glm53f_cache_reset_stats(C.byref(cache))
+    glm53h.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    glm53h.sync()
+    dt = time.perf_counter() - t0
+    us_layer = dt * 1e6 / (steps * NL)
+    hits, misses, bg_reads, bg_used = cache.hits, cache.misses, cache.bg_reads, cache.bg_used
+    h2d = cache.bytes_read + cache.bg_bytes
+    # the link's rate on its own: 16 expert copies from the pinned store into a slot-sized buffer
+    q = glm53h.Glm53fExpertQ()
+    st.view(C.cast(C.pointer(st), C.c_void_p), 0, 0, C.byref(q))
+    dbuf = DevBuf(int(cache.slot_bytes))
+    mats = [q.gate, q.up, q.down]
+    t1 = time.perf_counter()
+    for _ in range(16):
+        for m in mats:
+            check(L.g53h_h2d(dbuf.ptr, m.w, m.rows * m.cols), "h2d")
+    link = 16 * sum(m.rows * m.cols for m in mats) / (time.perf_counter() - t1) / 1e9
+    L.glm53f_cache_report(C.byref(cache), b"config 5")
+    nslot = cache.nslot
+    L.glm53f_cache_free(C.byref(cache))
+    L.g53h_store_synth_free(C.byref(st))
+    eb = base.expert_bytes()
+    line = {
+        "metric": "moe_stack_decode_layer_time",
+        "value": round(us_layer, 2),
+        "unit": "us/layer",
+        "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(dt * 1e3 / steps, 3),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded FP8 experts; per-layer bf16 routers with Zipf(1.1) bias; correlated bf16 inputs)",
+        "config": {"workload": "BASELINE config 5: 42-layer decode stack, 32 steps, HBM expert cache of 200 GB, "
+                               "the rest in pinned host memory, next-layer prefetch",
+                   "layers": NL, "slots": nslot,
+                   "prefetch_n": pf, "prefetch_reads_in_flight": n_io, "input_correlation": rho,
+                   "parallelism": "single GPU"},
+        "hit_rate": round(hits / max(hits + misses, 1), 4),
+        "requests": int(hits + misses), "misses": int(misses),
+        "prefetch_reads": int(bg_reads), "prefetch_used": int(bg_used),
+        "h2d_GB": round(h2d / 1e9, 3), "h2d_GBps_avg": round(h2d / dt / 1e9, 2), "h2d_link_GBps": round(link, 2),
+        "hbm_GBps_experts": round((K + 1) * eb / (us_layer * 1e-6) / 1e9, 1),
+        "cpu_baseline": None if a.no_cpu else cpu_stack_layer(base, W[0], B[0], xs[0], sh, a.cpu_seconds),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,12 +401,17 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
     a = ap.parse_args()
     if a.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (expert-parallel "
                  "sharding is a design note only); run with --gpus 1")
     if a.copy_calibration:
         return copy_calibration()
+    if a.workload in (3, 4):
+        return bench_grouped(a)
+    if a.workload == 5:
+        return bench_stack(a)
     L = glm53h.init(0)
     sp = S.spec(2)
     layer = S.DeviceLayer.build(sp)
