@@ -54,17 +54,31 @@ typedef __attribute__((address_space(1))) const g53_v8i g53_gv8i;
 typedef __attribute__((address_space(1))) const g53_v4i g53_gv4i;
 typedef __attribute__((address_space(1))) const float g53_gflt;
 
-#define G53_GRP_NT    64      /* positions per tile                                        */
+#define G53_GRP_NT    128     /* positions per tile                                        */
+#define G53_GRP_NH    (G53_GRP_NT / 32)   /* 32-position halves of a tile (matrix-core columns) */
 #define G53_GRP_XST   144     /* LDS bytes per token row of a 128-byte slice (16 B padding) */
 #define G53_GRP_MAXT  2048    /* tokens per planning pass                                   */
 #define G53_GRP_NPX   2       /* E4M3 planes of the input activations                       */
 #define G53_GRP_NPA   2       /* E4M3 planes of the SwiGLU activations                      */
 #define G53_GRP_MASKS 12288   /* LDS 64-token masks of the planner (chunks x experts)       */
-#define G53_GRP_NW    4       /* waves of a GEMM workgroup (two workgroups per CU)           */
+#define G53_GRP_NW    8       /* waves of a GEMM workgroup                                   */
+#ifndef G53_GRP_WPC
+#define G53_GRP_WPC   1       /* GEMM workgroups resident per CU                             */
+#endif
+#ifndef G53_GRP_RS
+#define G53_GRP_RS    4       /* weight blocks in a lane's ring                              */
+#endif
+#ifndef G53_GRP_LXS
+#define G53_GRP_LXS   2       /* activation slices in a thread's ring                        */
+#endif
+#ifndef G53_GRP_NS
+#define G53_GRP_NS    4       /* activation slices in the workgroup's LDS ring               */
+#endif
 
 /* error flags (meta[1]) */
 #define G53_GRP_EIDX  1       /* a routed index outside [0, n_experts)                      */
 #define G53_GRP_EDESC 8       /* an expert descriptor without the expected 128x128 layout   */
+#define G53_GRP_ESPIN 2       /* a wait on the slice ring timed out                          */
 
 /* ------------------------------------------------------------------ planning ---- */
 /* Counting sort of the T*K (token, slot) pairs by expert, stable in token order. For each
@@ -210,64 +224,78 @@ k_grp_xq(const float *__restrict__ x, int E, int T, uint8_t *__restrict__ xq, fl
  * ring of R slots), runs block kb on the matrix cores from LDS slice kb, then stores slice
  * kb + 1 to the other LDS buffer. Loads complete in issue order, so that store waits for the
  * weights up to block kb + LX - 1 only, issued LX + 1 blocks earlier. */
-template <int NP, bool TWO>
-__device__ __forceinline__ void g53_grp_block(g53_v16f (&acc)[2], const g53_v8i &w0, const g53_v8i &w1,
+template <int NP, int NH>
+__device__ __forceinline__ void g53_grp_block(g53_v16f (&acc)[G53_GRP_NH], const g53_v8i &w0, const g53_v8i &w1,
                                               const uint8_t *xb, int c0b, int c1b)
 {
     const float c0 = __int_as_float(c0b), c1 = __int_as_float(c1b);
-    g53_v16f b0 = {}, b1 = {};
 #pragma unroll
-    for (int p = 0; p < NP; p++) {
+    for (int h = 0; h < NH; h++) {
+        g53_v16f b = {};
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const uint8_t *xp = xb + p * G53_GRP_NT * G53_GRP_XST + s * 32;
-            const g53_v8i x0 = *(const g53_v8i *)xp;
-            b0 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(s ? w1 : w0, x0, b0, 0, 0, 0, 127, 0, 127 - 4 * p);
-            if (TWO) {
-                const g53_v8i x1 = *(const g53_v8i *)(xp + 32 * G53_GRP_XST);
-                b1 = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(s ? w1 : w0, x1, b1, 0, 0, 0, 127, 0,
-                                                                     127 - 4 * p);
+        for (int p = 0; p < NP; p++) {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const g53_v8i x = *(const g53_v8i *)(xb + p * G53_GRP_NT * G53_GRP_XST + h * 32 * G53_GRP_XST + s * 32);
+                b = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(s ? w1 : w0, x, b, 0, 0, 0, 127, 0, 127 - 4 * p);
             }
         }
-    }
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const float c = r < 8 ? c0 : c1;
-        acc[0][r] = fmaf(b0[r], c, acc[0][r]);
-        if (TWO) acc[1][r] = fmaf(b1[r], c, acc[1][r]);
+        for (int r = 0; r < 16; r++) acc[h][r] = fmaf(b[r], r < 8 ? c0 : c1, acc[h][r]);
+        /* pin the half's arithmetic here: the compiler would otherwise sink the pure matrix
+         * arithmetic past the ring waits to the loop's end and keep every block's operands live */
+        asm volatile("" : "+v"(acc[h]));
     }
-    /* pin the block's arithmetic here: the compiler would otherwise sink the pure matrix
-     * arithmetic past the barriers to the loop's end and keep every block's operands live */
-    asm volatile("" : "+v"(acc[0]));
-    if (TWO) asm volatile("" : "+v"(acc[1]));
 }
 
-/* The activation slice loader of a workgroup of NW waves: a slice is 64 positions x 128 bytes
- * x NP planes, 16-byte pieces; thread t takes piece t % 8 of positions t / 8 + j * 8 * NW. */
+/* LDS counters of the slice ring: relaxed workgroup-scope atomics (a wave's LDS operations
+ * execute in order, so a count added after a wave's slice stores is seen after them), and a
+ * bounded sleep-poll that reports a timeout instead of hanging. */
+#define G53_CBAR() asm volatile("" ::: "memory")
+__device__ __forceinline__ void g53_grp_lds_add(int *p, int v)
+{
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ int g53_grp_wait(int *p, int want)
+{
+    int spins = 0;
+    while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < want) {
+        if (++spins > (1 << 22)) return 1;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    G53_CBAR();
+    return 0;
+}
+
+/* The activation slice loader of a workgroup of NW waves: a slice is G53_GRP_NT positions x
+ * 128 bytes x NP planes, 16-byte pieces; thread t takes piece t % 8 of positions
+ * t / 8 + j * 8 * NW. */
 template <int NW>
 struct G53GrpLd {
-    static constexpr int RPT = 8 / NW;                 /* positions per thread           */
+    static constexpr int RPT = G53_GRP_NT * 8 / (64 * NW);   /* positions per thread    */
     const uint8_t *src[RPT];                           /* source rows (+ 16 * piece)     */
     int dst[RPT];                                      /* LDS offsets in a slice         */
 };
 
-/* acc[h][r] += scale_r * (A_rows x B_tile-half-h) over NKB blocks of 128 bytes.
+/* acc[h][r] += scale_r * (A_rows x B_tile-half-h), h < NH, over NKB blocks of 128 bytes.
  *   arow    this lane's weight row + (l / 32) * 64
  *   s0, s1  scale rows for C registers 0-7 and 8-15 (one float per block)
  *   ld      this thread's slice loader; plane p of a source row at + p * xps
- *   TWO     the tile has more than 32 positions */
-template <int NW, int NP, int NKB, bool TWO>
-__device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[2], const uint8_t *arow, const float *s0,
+ *   NH      32-position halves the tile has (positions beyond the tile's count are padding) */
+template <int NW, int NP, int NKB, int NH>
+__device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const uint8_t *arow, const float *s0,
                                               const float *s1, const G53GrpLd<NW> &ld, size_t xps, uint8_t *xs,
-                                              int lane)
+                                              int *flags, int &spin_err, int lane)
 {
     constexpr int SL = NP * G53_GRP_NT * G53_GRP_XST;           /* one slice in LDS        */
     constexpr int PL = G53_GRP_NT * G53_GRP_XST;                /* one plane of a slice    */
     constexpr int RPT = G53GrpLd<NW>::RPT;
-    constexpr int LX = NW == 8 ? 4 : 2;                         /* slice slots             */
-    constexpr int R0 = NW == 8 ? 8 : 4;                         /* weight slots            */
+    constexpr int LX = G53_GRP_LXS;                             /* slice slots             */
+    constexpr int R0 = G53_GRP_RS;                              /* weight slots            */
     constexpr int R = NKB < R0 ? NKB : R0;
-    static_assert(NKB % R == 0 && R % LX == 0, "ring sizes");
+    constexpr int NS = G53_GRP_NS;                              /* LDS slice slots         */
+    static_assert(NKB % R == 0 && R % LX == 0 && R % NS == 0, "ring sizes");
+    int *ready = flags, *freed = flags + NS;
     static_assert(NKB <= 64, "one scale per lane");
     static_assert(NP == 2 || NP == 3, "two or three planes");
     const uint8_t *xrd = xs + (lane >> 5) * 64 + (lane & 31) * G53_GRP_XST;
@@ -296,8 +324,12 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[2], const uint8_t 
 #pragma unroll
     for (int k = 0; k < R - 1; k++) G53_LDA(k, k);
     G53_STX(0, 0);
-    __syncthreads();
-    /* loads past the end re-read the last block (no branch around a load) */
+    G53_CBAR();
+    if (lane == 0) g53_grp_lds_add(&ready[0], 1);
+    /* Block kb: issue slice kb+LX and weights kb+R-1; store slice kb+1 into its slot once every
+     * wave has finished the block that slot held (freed), and count it ready; wait until every
+     * wave has stored slice kb (ready), multiply, count it freed. No workgroup barrier: waves
+     * drift up to NS-1 blocks apart. Loads past the end re-read the last block. */
 #pragma nounroll
     for (int kb0 = 0; kb0 < NKB; kb0 += R) {
 #pragma unroll
@@ -307,11 +339,19 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[2], const uint8_t 
             const int ka = kb + R - 1 < NKB ? kb + R - 1 : NKB - 1;
             G53_LDX(u % LX, kx);
             G53_LDA((u + R - 1) % R, ka);
-            g53_grp_block<NP, TWO>(acc, a[u][0], a[u][1], xrd + (u & 1) * SL,
+            if (kb + 1 < NKB) {
+                const int sn = (u + 1) % NS;
+                spin_err |= g53_grp_wait(&freed[sn], NW * ((kb + 1) / NS));
+                G53_STX((u + 1) % LX, sn);
+                G53_CBAR();
+                if (lane == 0) g53_grp_lds_add(&ready[sn], 1);
+            }
+            spin_err |= g53_grp_wait(&ready[u % NS], NW * (kb / NS + 1));
+            g53_grp_block<NP, NH>(acc, a[u][0], a[u][1], xrd + (u % NS) * SL,
                                    __builtin_amdgcn_readlane(__float_as_int(sv0), kb),
                                    __builtin_amdgcn_readlane(__float_as_int(sv1), kb));
-            if (kb + 1 < NKB) G53_STX((u + 1) % LX, (u + 1) & 1);
-            __syncthreads();
+            G53_CBAR();
+            if (lane == 0) g53_grp_lds_add(&freed[u % NS], 1);
             __builtin_amdgcn_sched_barrier(0);   /* keep the blocks in program order */
         }
     }
@@ -373,10 +413,11 @@ __device__ __forceinline__ bool g53_grp_item(const int4 *tiles, int ntile, int M
  * rows mb*16*NW + w*16 + 0..15, rows 16-31 = the up rows of the same indices, so C registers r
  * and r + 8 of a lane are gate and up of one intermediate row and one position. */
 template <int NW, int NKB>
-__global__ void __launch_bounds__(64 * NW, 8 / NW) k_grp_gateup(G53GrpArgs a)
+__global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs a)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * G53_GRP_NPX * G53_GRP_NT * G53_GRP_XST];
+    __shared__ __attribute__((aligned(16))) uint8_t xs[G53_GRP_NS * G53_GRP_NPX * G53_GRP_NT * G53_GRP_XST];
     __shared__ uint64_t etab[32];                        /* the exponential's table (LDS) */
+    __shared__ int flags[2 * G53_GRP_NS];
     int4 tl;
     int mb;
     G53_GTRACE(0, __builtin_amdgcn_s_memrealtime());
@@ -406,18 +447,26 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) k_grp_gateup(G53GrpArgs a)
     const uint8_t *arow = m.w + (size_t)(r0 + (i & 15)) * a.E + g * 64;
     const float *s0 = (const float *)ex->gate.s + (size_t)(r0 / 128) * ex->gate.scols;
     const float *s1 = (const float *)ex->up.s + (size_t)(r0 / 128) * ex->up.scols;
-    g53_v16f acc[2] = {{}, {}};
-    /* the token scales of this lane's two positions, loaded before the weights stream */
-    float xi[2];
+    g53_v16f acc[G53_GRP_NH] = {};
+    /* the token scales of this lane's positions, loaded before the weights stream */
+    float xi[G53_GRP_NH];
 #pragma unroll
-    for (int h = 0; h < 2; h++) xi[h] = a.xinv[a.tok_of[pos0 + (h * 32 + i < n ? h * 32 + i : 0)]];
+    for (int h = 0; h < G53_GRP_NH; h++) xi[h] = a.xinv[a.tok_of[pos0 + (h * 32 + i < n ? h * 32 + i : 0)]];
     G53_GTRACE(1, __builtin_amdgcn_s_memrealtime());
-    if (n > 32) g53_grp_kloop<NW, G53_GRP_NPX, NKB, true>(acc, arow, s0, s1, ld, xps, xs, lane);
-    else        g53_grp_kloop<NW, G53_GRP_NPX, NKB, false>(acc, arow, s0, s1, ld, xps, xs, lane);
+    if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
+    __syncthreads();
+    int spin_err = 0;
+    switch ((n + 31) >> 5) {
+    case 1: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 1>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+    case 2: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 2>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+    case 3: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 3>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+    default: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 4>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+    }
+    if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
     G53_GTRACE(2, __builtin_amdgcn_s_memrealtime());
     /* epilogue: SwiGLU and the activation planes */
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < G53_GRP_NH; h++) {
         const int j = h * 32 + i;
         if (j >= n) continue;
         const int pos = pos0 + j;
@@ -443,9 +492,10 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) k_grp_gateup(G53GrpArgs a)
 /* Down for (tile, block mb of 32*NW rows): wave w owns rows mb*32*NW + w*32 + 0..31 of the down
  * matrix (inside one 128-row scale block), the tile's activation planes are the B operand. */
 template <int NW, int NKB>
-__global__ void __launch_bounds__(64 * NW, 8 / NW) k_grp_down(G53GrpArgs a)
+__global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t xs[2 * G53_GRP_NPA * G53_GRP_NT * G53_GRP_XST];
+    __shared__ __attribute__((aligned(16))) uint8_t xs[G53_GRP_NS * G53_GRP_NPA * G53_GRP_NT * G53_GRP_XST];
+    __shared__ int flags[2 * G53_GRP_NS];
     constexpr int MR = 32 * NW;
     int4 tl;
     int mb;
@@ -473,11 +523,19 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) k_grp_down(G53GrpArgs a)
     const int r0 = mb * MR + w * 32;
     const uint8_t *arow = ex->down.w + (size_t)(r0 + i) * a.I + g * 64;
     const float *s0 = (const float *)ex->down.s + (size_t)(r0 / 128) * ex->down.scols;
-    g53_v16f acc[2] = {{}, {}};
-    if (n > 32) g53_grp_kloop<NW, G53_GRP_NPA, NKB, true>(acc, arow, s0, s0, ld, xps, xs, lane);
-    else        g53_grp_kloop<NW, G53_GRP_NPA, NKB, false>(acc, arow, s0, s0, ld, xps, xs, lane);
+    g53_v16f acc[G53_GRP_NH] = {};
+    if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
+    __syncthreads();
+    int spin_err = 0;
+    switch ((n + 31) >> 5) {
+    case 1: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 1>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+    case 2: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 2>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+    case 3: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 3>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+    default: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 4>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+    }
+    if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
+    for (int h = 0; h < G53_GRP_NH; h++) {
         const int j = h * 32 + i;
         if (j >= n) continue;
         float *dst = a.contrib + (size_t)(pos0 + j) * a.E + r0 + g * 4;
