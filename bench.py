@@ -240,11 +240,20 @@ def bench_grouped(a):
         "algorithmic_bytes_per_layer": int(layer_bytes),
         "kernels_us": per,
         "roofline": {"bound": "hbm", "kernel": "k_grp_gateup", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "traffic": _traffic(cfg),
                      "bytes_per_launch": int(gu_bytes), "avg_launch_us": per["k_grp_gateup"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def _traffic(cfg):
+    """HBM bytes per launch of the dominant kernel from the committed counter summary, if any."""
+    tp = os.path.join(ROOT, "profiles", f"k_grp_gateup_config{cfg}_traffic.json")
+    if not os.path.exists(tp):
+        return None
+    with open(tp) as f:
+        return json.load(f).get("traffic_bytes")
 
 
 def _routing(L, layer, xd, T):
