@@ -7,9 +7,12 @@
  *     `landed` event. The bookkeeping publishes the slot when the copies are issued: get()
  *     makes the library's compute stream wait for `landed`, so no host thread blocks on a
  *     read (the reference waits on a condition variable instead);
- *   - release() records the slot's `used` event on the compute stream; a later read into
- *     the slot first waits for `used` (and for the slot's previous `landed`, which may be on
- *     the other copy stream), so a slot is never overwritten while a kernel still reads it;
+ *   - release() records a `used` event on the compute stream (one event for all releases
+ *     between two get() calls: the caller launched the kernels that read those slots before
+ *     releasing them); a later read into the slot first waits for it (and for the slot's
+ *     previous `landed`, which may be on the other copy stream), so a slot is never
+ *     overwritten while a kernel still reads it. A `landed` event seen complete is not
+ *     waited on again;
  *   - prefetch keeps at most n_io expert reads in flight on the prefetch stream; the queue
  *     (ordered by layer, stale entries cancelled by later hints) feeds it whenever the cache is
  *     called and earlier reads have landed.
@@ -39,15 +42,22 @@ struct Geom {                       /* slot layout, from the probe expert */
 
 struct Copy {
     hipEvent_t ev;
-    int layer, expert, background;
+    int layer, expert, background, slot;
+    uint64_t gen;                   /* the slot's read generation this copy filled            */
 };
 
 struct Impl {
     G53hLru lru;
     uint8_t *arena = nullptr;
     Geom geo;
-    std::vector<hipEvent_t> landed, used;
-    std::vector<unsigned char> landed_ok, used_ok;
+    std::vector<hipEvent_t> landed;
+    std::vector<unsigned char> landed_ok;   /* landed[slot] may still be pending            */
+    std::vector<uint64_t> gen;              /* reads issued into each slot                  */
+    std::vector<int> used;                  /* the slot's last release: index into used_ev, -1 */
+    std::vector<hipEvent_t> used_ev;        /* release events, shared by a batch's releases */
+    std::vector<int> used_refs;
+    std::vector<int> used_free;
+    int cur_used = -1;                      /* event recorded since the last get(), or -1   */
     hipStream_t demand = nullptr, prefetch = nullptr;
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
@@ -77,7 +87,17 @@ void sync_stats(Glm53fCache *c, const Impl *m)
     c->bg_used = m->lru.bg_used;
 }
 
-/* Copies seen complete hand their host bytes back to the store. */
+/* Drop a slot's reference to its release event. */
+void unuse(Impl *m, int slot)
+{
+    const int u = m->used[slot];
+    if (u < 0) return;
+    m->used[slot] = -1;
+    if (--m->used_refs[u] == 0 && u != m->cur_used) m->used_free.push_back(u);
+}
+
+/* Copies seen complete hand their host bytes back to the store, and the slot they filled no
+ * longer needs its landed event waited on. */
 void poll(Glm53fCache *c, Impl *m)
 {
     size_t k = 0;
@@ -85,6 +105,7 @@ void poll(Glm53fCache *c, Impl *m)
         Copy &cp = m->inflight[i];
         if (hipEventQuery(cp.ev) == hipSuccess) {
             if (c->st->done) c->st->done(c->st, cp.layer, cp.expert);
+            if (m->gen[cp.slot] == cp.gen) m->landed_ok[cp.slot] = 0;
             m->pool.push_back(cp.ev);
         } else {
             m->inflight[k++] = cp;
@@ -114,7 +135,10 @@ int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t 
             return 0;
         }
     uint8_t *base = m->arena + (size_t)slot * (size_t)c->slot_bytes;
-    if (m->used_ok[slot] && hipStreamWaitEvent(s, m->used[slot], 0) != hipSuccess) return 0;
+    if (m->used[slot] >= 0) {
+        if (hipStreamWaitEvent(s, m->used_ev[m->used[slot]], 0) != hipSuccess) return 0;
+        unuse(m, slot);
+    }
     if (m->landed_ok[slot] && hipStreamWaitEvent(s, m->landed[slot], 0) != hipSuccess) return 0;
     for (int i = 0; i < 3; i++) {
         if (hipMemcpyAsync(base + m->geo.off[i], mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
@@ -125,11 +149,12 @@ int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t 
     }
     if (hipEventRecord(m->landed[slot], s) != hipSuccess) return 0;
     m->landed_ok[slot] = 1;
+    m->gen[slot]++;
     hipEvent_t ev;
     if (!m->pool.empty()) { ev = m->pool.back(); m->pool.pop_back(); }
     else if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return 0;
     if (hipEventRecord(ev, s) != hipSuccess) return 0;
-    m->inflight.push_back(Copy{ev, layer, expert, background});
+    m->inflight.push_back(Copy{ev, layer, expert, background, slot, m->gen[slot]});
     return 1;
 }
 
@@ -176,6 +201,8 @@ int cache_get(Glm53fExpertSrc *self, int layer, int expert, Glm53fExpertQ *out)
     const double t0 = now_s();
     std::lock_guard<std::mutex> g(m->mu);
     poll(c, m);
+    if (m->cur_used >= 0 && m->used_refs[m->cur_used] == 0) m->used_free.push_back(m->cur_used);
+    m->cur_used = -1;                 /* kernels launched after this use a later release event */
     int slot = g53_lru_hit(&m->lru, key);
     if (slot < 0) {
         m->lru.misses++;
@@ -221,7 +248,24 @@ void cache_release(Glm53fExpertSrc *self, int layer, int expert)
     std::lock_guard<std::mutex> g(m->mu);
     const int slot = m->lru.slot_of[key];
     if (slot >= 0 && m->lru.pins[slot] > 0) {
-        if (hipEventRecord(m->used[slot], g53h_stream()) == hipSuccess) m->used_ok[slot] = 1;
+        /* one event for all releases between two get() calls: the caller launched the kernels
+         * that read these slots before releasing any of them */
+        if (m->cur_used < 0) {
+            int u;
+            if (!m->used_free.empty()) { u = m->used_free.back(); m->used_free.pop_back(); }
+            else {
+                hipEvent_t e;
+                if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return;
+                u = (int)m->used_ev.size();
+                m->used_ev.push_back(e);
+                m->used_refs.push_back(0);
+            }
+            if (hipEventRecord(m->used_ev[u], g53h_stream()) != hipSuccess) return;
+            m->cur_used = u;
+        }
+        unuse(m, slot);
+        m->used[slot] = m->cur_used;
+        m->used_refs[m->cur_used]++;
         g53_lru_release(&m->lru, key);
     }
     poll(c, m);
@@ -350,13 +394,12 @@ extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53
         return -1;
     }
     m->landed.resize(c->nslot);
-    m->used.resize(c->nslot);
     m->landed_ok.assign(c->nslot, 0);
-    m->used_ok.assign(c->nslot, 0);
+    m->gen.assign(c->nslot, 0);
+    m->used.assign(c->nslot, -1);
     bool ok = true;
     for (int i = 0; i < c->nslot && ok; i++)
-        ok = hipEventCreateWithFlags(&m->landed[i], hipEventDisableTiming) == hipSuccess &&
-             hipEventCreateWithFlags(&m->used[i], hipEventDisableTiming) == hipSuccess;
+        ok = hipEventCreateWithFlags(&m->landed[i], hipEventDisableTiming) == hipSuccess;
     m->demand = g53h_copy_stream();
     ok = ok && hipStreamCreateWithFlags(&m->prefetch, hipStreamNonBlocking) == hipSuccess;
     c->impl = m;
@@ -391,7 +434,7 @@ extern "C" void glm53f_cache_free(Glm53fCache *c)
         (void)hipDeviceSynchronize();
         poll(c, m);
         for (hipEvent_t e : m->landed) if (e) (void)hipEventDestroy(e);
-        for (hipEvent_t e : m->used) if (e) (void)hipEventDestroy(e);
+        for (hipEvent_t e : m->used_ev) (void)hipEventDestroy(e);
         for (hipEvent_t e : m->pool) (void)hipEventDestroy(e);
         for (Copy &cp : m->inflight) (void)hipEventDestroy(cp.ev);
         if (m->prefetch) (void)hipStreamDestroy(m->prefetch);

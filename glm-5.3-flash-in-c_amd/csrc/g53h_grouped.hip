@@ -248,6 +248,14 @@ __device__ __forceinline__ void g53_grp_block(g53_v16f (&acc)[G53_GRP_NH], const
     }
 }
 
+#ifdef G53_GRP_KTRACE
+__device__ uint64_t *g53_ktrace;     /* diagnostic builds only: per-block timestamps */
+extern "C" int g53h_set_grouped_ktrace(void *p)
+{
+    return hipMemcpyToSymbol(HIP_SYMBOL(g53_ktrace), &p, sizeof p) == hipSuccess ? 0 : -1;
+}
+#endif
+
 /* LDS counters of the slice ring: relaxed workgroup-scope atomics (a wave's LDS operations
  * execute in order, so a count added after a wave's slice stores is seen after them), and a
  * bounded sleep-poll that reports a timeout instead of hanging. */
@@ -337,6 +345,9 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const
             const int kb = kb0 + u;
             const int kx = kb + LX < NKB ? kb + LX : NKB - 1;
             const int ka = kb + R - 1 < NKB ? kb + R - 1 : NKB - 1;
+#ifdef G53_GRP_KTRACE
+            uint64_t kt0 = __builtin_amdgcn_s_memrealtime(), kt1 = 0, kt2 = 0;
+#endif
             G53_LDX(u % LX, kx);
             G53_LDA((u + R - 1) % R, ka);
             if (kb + 1 < NKB) {
@@ -346,12 +357,24 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const
                 G53_CBAR();
                 if (lane == 0) g53_grp_lds_add(&ready[sn], 1);
             }
+#ifdef G53_GRP_KTRACE
+            kt1 = __builtin_amdgcn_s_memrealtime();
+#endif
             spin_err |= g53_grp_wait(&ready[u % NS], NW * (kb / NS + 1));
+#ifdef G53_GRP_KTRACE
+            kt2 = __builtin_amdgcn_s_memrealtime();
+#endif
             g53_grp_block<NP, NH>(acc, a[u][0], a[u][1], xrd + (u % NS) * SL,
                                    __builtin_amdgcn_readlane(__float_as_int(sv0), kb),
                                    __builtin_amdgcn_readlane(__float_as_int(sv1), kb));
             G53_CBAR();
             if (lane == 0) g53_grp_lds_add(&freed[u % NS], 1);
+#ifdef G53_GRP_KTRACE
+            if (g53_ktrace && lane == 0 && NKB == 32) {   /* the gate/up kernel */
+                uint64_t *o = g53_ktrace + (((size_t)blockIdx.x * NW + (threadIdx.x >> 6)) * 32 + kb) * 4;
+                o[0] = kt0; o[1] = kt1; o[2] = kt2; o[3] = __builtin_amdgcn_s_memrealtime();
+            }
+#endif
             __builtin_amdgcn_sched_barrier(0);   /* keep the blocks in program order */
         }
     }

@@ -163,12 +163,14 @@ __global__ void __launch_bounds__(64) k_router_scores(float *__restrict__ score,
 
 /* The same scores for many tokens on the FP64 matrix cores (v_mfma_f64_16x16x4f64). Every
  * product (double)bf16 * (double)x is exact in double, as in k_router_scores; the instruction
- * adds them with double FMAs. Wave w of a workgroup computes the 16 x 16 tile of experts
- * e0 = 64 * blockIdx.x + 16 * w .. +15 and tokens t0 = 16 * blockIdx.y .. +15. Operands: lane l
- * gives A[l % 16][l / 16] (an expert's weight) and B[l / 16][l % 16] (a token's x); step s of
- * a 256-column chunk uses column 64 * (l / 16) + s, so each lane reads 128 consecutive router
- * bytes per chunk. Result: lane l, register r holds C[4 * r + l / 16][l % 16]. x chunks are
- * staged in LDS. bf16 router rows, E a multiple of 256. */
+ * adds them with double FMAs, in an order of its own. A workgroup computes the 16 x 16 tile of
+ * experts e0 = 16 * blockIdx.x .. +15 and tokens t0 = 16 * blockIdx.y .. +15; its four waves
+ * split the columns (wave w takes columns 64w .. 64w+63 of every 256-column chunk) and their
+ * partial sums are added in LDS at the end. Operands: lane l gives A[l % 16][l / 16] (an
+ * expert's weight) and B[l / 16][l % 16] (a token's x); step s uses column 64w + 16(l/16) + s
+ * of the chunk, so a lane reads 32 consecutive router bytes per chunk. Result: lane l, register
+ * r holds C[4r + l/16][l % 16]. x chunks are staged in LDS. bf16 router rows, E a multiple of
+ * 256. */
 typedef double g53_v4d __attribute__((ext_vector_type(4)));
 #define G53_RM_XST 260                                  /* LDS floats per token row       */
 __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, float *__restrict__ choice,
@@ -177,17 +179,16 @@ __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, 
                                                      const float *__restrict__ bias, int NE, int E)
 {
     __shared__ __attribute__((aligned(16))) float xs[16 * G53_RM_XST];
+    __shared__ g53_v4d part[3][64];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 64 + w * 16;
+    const int t0 = blockIdx.y * 16, e0 = blockIdx.x * 16;
     const int i = lane & 15, g = lane >> 4;
     const int er = e0 + i < NE ? e0 + i : NE - 1;          /* rows past NE: discarded       */
-    const uint16_t *wrow = gate + (size_t)er * E + g * 64;
-    const float *xl = xs + i * G53_RM_XST + g * 64;
+    const uint16_t *wrow = gate + (size_t)er * E + w * 64 + g * 16;
+    const float *xl = xs + i * G53_RM_XST + w * 64 + g * 16;
     g53_v4d acc = {0.0, 0.0, 0.0, 0.0};
     for (int k0 = 0; k0 < E; k0 += 256) {
-        uint4 wv[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) wv[q] = *(const uint4 *)(wrow + k0 + q * 8);
+        const uint4 wv0 = *(const uint4 *)(wrow + k0), wv1 = *(const uint4 *)(wrow + k0 + 8);
         __syncthreads();
         for (int q = threadIdx.x; q < 16 * 64; q += 256) {
             const int tk = q >> 6, c = (q & 63) * 4;
@@ -195,20 +196,18 @@ __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, 
             *(float4 *)(xs + tk * G53_RM_XST + c) = *(const float4 *)(x + (size_t)tt * E + k0 + c);
         }
         __syncthreads();
+        const uint32_t d[8] = {wv0.x, wv0.y, wv0.z, wv0.w, wv1.x, wv1.y, wv1.z, wv1.w};
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const uint32_t d[4] = {wv[q].x, wv[q].y, wv[q].z, wv[q].w};
-            const float4 xa = *(const float4 *)(xl + q * 8), xb = *(const float4 *)(xl + q * 8 + 4);
-            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)g53_bitsf(d[k] << 16), (double)xv[2 * k], acc,
-                                                           0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)g53_bitsf(d[k] & 0xffff0000u),
-                                                           (double)xv[2 * k + 1], acc, 0, 0, 0);
-            }
+        for (int k = 0; k < 8; k++) {
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)g53_bitsf(d[k] << 16), (double)xl[2 * k], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)g53_bitsf(d[k] & 0xffff0000u), (double)xl[2 * k + 1],
+                                                       acc, 0, 0, 0);
         }
     }
+    if (w > 0) part[w - 1][lane] = acc;
+    __syncthreads();
+    if (w > 0) return;
+    acc = acc + part[0][lane] + part[1][lane] + part[2][lane];
     const int t = t0 + i;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -313,7 +312,7 @@ int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate
     if (K < 1 || K > NE || K > GLM53F_MAX_TOPK_DEV) return g53h_fail("g53h_router: topk %d", K);
     float *score = scratch, *choice = scratch + (size_t)T * NE;
     if (T >= 2 && gate_dt == 1 && E % 256 == 0) {           /* batches: the matrix-core form */
-        hipLaunchKernelGGL(k_router_mfma, dim3((NE + 63) / 64, (T + 15) / 16), dim3(256), 0, g53h_stream(), score,
+        hipLaunchKernelGGL(k_router_mfma, dim3((NE + 15) / 16, (T + 15) / 16), dim3(256), 0, g53h_stream(), score,
                            choice, x, T, (const uint16_t *)gate, bias, NE, E);
         G53_LAUNCHED("k_router_mfma");
     } else {

@@ -126,6 +126,14 @@ extern "C" int g53h_h2d(void *dst, const void *src, size_t n)
     return 0;
 }
 
+extern "C" int g53h_h2d_async(void *dst, const void *src, size_t n)
+{
+    if (g53h_ready()) return -1;
+    if (!n) return 0;
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_stream));
+    return 0;
+}
+
 extern "C" int g53h_d2h(void *dst, const void *src, size_t n)
 {
     if (g53h_ready()) return -1;

@@ -17,7 +17,7 @@ import os
 import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_DIR, "lib", "libglm53h.so")
+LIB_PATH = os.environ.get("G53H_LIB") or os.path.join(PKG_DIR, "lib", "libglm53h.so")
 INCLUDE_DIR = os.path.join(os.path.dirname(PKG_DIR), "include")
 
 _lib = None
@@ -129,6 +129,7 @@ _SIGS = {
     "g53h_h2d": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_d2h": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_d2d": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "g53h_h2d_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_memset": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t]),
     "g53h_is_device_ptr": (C.c_int, [C.c_void_p]),
     "g53h_mark": (C.c_int, []),

@@ -397,6 +397,120 @@ static int predict_next(int *pred, const float *x_host, const float *xd, const G
     return no;
 }
 
+/* Single-token decode with experts served from the HBM cache: the reference's protocol
+ * (route, hint own then next-layer experts, get, multiply, release; src/core/glm53f_ops.c:
+ * 1169-1342) with two host round trips. x goes up through pinned memory without a wait; the
+ * routing, the next-layer prediction and the NaN flag come back in one copy; the routed
+ * experts' cache views go into a pinned descriptor table copied up on the stream; the layer
+ * then runs as g53h_moe at T = 1 (the fused decode kernels at the released shapes), whose own
+ * routing is the same bit-exact routing and reads only the table entries filled here (the
+ * others are zero, so a different choice would contribute nothing and raise the decode error
+ * flag, never read a stale slot); release() orders each slot's reuse after these kernels.
+ * Returns 0 when done, 1 when the general path must take the call (an expert failed to load). */
+static void *g_pin_x, *g_pin_tab;
+static size_t g_pin_x_n, g_pin_tab_n;
+
+static void *pinned(void **p, size_t *have, size_t n)
+{
+    if (n <= *have) return *p;
+    if (*p && (g53h_sync() || g53h_host_free(*p))) g53_die("freeing pinned staging");
+    *p = g53h_host_alloc(n);
+    if (!*p) g53_die("allocating pinned staging");
+    *have = n;
+    return *p;
+}
+
+static int decode_cached(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int with_shared)
+{
+    const int E = c->hidden, K = c->topk, NE = c->n_experts;
+    Glm53fExpertSrc *src = w->src;
+    /* x up, no wait (the copy below waits for the stream) */
+    float *xd = (float *)x;
+    if (!g53h_is_device_ptr(x)) {
+        float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, (size_t)E * sizeof(float));
+        memcpy(xp, x, (size_t)E * sizeof(float));
+        xd = (float *)buf_get(&g_xin, (size_t)E * sizeof(float));
+        if (g53h_h2d_async(xd, xp, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
+    }
+    /* routing, prediction and flag in one device buffer, read back with one copy */
+    const int per_max = 2 * GLM53F_MAX_TOPK;
+    int *rd = (int *)buf_get(&g_pred, (size_t)(2 * K + per_max + 1) * sizeof(int));
+    int *idx_d = rd, *flag_d = rd + K, *pred_d = rd + K + 1;
+    float *w_d = (float *)buf_get(&g_w, (size_t)K * sizeof(float));
+    int dt = 0;
+    const void *gate = resident_router(w->gate, (size_t)NE * E, &dt);
+    const float *bias = (const float *)resident(w->bias, (size_t)NE * sizeof(float));
+    if (g53h_memset(flag_d, 0, sizeof(int)) ||
+        g53h_router(idx_d, w_d, xd, 1, gate, dt, bias, NE, E, K, c->norm_topk, c->routed_scale, flag_d))
+        g53_die("glm53f_router");
+    const int prefetch = w->prefetch_n > 0 && src->hint != NULL;
+    int per = 0;
+    if (prefetch && w->next_gate) {
+        per = w->prefetch_n < per_max ? w->prefetch_n : per_max;
+        int ndt = 0;
+        const void *ngate = resident_router(w->next_gate, (size_t)NE * E, &ndt);
+        const float *nbias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
+        if (g53h_route_topn(pred_d, per, xd, ngate, ndt, nbias, NE, E)) g53_die("next-layer prediction");
+    }
+    int back[2 * GLM53F_MAX_TOPK + GLM53F_MAX_TOPK + 1];
+    if (g53h_d2h(back, rd, (size_t)(K + 1 + per) * sizeof(int))) g53_die("glm53f_moe routing");
+    if (back[K]) {
+        fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) found no candidate\n");
+        abort();
+    }
+    const int *ids = back;
+    if (prefetch) {
+        src->hint(src, w->layer, ids, K);
+        if (per > 0) src->hint(src, w->layer + 1, back + K + 1, per);
+    }
+    /* the routed experts' views into a zeroed pinned table; the shared expert at [NE] */
+    G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
+    memset(tab, 0, (size_t)(NE + 1) * sizeof(G53hExpert));
+    int held[GLM53F_MAX_TOPK], nh = 0;
+    for (int j = 0; j < K; j++) {
+        Glm53fExpertQ q;
+        memset(&q, 0, sizeof q);
+        if (src->get(src, w->layer, ids[j], &q) != 0) {          /* a drop: the general path */
+            for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
+            return 1;
+        }
+        held[nh++] = ids[j];
+        check_expert_shape(&q, c, w->layer, ids[j]);
+        tab[ids[j]].gate = view_mat_f8(&q.gate);
+        tab[ids[j]].up = view_mat_f8(&q.up);
+        tab[ids[j]].down = view_mat_f8(&q.down);
+    }
+    int block_c = 128;
+    for (int j = 0; j < K; j++) {
+        const G53hExpert *e = &tab[ids[j]];
+        if (e->gate.bc != 128 || e->up.bc != 128 || e->down.bc != 128) block_c = 0;
+    }
+    if (with_shared) {
+        tab[NE].gate = dev_mat_resident(&w->sh_gate, "shared gate");
+        tab[NE].up = dev_mat_resident(&w->sh_up, "shared up");
+        tab[NE].down = dev_mat_resident(&w->sh_down, "shared down");
+        if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128) block_c = 0;
+    }
+    G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
+    if (g53h_h2d_async(tab_d, tab, (size_t)(NE + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
+    G53hMoeLayer L;
+    memset(&L, 0, sizeof L);
+    L.hidden = E; L.inter = c->moe_inter; L.n_experts = NE; L.topk = K; L.norm_topk = c->norm_topk;
+    L.routed_scale = c->routed_scale; L.swiglu_limit = c->swiglu_limit;
+    L.router = gate; L.router_dt = dt; L.bias = bias;
+    L.experts = tab_d; L.shared = with_shared ? tab_d + NE : NULL; L.block_c = block_c;
+    const int odev = g53h_is_device_ptr(out);
+    float *od = odev ? out : (float *)buf_get(&g_out, (size_t)E * sizeof(float));
+    if (g53h_moe(od, xd, 1, &L, NULL, NULL)) g53_die("glm53f_moe");
+    for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
+    if (!odev) {
+        if (g53h_d2h(out, od, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
+    } else if (g53h_sync()) {
+        g53_die("glm53f_moe");
+    }
+    return 0;
+}
+
 static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T,
                      int with_shared)
 {
@@ -407,6 +521,7 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
         fprintf(stderr, "glm53f: FATAL, routed experts is %d, above the limit of 1024.\n", NE);
         abort();
     }
+    if (T == 1 && g53h_cache_is(w->src) && decode_cached(out, x, w, c, with_shared) == 0) return;
     const float *xd = stage_in(&g_xin, x, (size_t)T * E);
     int *idx_d = (int *)buf_get(&g_idx, (size_t)T * K * sizeof(int));
     float *w_d = (float *)buf_get(&g_w, (size_t)T * K * sizeof(float));

@@ -30,6 +30,9 @@ int         g53h_host_free(void *p);
 int         g53h_h2d(void *dst_d, const void *src_h, size_t bytes);   /* synchronous */
 int         g53h_d2h(void *dst_h, const void *src_d, size_t bytes);   /* synchronous */
 int         g53h_d2d(void *dst_d, const void *src_d, size_t bytes);   /* stream-ordered */
+/* Stream-ordered copy to HBM; src must stay unchanged until the stream has passed the copy
+ * (pinned host memory makes it asynchronous). */
+int         g53h_h2d_async(void *dst_d, const void *src_h, size_t bytes);
 int         g53h_memset(void *dst_d, int value, size_t bytes);        /* stream-ordered */
 int         g53h_is_device_ptr(const void *p);   /* 1 = HBM of a device, 0 = host      */
 /* Timing on the compute stream: the elapsed time between the two most recent marks. */

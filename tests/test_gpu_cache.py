@@ -183,3 +183,77 @@ def test_cache_rejects_int4_and_tiny_budgets(L):
     sb = probe.slot_bytes
     L.glm53f_cache_free(C.byref(probe))
     assert L.glm53f_cache_init(C.byref(c), C.byref(store.st), C.byref(cf), sb * sp.K, 0, 0) == -1   # < topk+1
+
+
+class PoolSrc:
+    """A host-memory Glm53fExpertSrc serving the synthetic store's bytes: expert (L, e) is
+    synthetic expert (L * n_experts + e) % n_pool."""
+
+    def __init__(self, sp, pool):
+        self.sp, self.pool = sp, pool
+        self.src = glm53h.Glm53fExpertSrc()
+        self._get = glm53h.GET_FN(self.get)
+        self._rel = glm53h.RELEASE_FN(lambda *a: None)
+        self.src.get, self.src.release = self._get, self._rel
+
+    def get(self, selfp, layer, e, q):
+        sp = self.sp
+        (gw, gs), (uw, us), (dw, ds) = self.pool[(layer * sp.NE + e) % len(self.pool)]
+        q[0].gate, q[0].up = fmat(gw, gs, sp.I, sp.E, sp.br, sp.bc), fmat(uw, us, sp.I, sp.E, sp.br, sp.bc)
+        q[0].down = fmat(dw, ds, sp.E, sp.I, sp.br, sp.bc)
+        return 0
+
+
+def test_cache_config2_decode_through_fused_kernels(L):
+    """Released shapes: two layers, four tokens each, through the cache (the drop-in's cached
+    single-token path: one read-back of routing and prediction, the fused decode kernels on
+    cache slots), bit-identical to the same experts served from host memory (the drop-in's
+    general path)."""
+    sp = S.spec(2)
+    NP = 12
+    cf = make_cfg(sp)
+    cf.n_layers = 2
+    pool = [S.expert_host(sp, p) for p in range(NP)]
+    W = [S.router_host(S.spec(2, layer=l)) for l in range(2)]
+    B = [S.bias_host(S.spec(2, layer=l)) for l in range(2)]
+    sh = S.expert_host(sp, "shared")
+    x = S.x_host(sp, 4, batch=7)
+
+    def run(src, pf):
+        outs = []
+        for t in range(4):
+            for l in range(2):
+                w = glm53h.Glm53fMoeW()
+                w.gate, w.bias = W[l].ctypes.data, B[l].ctypes.data
+                (gw, gs), (uw, us), (dw, ds) = sh
+                w.sh_gate = fmat(gw, gs, sp.I, sp.E, sp.br, sp.bc)
+                w.sh_up = fmat(uw, us, sp.I, sp.E, sp.br, sp.bc)
+                w.sh_down = fmat(dw, ds, sp.E, sp.I, sp.br, sp.bc)
+                w.src = C.pointer(src)
+                w.layer, w.prefetch_n = l, pf
+                if pf and l == 0:
+                    w.next_gate, w.next_bias = W[1].ctypes.data, B[1].ctypes.data
+                out = np.zeros((1, sp.E), np.float32)
+                xt = np.ascontiguousarray(x[t:t + 1])
+                L.glm53f_moe(out.ctypes.data, xt.ctypes.data, C.byref(w), C.byref(cf), 1, None)
+                outs.append(out[0])
+        return np.asarray(outs)
+
+    say("config 2 through host memory (general path)")
+    host = PoolSrc(sp, pool)
+    want = run(host.src, 0)
+    st = glm53h.Glm53fSt()
+    check(L.g53h_store_synth_init(C.byref(st), sp.E, sp.I, 3, sp.NE, NP, sp.seed, C.c_float(sp.expert_sigma)), "store")
+    try:
+        for slots, n_io, pf in [(sp.K + 1, 0, 0), (12, 2, 6)]:
+            say("config 2 through the cache: slots", slots, "prefetch", n_io, pf)
+            c = new_cache(cf, st, slots, n_io)
+            try:
+                got = run(c.src, pf)
+                assert L.g53h_decode_errors() == 0
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+                assert c.hits + c.misses == 4 * 2 * sp.K
+            finally:
+                L.glm53f_cache_free(C.byref(c))
+    finally:
+        L.g53h_store_synth_free(C.byref(st))
