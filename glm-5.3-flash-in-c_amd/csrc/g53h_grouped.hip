@@ -406,6 +406,8 @@ struct G53GrpArgs {
     float *contrib;                /* [P][E]                                             */
     int T, P, E, I, NE;
     float limit, aq_scale, aq_inv;
+    int partial;                   /* 1: experts without weights are outside this batch and
+                                      left alone, unless marked dropped (gate.pad_ == 1)    */
     uint64_t *trace;               /* optional: [grid][8] timestamps of each workgroup    */
 };
 
@@ -448,7 +450,7 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
     if (threadIdx.x < 32) etab[threadIdx.x] = g53_exp2_tab_dev[threadIdx.x];
     G53_GTRACE(4, (uint64_t)__smid() << 32 | (uint32_t)(tl.y << 8 | tl.z));
     const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
-    if (ex->gate.w == nullptr) return;                   /* absent expert: down writes zeros */
+    if (!ex || ex->gate.w == nullptr) return;            /* absent expert: down writes zeros */
     if (!g53_grp_desc_ok(*ex, a.E, a.I)) {
         if (threadIdx.x == 0) atomicOr(&a.meta_w[1], G53_GRP_EDESC);
         return;
@@ -527,7 +529,9 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n = tl.z, pos0 = tl.y;
     const int i = lane & 31, g = lane >> 5;
-    const bool ok = ex->gate.w != nullptr && g53_grp_desc_ok(*ex, a.E, a.I);
+    const bool present = ex && ex->gate.w != nullptr;
+    if (!present && a.partial && !(ex && ex->gate.pad_ == G53_DROPPED)) return;   /* another batch */
+    const bool ok = present && g53_grp_desc_ok(*ex, a.E, a.I);
     if (!ok) {                                           /* zero contributions */
         for (int q = tid; q < n * (MR / 4); q += 64 * NW) {
             const int j = q / (MR / 4), c = (q % (MR / 4)) * 4;
@@ -617,10 +621,10 @@ extern "C" int g53h_set_grouped(int mode)
     return prev;
 }
 
-/* The layer shapes this path serves. */
-extern "C" int g53h_grouped_ok(const G53hMoeLayer *L)
+/* The layer shapes this path serves (routing aside). */
+static int g53_grp_shapes_ok(const G53hMoeLayer *L)
 {
-    if (!L || !L->router || !L->bias) return 0;
+    if (!L) return 0;
     const float lim = L->swiglu_limit;
     const int nbe = L->hidden / 128, nbi = L->inter / 128;
     const int pow2 = (nbe & (nbe - 1)) == 0 && (nbi & (nbi - 1)) == 0;
@@ -629,7 +633,14 @@ extern "C" int g53h_grouped_ok(const G53hMoeLayer *L)
            lim < 1.0e4f;
 }
 
+extern "C" int g53h_grouped_ok(const G53hMoeLayer *L)
+{
+    return L && L->router && L->bias && g53_grp_shapes_ok(L);
+}
+
 int g53h_grouped_use(const G53hMoeLayer *L, int T) { return g_grp_mode && T >= 2 && g53h_grouped_ok(L); }
+
+
 
 extern "C" int g53h_grouped_errors(void)
 {
@@ -646,9 +657,17 @@ __global__ void k_grp_errfold(int *err, int *meta)
     if (threadIdx.x == 0) { if (meta[1]) atomicOr(err, meta[1]); meta[0] = 0; meta[1] = 0; }
 }
 
-/* One planning pass over tc <= G53_GRP_MAXT tokens. */
-static int g53_grp_chunk(float *out, const float *x, int tc, const G53hMoeLayer *L, const int *idx,
-                         const float *wts, char *ws, int *meta)
+/* One planning pass of tc <= G53_GRP_MAXT tokens, in three phases: plan (sort, tiles, input
+ * planes), run (the expert GEMMs for the experts present in L->experts / L->shared), combine. */
+struct G53GrpPass {
+    int active, tc, K, hs, maxtiles;
+    int *pos_of, *meta;
+    float *contrib;
+    G53GrpArgs a;
+};
+static G53GrpPass g_pass;
+
+static int g53_grp_plan_pass(const float *x, int tc, const G53hMoeLayer *L, const int *idx, char *ws, int *meta)
 {
     const int E = L->hidden, I = L->inter, K = L->topk, NE = L->n_experts, hs = L->shared ? 1 : 0;
     const int P = tc * K + hs * tc;
@@ -671,17 +690,28 @@ static int g53_grp_chunk(float *out, const float *x, int tc, const G53hMoeLayer 
     hipLaunchKernelGGL(k_grp_xq<G53_GRP_NPX>, dim3(tc), dim3(256), 0, st, x, E, tc, xq, xinv);
     G53_LAUNCHED("k_grp_xq");
     g53h_prof_mark(G53_PROF_GROUPED);
-
     float bound = L->swiglu_limit > 0.28f ? L->swiglu_limit : 0.28f;
     bound *= L->swiglu_limit;
     int ex = 0;
     (void)frexpf(bound, &ex);                      /* |act| <= bound < 2^ex */
-    G53GrpArgs a;
+    G53GrpArgs &a = g_pass.a;
     a.experts = L->experts; a.shared = L->shared; a.tiles = tiles; a.meta = meta; a.meta_w = meta;
     a.tok_of = tok_of; a.xq = xq; a.xinv = xinv; a.aq = aq; a.contrib = contrib;
     a.T = tc; a.P = P; a.E = E; a.I = I; a.NE = NE;
     a.limit = L->swiglu_limit; a.aq_scale = ldexpf(1.0f, 8 - ex); a.aq_inv = ldexpf(1.0f, ex - 8);
+    a.partial = 0;
     a.trace = g_grp_trace;
+    g_pass.active = 1; g_pass.tc = tc; g_pass.K = K; g_pass.hs = hs; g_pass.maxtiles = maxtiles;
+    g_pass.pos_of = pos_of; g_pass.meta = meta; g_pass.contrib = contrib;
+    return 0;
+}
+
+static int g53_grp_run_pass(const G53hExpert *experts, const G53hExpert *shared, int partial)
+{
+    G53GrpArgs &a = g_pass.a;
+    a.experts = experts; a.shared = shared; a.partial = partial;
+    const int E = a.E, I = a.I, maxtiles = g_pass.maxtiles;
+    hipStream_t st = g53h_stream();
     constexpr int NW = G53_GRP_NW;
     const unsigned g1 = (unsigned)((maxtiles * (I / (16 * NW)) + 7) / 8 * 8);
     const unsigned g2 = (unsigned)((maxtiles * (E / (32 * NW))) + 7) / 8 * 8;
@@ -697,14 +727,29 @@ static int g53_grp_chunk(float *out, const float *x, int tc, const G53hMoeLayer 
 #undef G53_DN
     G53_LAUNCHED("k_grp_down");
     g53h_prof_mark(G53_PROF_DOWN);
+    return 0;
+}
+
+static int g53_grp_combine_pass(float *out, const float *wts)
+{
+    hipStream_t st = g53h_stream();
+    const int tc = g_pass.tc, E = g_pass.a.E;
     const long nq = (long)tc * E / 4;
-    hipLaunchKernelGGL(k_grp_combine, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, out, contrib, wts,
-                       pos_of, tc, E, K, hs);
+    hipLaunchKernelGGL(k_grp_combine, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, out, g_pass.contrib, wts,
+                       g_pass.pos_of, tc, E, g_pass.K, g_pass.hs);
     G53_LAUNCHED("k_grp_combine");
-    hipLaunchKernelGGL(k_grp_errfold, dim3(1), dim3(64), 0, st, g_grp_err, meta);
+    hipLaunchKernelGGL(k_grp_errfold, dim3(1), dim3(64), 0, st, g_grp_err, g_pass.meta);
     G53_LAUNCHED("k_grp_errfold");
     g53h_prof_mark(G53_PROF_COMBINE);
+    g_pass.active = 0;
     return 0;
+}
+
+static int g53_grp_chunk(float *out, const float *x, int tc, const G53hMoeLayer *L, const int *idx,
+                         const float *wts, char *ws, int *meta)
+{
+    if (g53_grp_plan_pass(x, tc, L, idx, ws, meta) || g53_grp_run_pass(L->experts, L->shared, 0)) return -1;
+    return g53_grp_combine_pass(out, wts);
 }
 
 /* Workspace of one planning pass of tc tokens. */
@@ -753,4 +798,46 @@ extern "C" int g53h_moe_grouped(float *out, const float *x, int T, const G53hMoe
             return -1;
     }
     return 0;
+}
+
+/* ------------------------------------------------------------- phased entry ---- */
+static int g53_grp_tcmax(int NE)
+{
+    int tcmax = G53_GRP_MASKS / NE * 64;
+    return tcmax > G53_GRP_MAXT ? G53_GRP_MAXT : tcmax;
+}
+
+extern "C" int g53h_grouped_max_tokens(const G53hMoeLayer *L)
+{
+    if (!g_grp_mode || !g53_grp_shapes_ok(L)) return 0;
+    return g53_grp_tcmax(L->n_experts);
+}
+
+extern "C" int g53h_grouped_begin(const float *x, int T, const G53hMoeLayer *L, const int *idx)
+{
+    if (g53h_ready()) return -1;
+    if (!g53_grp_shapes_ok(L)) return g53h_fail("g53h_grouped_begin: layer shapes not supported");
+    if (T < 1 || T > g53_grp_tcmax(L->n_experts)) return g53h_fail("g53h_grouped_begin: T %d", T);
+    if (!g_grp_err) {
+        G53_TRY(hipMalloc((void **)&g_grp_err, 256));
+        G53_TRY(hipMemset(g_grp_err, 0, 256));
+    }
+    char *ws = (char *)g53h_workspace(g53_grp_ws(L, T));
+    if (!ws) return -1;
+    return g53_grp_plan_pass(x, T, L, idx, ws, g_grp_err + 16);
+}
+
+extern "C" int g53h_grouped_batch(const G53hMoeLayer *L)
+{
+    if (!g_pass.active) return g53h_fail("g53h_grouped_batch: no pass begun");
+    if (!L || L->n_experts != g_pass.a.NE || L->hidden != g_pass.a.E || L->inter != g_pass.a.I)
+        return g53h_fail("g53h_grouped_batch: another layer than the pass's");
+    if (L->shared && !g_pass.hs) return g53h_fail("g53h_grouped_batch: the pass was planned without a shared expert");
+    return g53_grp_run_pass(L->experts, L->shared, 1);
+}
+
+extern "C" int g53h_grouped_end(float *out, const float *wts)
+{
+    if (!g_pass.active) return g53h_fail("g53h_grouped_end: no pass begun");
+    return g53_grp_combine_pass(out, wts);
 }

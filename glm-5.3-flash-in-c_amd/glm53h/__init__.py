@@ -155,6 +155,10 @@ _SIGS = {
     "g53h_moe_grouped": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.POINTER(G53hMoeLayer), C.c_void_p,
                                    C.c_void_p]),
     "g53h_set_grouped": (C.c_int, [C.c_int]),
+    "g53h_grouped_max_tokens": (C.c_int, [C.POINTER(G53hMoeLayer)]),
+    "g53h_grouped_begin": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(G53hMoeLayer), C.c_void_p]),
+    "g53h_grouped_batch": (C.c_int, [C.POINTER(G53hMoeLayer)]),
+    "g53h_grouped_end": (C.c_int, [C.c_void_p, C.c_void_p]),
     "g53h_grouped_ok": (C.c_int, [C.POINTER(G53hMoeLayer)]),
     "g53h_grouped_errors": (C.c_int, []),
     "g53h_set_grouped_trace": (C.c_int, [C.c_void_p]),

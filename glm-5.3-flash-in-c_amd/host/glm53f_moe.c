@@ -568,6 +568,15 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
     L.hidden = E; L.inter = c->moe_inter; L.n_experts = NE; L.topk = K; L.norm_topk = c->norm_topk;
     L.routed_scale = c->routed_scale; L.swiglu_limit = c->swiglu_limit;
     L.experts = table_d;
+    L.block_c = 128;
+    /* a chunk of tokens takes the grouped matrix-core kernels when the layer qualifies: every
+     * batch of fetched experts is multiplied for all its tokens at once */
+    const int grouped = T >= 2 && T <= g53h_grouped_max_tokens(&L) && (!with_shared || (w->sh_gate.bc == 128 &&
+                        w->sh_up.bc == 128 && w->sh_down.bc == 128));
+    if (grouped) {                               /* the plan reserves the shared expert's rows */
+        L.shared = with_shared ? table_d + NE : NULL;
+        if (g53h_grouped_begin(xd, T, &L, idx_d)) g53_die("glm53f_moe");
+    }
     int *held = (int *)malloc((size_t)B * sizeof(int));
     if (!held) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
     for (int b0 = 0; b0 < nu || (b0 == 0 && with_shared); b0 += B) {
@@ -614,7 +623,13 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
         }
         if (g53h_h2d(table_d, table, (size_t)NE * sizeof(G53hExpert))) g53_die("glm53f_moe");
         L.block_c = block_c;
-        if (L.shared) {
+        if (grouped) {
+            if (block_c != 128) {
+                fprintf(stderr, "glm53f: FATAL, a routed expert of layer %d has no 128-column blocks\n", w->layer);
+                abort();
+            }
+            if (g53h_grouped_batch(&L)) g53_die("glm53f_moe");
+        } else if (L.shared) {
             if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
         } else {
             /* a layout with the shared slot still has K+1 slots per token */
@@ -638,7 +653,11 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
     L.shared = with_shared ? table_d + NE : NULL;
     const int odev = g53h_is_device_ptr(out);
     float *od = odev ? out : (float *)buf_get(&g_out, (size_t)T * E * sizeof(float));
-    if (g53h_moe_combine(od, contrib, w_d, T, &L)) g53_die("glm53f_moe");
+    if (grouped) {
+        if (g53h_grouped_end(od, w_d)) g53_die("glm53f_moe");
+    } else if (g53h_moe_combine(od, contrib, w_d, T, &L)) {
+        g53_die("glm53f_moe");
+    }
     if (!odev) {
         if (g53h_d2h(out, od, (size_t)T * E * sizeof(float))) g53_die("glm53f_moe");
     } else if (g53h_sync()) {

@@ -132,6 +132,18 @@ int g53h_moe_combine(float *out_d, const float *contrib_d, const float *w_d, int
  * (1: a routed index out of range, 8: an expert descriptor without the 128x128 layout). */
 int g53h_moe_grouped(float *out_d, const float *x_d, int T, const G53hMoeLayer *L, int *idx_d,
                      float *w_d);
+/* The grouped layer in phases, for a host driver that fetches experts in batches (the C
+ * drop-in; replaces the expert loop of src/core/glm53f_ops.c:1240-1340 for a chunk of tokens):
+ * begin plans T <= g53h_grouped_max_tokens(L) tokens with the routing given (idx_d
+ * [T][topk]) and splits x; each batch call multiplies the experts whose descriptors in
+ * L->experts (and L->shared) are present, leaves the others for other batches, and gives zero
+ * contributions to descriptors marked dropped (gate.w == NULL, gate.pad_ == 1); end combines
+ * into out_d with the weights w_d [T][topk]. Between begin and end the library's workspace
+ * holds the pass: no other g53h layer call may run in between (copies may). */
+int g53h_grouped_max_tokens(const G53hMoeLayer *L);   /* 0: the layer's shapes do not qualify */
+int g53h_grouped_begin(const float *x_d, int T, const G53hMoeLayer *L, const int *idx_d);
+int g53h_grouped_batch(const G53hMoeLayer *L);
+int g53h_grouped_end(float *out_d, const float *w_d);
 int g53h_set_grouped(int on);
 int g53h_grouped_ok(const G53hMoeLayer *L);
 int g53h_grouped_errors(void);

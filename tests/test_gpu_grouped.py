@@ -185,3 +185,81 @@ def test_grouped_absent_expert_contributes_zero(L):
     mats[drop] = zero                                  # zero codes and scales: contributions 0
     want, _, _ = O.moe(O.oracle(), x, sp, layer.router_f32, layer.bias_f32, mats, layer.fetch_expert("shared"))
     within(got, want, "absent expert")
+
+
+
+def test_dropin_grouped_batches_vs_exact_and_oracle(L):
+    """The C drop-in glm53f_moe at T >= 2 on grouped-eligible shapes (hidden 512, inter 512, 32
+    experts top-8): the reference's protocol (get, compute and release the routed experts in
+    batches, src/core/glm53f_ops.c:1240-1290) with the grouped kernels run once per batch and
+    one combine at the end. Against the same call on the exact per-token kernels and the
+    oracle, with and without the shared expert, with failing experts, and served from the HBM
+    cache (bit-identical to the host-memory source: the plan does not depend on the batches)."""
+    from test_gpu_cache import new_cache
+    from test_gpu_parity import HostSrc, cfg_struct, dropin_moe, fmat
+
+    sp = S.LayerSpec(**dict(MID, NE=32), shared=True)
+    cf = cfg_struct(dict(E=sp.E, I=sp.I, NE=sp.NE, K=sp.K, routed_scale=sp.routed_scale, norm_topk=sp.norm_topk,
+                         limit=sp.limit, br=sp.br, bc=sp.bc))
+    W, b = S.router_host(sp), S.bias_host(sp)
+    ex = {e: S.expert_host(sp, e) for e in range(sp.NE)}
+    sh = S.expert_host(sp, "shared")
+    T = 48
+    x = S.x_host(sp, T, batch=5)
+
+    def both(shared=True, drop=()):
+        prev = L.g53h_set_grouped(1)
+        try:
+            src = HostSrc(cf, ex, drop)
+            got = dropin_moe(cf, W, b, ex, sh, x, shared=shared, src=src)
+            assert L.g53h_grouped_errors() == 0
+            assert src.max_pinned <= sp.K and sorted(e for e in src.gets if e not in drop) == sorted(src.releases)
+            assert len(set(src.gets)) > sp.K                 # more than one batch of experts
+            L.g53h_set_grouped(0)
+            ref = dropin_moe(cf, W, b, ex, sh, x, drop=drop, shared=shared)
+        finally:
+            L.g53h_set_grouped(prev)
+        return got, ref
+
+    say("drop-in grouped T", T, "with shared")
+    got, ref = both()
+    within(got, ref, "drop-in grouped vs exact")
+    sel = [0, 7, 47]
+    want, _, _ = O.moe(O.oracle(), x[sel], sp, W, b, ex, sh)
+    within(got[sel], want, "drop-in grouped vs oracle")
+    say("drop-in grouped, routed only")
+    got_r, ref_r = both(shared=False)
+    within(got_r, ref_r, "drop-in grouped routed-only vs exact")
+    say("drop-in grouped, experts 3 and 20 failing")
+    got_d, ref_d = both(drop=(3, 20))
+    within(got_d, ref_d, "drop-in grouped with drops vs exact")
+    assert not np.array_equal(got_d, got)
+
+    say("drop-in grouped through the HBM cache")
+    cf.n_layers = 2
+    st = glm53h.Glm53fSt()
+    check(L.g53h_store_synth_init(C.byref(st), sp.E, sp.I, 2, sp.NE, sp.NE, sp.seed, C.c_float(sp.expert_sigma)),
+          "store")
+    w = glm53h.Glm53fMoeW()
+    w.gate, w.bias = W.ctypes.data, b.ctypes.data
+    (gw, gs), (uw, us), (dw, ds) = sh
+    w.sh_gate = fmat(gw, gs, sp.I, sp.E, sp.br, sp.bc)
+    w.sh_up = fmat(uw, us, sp.I, sp.E, sp.br, sp.bc)
+    w.sh_down = fmat(dw, ds, sp.E, sp.I, sp.br, sp.bc)
+    try:
+        for slots in (sp.K + 1, 40):
+            c = new_cache(cf, st, slots, 0)
+            prev = L.g53h_set_grouped(1)
+            try:
+                w.src = C.pointer(c.src)
+                out = np.zeros((T, sp.E), np.float32)
+                L.glm53f_moe(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cf), T, None)
+                assert L.g53h_grouped_errors() == 0
+                say("cache slots", slots, "hits", c.hits, "misses", c.misses)
+                assert np.array_equal(out.view(np.uint32), got.view(np.uint32))
+            finally:
+                L.g53h_set_grouped(prev)
+                L.glm53f_cache_free(C.byref(c))
+    finally:
+        L.glm53f_forget_host_weights()
+        L.g53h_store_synth_free(C.byref(st))
