@@ -10,7 +10,7 @@ that cache either. Inputs are resident in HBM when the timed region starts. Weig
 synthetic (no checkpoint), generated in HBM.
 
 Prints one JSON line: the layer time in microseconds (lower is better), achieved HBM GB/s, the
-roofline of the dominant kernel (k_dec_experts) measured live with HIP events on the library's
+roofline of the layer kernel (k_dec_layer) measured live with HIP events on the library's
 stream, and the reference CPU expert path (compiled from the reference's sources, oracle/_ref)
 timed on this host's cores on a bounded sample of the same workload.
 
@@ -463,8 +463,7 @@ def main():
     cnt = (C.c_int * 8)()
     check(L.g53h_prof_collect(tms, cnt, 8), "collect")
     check(L.g53h_prof_enable(0), "prof")
-    per = {name: (tms[i] / cnt[i] * 1e3 if cnt[i] else None) for i, name in
-           [(1, "k_dec_route_us"), (7, "k_dec_experts_us")]}
+    per = {name: (tms[i] / cnt[i] * 1e3 if cnt[i] else None) for i, name in [(7, "k_dec_layer_us")]}
     errs = L.g53h_decode_errors()
     if errs:
         sys.exit(f"the decode kernels reported error flags {errs}")
@@ -473,13 +472,13 @@ def main():
     router_bytes = sp.NE * sp.E * 2 + sp.NE * 4                           # bf16 router + bias
     layer_bytes = layer.algorithmic_bytes(sp.K) + sp.E * 4 * 2           # + x in, out
     gbps = layer_bytes / (us_layer * 1e-6) / 1e9
-    dom_bytes = (sp.K + 1) * eb                                          # 8 routed + shared expert
-    dom_us = per["k_dec_experts_us"]
+    dom_bytes = (sp.K + 1) * eb + router_bytes                           # router, 8 routed + shared
+    dom_us = per["k_dec_layer_us"]
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
     traffic = None                      # HBM bytes per launch from the committed counter summary
-    tp = os.path.join(ROOT, "profiles", "k_dec_experts_config2_traffic.json")
+    tp = os.path.join(ROOT, "profiles", "k_dec_layer_config2_traffic.json")
     if os.path.exists(tp):
         with open(tp) as f:
             traffic = json.load(f).get("traffic_bytes")
@@ -503,11 +502,9 @@ def main():
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes_per_layer": layer_bytes,
         "kernels_us": {k: (round(v, 2) if v else v) for k, v in per.items()},
-        "roofline": {"bound": "hbm", "kernel": "k_dec_experts", "achieved": round(dom_gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_dec_layer", "achieved": round(dom_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 2),
-                     "router_kernel": {"kernel": "k_dec_route", "bytes_per_launch": router_bytes,
-                                       "avg_launch_us": round(per["k_dec_route_us"], 2)}},
+                     "traffic": traffic, "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 2)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,39 +1,38 @@
-/* g53h_decode.hip - single-token decode of one MoE layer in two launches.
+/* g53h_decode.hip - single-token decode of one MoE layer in one launch (k_dec_layer).
  *
  * The layer (reference src/core/glm53f_ops.c:1144-1342 at T = 1, with the router of
  * :945-976) is cut into work items of one 8 KB step of HBM codes for one wave:
  *
  *   R   one router row (bf16, 8 KB): the score of one expert
  *   G   one (gate row o, up row o) pair of one slot (2 x 4 KB of E4M3 codes) and its SwiGLU
+ *   A   half of one slot's activation vector, copied into LDS
  *   D   four down rows of one slot (4 x 2 KB of codes): four contributions
  *
- * Under a saturated HBM stream every access that crosses from one workgroup to another (an
- * atomic publish, a coherent poll) takes several microseconds, so the layer is arranged to
- * need almost none, and uses the kernel boundary (about 3 us) for the one dependency every
- * workgroup has: the routing.
+ * One workgroup of 12 waves per CU. Every workgroup owns the same share of every slot's gate/up
+ * rows and of every slot's down rows, so the final weighted combine of its rows is local to
+ * it. Its list: its router rows; its shared-expert G items; the shared expert's A and D
+ * items; its G items of every routed slot, slot by slot; then per routed slot its A and D
+ * items. The waves take items from the list through an LDS counter, one ahead: the codes of
+ * the next item are in flight while the current one is multiplied.
  *
- * k_dec_route: the R items and the shared expert's G items, which depend on nothing, dealt
- *   over the grid. The last workgroup to finish (found by a counter after a release fence,
- *   when the GPU is nearly idle) selects the top-k of score + bias and writes the routing
- *   record: indices, weights, and the reference's outputs idx / w.
+ * Codes are read coalesced (each load instruction of a wave covers consecutive bytes) and
+ * the lanes trade 16-byte chunks through LDS so that each holds one 128-column block, the
+ * unit of the reference's arithmetic.
  *
- * k_dec_experts: every workgroup owns the same row groups of every slot's down product and a
- *   share of every slot's gate/up rows, so the final weighted combine is local to it. Its
- *   list runs: the shared expert's D items; then the routed slots' G items slot after slot,
- *   each slot's D items following two slots later (by then the slot's activation vector,
- *   written by all workgroups, is long complete); then the last slots' D items. Its four
- *   waves take items from the list through an LDS counter, one ahead: the codes of the next
- *   item are in flight while the current one is multiplied. Activations of the routed slots
- *   are published as 64-bit words carrying the launch's epoch in their upper half (by an
- *   atomic exchange, which is performed past the writer's L2); the first wave of a workgroup
- *   to claim a D item of a slot copies that vector into LDS with direct global->LDS loads
- *   issued with the item's codes, and checks the epochs when the item is multiplied (stale
- *   values are re-read). The buffers are never cleared: the epoch grows by one per launch.
+ * Two things cross workgroups, both through words tagged with the launch's epoch in their
+ * upper half and published by atomic exchange (performed past the writer's L2); readers load
+ * them coherently and re-read until the tags are current, so nothing is ever cleared and no
+ * intra-launch barrier is needed:
+ *   - the scores: the last wave of every workgroup waits for all of them, selects the top-k,
+ *     and loads the chosen experts' descriptors; meanwhile only a few waves stream (the
+ *     shared expert), so that the routing's loads are not queued behind a saturated memory
+ *     system, and the other waves start the routed slots when it is done;
+ *   - the activations: a slot's A items read what every workgroup's G items wrote, long
+ *     after they were written in the normal case.
  *
  * Arithmetic is the reference's, bit for bit (see g53h_gemv.h). Every wait is bounded: a wait
  * that runs out sets an error flag (read by g53h_decode_errors) and the wave goes on, so the
- * grid always drains. The grid is sized to the occupancy the runtime reports, so every
- * workgroup is resident at once.
+ * grid always drains. The grid is one workgroup per CU, all resident at once.
  */
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -53,12 +52,16 @@
 #define G53_DEC_RPD 4              /* down rows per item                                 */
 #define G53_DEC_NGRP (G53_DEC_E / G53_DEC_RPD)
 #define G53_DEC_MAXRG 4            /* row groups one workgroup owns (grid >= 256)         */
-#define G53_DEC_LAG 3              /* slots between a slot's G items and its D items      */
+#define G53_DEC_NT 768             /* threads of a k_dec_layer workgroup (one per CU)     */
+#define G53_DEC_EARLY 3            /* waves that stream before the routing is known       */
 #define G53_DEC_NENT 3             /* activation copies a workgroup keeps in LDS          */
 #define G53_DEC_ROT 16             /* copies of the tagged activations, used in rotation  */
 #define G53_SPIN_LIMIT (1 << 20)   /* polls before a wait gives up                       */
 
 typedef unsigned long long g53_u64;
+/* 16 bytes of codes in four VGPRs, as a native vector so that the compiler keeps each buffer
+ * whole in registers */
+typedef unsigned g53_u4 __attribute__((ext_vector_type(4)));
 
 /* ---------------------------------------------------------------- helpers ---- */
 __device__ __forceinline__ g53_u64 g53_tag(unsigned epoch, float v)
@@ -126,7 +129,7 @@ __device__ __forceinline__ bool g53_desc_ok(const G53hExpert &e)
 /* Router dot product of one bf16 row (8 KB) whose 128 bytes for this lane are in c[], x in LDS
  * (padded blocks): columns lane*64 .. lane*64+63, every product exact in double, summed in
  * order per lane and then across the wave (the order of g53_router_dot). */
-__device__ __forceinline__ double g53_router_row(const uint4 (&c)[8], const float *xs, int lane)
+__device__ __forceinline__ double g53_router_row(const g53_u4 (&c)[8], const float *xs, int lane)
 {
     double acc = 0.0;
     const uint32_t d[32] = {c[0].x, c[0].y, c[0].z, c[0].w, c[1].x, c[1].y, c[1].z, c[1].w,
@@ -170,7 +173,7 @@ __device__ __forceinline__ double g53_row_sum(double t, double *pt, int lane)
 
 /* One gate/up row pair (lanes 0-31 gate blocks, 32-63 up blocks) with x in LDS: the two row
  * sums in block order and the SwiGLU, valid in lane 0. */
-__device__ __forceinline__ float g53_gateup_pair(const uint4 (&c)[8], float sc, const float *xs, double *pt,
+__device__ __forceinline__ float g53_gateup_pair(const g53_u4 (&c)[8], float sc, const float *xs, double *pt,
                                                  float limit, const uint64_t *etab, int lane)
 {
     const int bb = lane & 31;
@@ -181,119 +184,131 @@ __device__ __forceinline__ float g53_gateup_pair(const uint4 (&c)[8], float sc, 
 }
 
 extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
-extern "C" __device__ unsigned __ockl_wfred_min_u32(unsigned);
-
-/* Top-k of score + bias by one wave (reference src/core/glm53f_ops.c:957-969: K rounds of
- * "first strictly greater" arg-max, so the larger value first, the lower index among equal
- * values, NaN and -inf never), then the weights (:970-975). NV = ceil(NE / 64) values per lane;
- * each round is two wave reductions (the largest value, then the lowest index holding it).
- * The scores and biases are loaded by g53_topk_load first, so that other work can overlap the
- * loads. idx[j] = -1 where no expert could be selected (the reference aborts there; the return
- * value is then nonzero). */
-template <int NV>
-__device__ __forceinline__ void g53_topk_load(const float *score, const float *bias, int NE, float (&scv)[NV],
-                                              float (&bl)[NV], int lane)
-{
-#pragma unroll
-    for (int v = 0; v < NV; v++) {
-        const int e = min(lane + 64 * v, NE - 1);
-        scv[v] = score[e];
-        bl[v] = bias[e];
-    }
-}
-
-template <int NV>
-__device__ __forceinline__ int g53_topk_weights(const float (&scv)[NV], const float (&bl)[NV], int NE, int K,
-                                                int norm_topk, float routed_scale, int *idx, float *wv, int lane)
-{
-    uint32_t key[NV];
-#pragma unroll
-    for (int v = 0; v < NV; v++) {
-        const float ch = scv[v] + bl[v];
-        key[v] = (lane + 64 * v < NE && ch > -INFINITY) ? g53_fkey(ch) : 0u;    /* 0: never chosen */
-    }
-    int bad = 0;
-    for (int j = 0; j < K; j++) {
-        uint32_t m = 0;
-        int mv = 0;
-#pragma unroll
-        for (int v = 0; v < NV; v++)
-            if (key[v] > m) { m = key[v]; mv = v; }        /* strict: the lowest v among equals */
-        const uint32_t g = __ockl_wfred_max_u32(m);
-        if (g == 0) { bad = 1; if (lane == 0) { wv[j] = 0.0f; idx[j] = -1; } continue; }
-        const uint32_t e = __ockl_wfred_min_u32(m == g ? (uint32_t)(lane + 64 * mv) : 0xffffffffu);
-        if ((uint32_t)(lane + 64 * mv) == e && m == g) {  /* the owner of the winner */
-            float sv = 0.0f;
-#pragma unroll
-            for (int v = 0; v < NV; v++)
-                if (v == mv) { key[v] = 0; sv = scv[v]; }
-            wv[j] = sv;
-            idx[j] = (int)e;
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    /* the weights: every lane forms the sum in slot order, lane j divides weight j */
-    float wj = 0.0f;
-    if (lane < K) wj = wv[lane];
-    if (norm_topk) {
-        double s = 0.0;
-        for (int j = 0; j < K; j++) s += (double)wv[j];
-        if (lane < K) wj = (float)((double)wj / (s + 1e-20));
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < K) wv[lane] = wj * routed_scale;
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    return bad;
-}
 
 /* Diagnostics: per-workgroup timestamps (100 MHz) into a.trace when it is set. */
 #define G53_TRACE(k) do { if (a.trace && lane == 0) \
     a.trace[(size_t)blockIdx.x * 32 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 
-/* ------------------------------------------------------------ k_dec_route ---- */
-struct G53RouteArgs {
-    const float *x;
-    const uint16_t *router;        /* bf16 [NE][E]                                       */
-    float *score;                  /* [NE]                                               */
-    int NE;
-    g53_u64 *trace;                /* optional: [grid][32]; slots 9-10 of each workgroup  */
-};
-
-/* The router rows: one wave per row. */
-__global__ void __launch_bounds__(64) k_dec_route(G53RouteArgs a)
+/* ------------------------------------------------------------------ routing ---- */
+/* Top-k of score + bias by one wave (reference src/core/glm53f_ops.c:957-969: K rounds of
+ * "first strictly greater" arg-max, so the larger value first, the lower index among equal
+ * values, NaN and -inf never), then the weights (:970-975). The scores are the tagged words
+ * other workgroups of this launch publish; they are read coherently, and re-read until every
+ * tag carries this launch's epoch. The K-th largest key is found by a binary search over the
+ * keys with wave ballots, then the chosen experts are ranked among themselves. sidx[j] = -1
+ * where fewer than K experts are selectable (the reference aborts there; bit 2 of the error
+ * flags is then set). Returns false when the scores did not all arrive in time. */
+template <int NV>
+__device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float *bias, int NE, int K, int norm_topk,
+                                               float routed_scale, unsigned epoch, int *sidx, float *sw,
+                                               uint32_t *kbuf, int *ebuf, int *err, int lane, g53_u64 &t_seen,
+                                               int &n_polls, g53_u64 &t_tau, g53_u64 &t_rank)
 {
-    __shared__ __attribute__((aligned(16))) float xs[G53_DEC_NBE * G53_PADB];
-    __shared__ uint64_t etab[32];                      /* the exponential's table */
-    const int lane = threadIdx.x;
-    G53_TRACE(9);
-    for (int e = blockIdx.x; e < a.NE; e += gridDim.x) {
-        uint4 c[8];
-        g53_ld_blk(c, (const uint8_t *)(a.router + (size_t)e * G53_DEC_E + lane * 64));
-        if (e == (int)blockIdx.x) {                    /* x into LDS while the row loads */
-            if (lane < 32) etab[lane] = g53_exp2_tab_dev[lane];
-            g53_vec_to_lds_pad<G53_DEC_E, 64>(xs, a.x, lane);
-            __syncthreads();
-        }
-        const double d = g53_router_row(c, xs, lane);
-        if (lane == 0) a.score[e] = g53_sigmoidf_tab((float)d, etab);
+    const __amdgpu_buffer_rsrc_t rs = g53_rsrc(score);
+    float scv[NV];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int e = min(lane + 64 * v, NE - 1);
+        const g53_u64 t = g53_ld_coh64(rs, 8 * e);
+        scv[v] = __uint_as_float((uint32_t)t);
+        if ((unsigned)(t >> 32) != epoch) pend |= 1u << v;
     }
-    G53_TRACE(10);
+    int spins = 0;
+    while (__ballot(pend != 0)) {
+        if (++spins > G53_SPIN_LIMIT) return false;
+        n_polls++;
+        __builtin_amdgcn_s_sleep(2);
+        g53_u64 t[NV];                                    /* every load in flight at once */
+#pragma unroll
+        for (int v = 0; v < NV; v++) t[v] = g53_ld_coh64(rs, 8 * min(lane + 64 * v, NE - 1));
+#pragma unroll
+        for (int v = 0; v < NV; v++)
+            if ((pend & (1u << v)) && (unsigned)(t[v] >> 32) == epoch) {
+                scv[v] = __uint_as_float((uint32_t)t[v]);
+                pend &= ~(1u << v);
+            }
+    }
+    t_seen = __builtin_amdgcn_s_memrealtime();
+    uint32_t key[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int e = lane + 64 * v;
+        const float ch = e < NE ? scv[v] + bias[e] : -INFINITY;
+        key[v] = (ch > -INFINITY) ? g53_fkey(ch) : 0u;    /* 0: never chosen */
+    }
+    /* K rounds of arg-max: each lane keeps the largest of its remaining keys (the lowest v
+     * among equals, so the lowest expert index of the lane); the wave maximum picks the round's
+     * key and, among lanes holding it, the lowest expert index wins */
+    uint32_t lm = 0;
+    int lv = 0;
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+        if (key[v] > lm) { lm = key[v]; lv = v; }
+    int pos = 0;
+    for (int j = 0; j < K; j++) {
+        const uint32_t m = __ockl_wfred_max_u32(lm);
+        if (m == 0) break;                                /* fewer than K selectable */
+        const uint64_t cand = __ballot(lm == m);
+        int win;
+        if (__popcll(cand) == 1) {
+            win = (int)__builtin_ctzll(cand);
+        } else {                                          /* equal keys: the lowest index */
+            const uint32_t ix = __ockl_wfred_min_u32(lm == m ? (uint32_t)(lane + 64 * lv) : 0xffffffffu);
+            win = (int)(ix & 63);
+        }
+        const int wv = __builtin_amdgcn_readlane(lv, win);
+        float wsc = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NV; v++) if (v == wv) wsc = scv[v];
+        wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wsc), win));
+        if (lane == 0) { sidx[j] = win + 64 * wv; sw[j] = wsc; }
+        if (lane == win) {                                /* the winner drops the key */
+#pragma unroll
+            for (int v = 0; v < NV; v++) if (v == wv) key[v] = 0u;
+            lm = 0;
+            lv = 0;
+#pragma unroll
+            for (int v = 0; v < NV; v++)
+                if (key[v] > lm) { lm = key[v]; lv = v; }
+        }
+        pos++;
+    }
+    t_tau = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0)
+        for (int j = pos; j < K; j++) { sidx[j] = -1; sw[j] = 0.0f; }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    t_rank = __builtin_amdgcn_s_memrealtime();
+    /* the weights: every lane forms the sum in slot order, lane j divides weight j */
+    float wj = 0.0f;
+    if (lane < K) wj = sw[lane];
+    if (norm_topk) {
+        double sum = 0.0;
+        for (int q = 0; q < K; q++) sum += (double)sw[q];
+        if (lane < K) wj = (float)((double)wj / (sum + 1e-20));
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < K) sw[lane] = wj * routed_scale;
+    if (pos < K && lane == 0) g53_flag_err(err, 2);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    return true;
 }
 
-/* ---------------------------------------------------------- k_dec_experts ---- */
-struct G53ExpertsArgs {
+/* --------------------------------------------------------------- k_dec_layer ---- */
+struct G53LayerArgs {
     float *out;
     const float *x;
+    const uint16_t *router;        /* bf16 [NE][E]                                       */
+    const float *bias;
     const G53hExpert *experts;
     const G53hExpert *shared;
-    const float *score;            /* [NE] written by k_dec_route                        */
-    const float *bias;
+    g53_u64 *score;                /* [NE] tagged scores                                 */
     g53_u64 *act;                  /* [MAXK + 1][I] tagged activations, slot K = shared  */
     int *err;
-    int *idx_out;                  /* the routing, written by workgroup 0 (may be NULL)   */
+    int *idx_out;                  /* the routing for the caller (may be NULL)            */
     float *w_out;
     int NE, K, norm_topk;
     unsigned epoch;
@@ -301,64 +316,76 @@ struct G53ExpertsArgs {
     g53_u64 *trace;                /* optional: [grid][32] timestamps and counters       */
 };
 
-enum { G53_IT_NONE = 0, G53_IT_G = 2, G53_IT_D = 3, G53_IT_A = 4 };
+enum { G53_IT_NONE = 0, G53_IT_R = 1, G53_IT_G = 2, G53_IT_D = 3, G53_IT_A = 4 };
 
 struct G53Item {
-    int kind, s, r;                /* slot (K = the shared expert), and o / row group / half */
-    int t;                         /* time slot (the order the slots are processed in)   */
+    int kind, s, r;                /* slot (K = the shared expert), and row / o / group / half */
+    int t;                         /* position of the slot in the down phase (0 = shared) */
 };
 
-/* The workgroup's list. Slots are processed in time order: the shared expert (when there is
- * one) first, then routed slots 0 .. K-1. With G_t = rows [g_lo, g_lo + g_n) of time slot t,
- * A_t = the two halves of its activation vector (copied into LDS), D_t = row groups [rg_lo,
- * rg_lo + n_rg) of its down product, L = G53_DEC_LAG:
- *   for t = 0 .. T-1:  [A_{t-L}] [G_t] [D_{t-L}]        then  [A_t][D_t] for t = T-L .. T-1
- * A slot's activations are read L slots after its G items were issued (so they are normally
- * complete), and a slot's A items come one G group ahead of its D items. */
+/* The workgroup's list (workgroup b of G, one per CU):
+ *   R      router rows b, b + G, ... (score of one expert each)
+ *   S      gate/up rows [g_lo, g_lo + g_n) of the shared expert (G items of slot K)
+ *   A A D  the shared expert's activations (two halves into LDS entry 0) and its down row
+ *          groups [rg_lo, rg_lo + n_rg)
+ *   G      gate/up rows [g_lo, g_lo + g_n) of every routed slot, slot by slot
+ *   A A D  per routed slot, in top-k order (entry t % NENT)
+ * Its waves take items in this order through an LDS counter. The last wave first computes
+ * the routing (the top-k, once the scores of every workgroup are in, and the chosen
+ * experts' descriptors), the one dependency on other workgroups at the start; the other
+ * waves meanwhile keep the memory busy with the router and shared-expert rows. By the time a workgroup reaches a slot's A items, every workgroup has
+ * long finished that slot's gate/up rows. */
 struct G53List {
-    int g_lo, g_n, rg_lo, n_rg, n, T;
+    int nR, g_lo, g_n, rg_lo, n_rg, K, hs, i_s, i_sd, i_g, i_rd, n;
 };
 
-__device__ __forceinline__ int g53_tslot(int t, int K, int has_shared)
-{
-    return has_shared ? (t == 0 ? K : t - 1) : t;
-}
-
-__device__ __forceinline__ G53Item g53_item(const G53List &l, int i, int K, int has_shared)
+__device__ __forceinline__ G53Item g53_item(const G53List &l, int i, int b, int G)
 {
     G53Item it{G53_IT_NONE, 0, 0, 0};
-    for (int t = 0; t < l.T; t++) {
-        const int u = t - G53_DEC_LAG;
-        if (u >= 0) {
-            if (i < 2) { it.kind = G53_IT_A; it.t = u; it.s = g53_tslot(u, K, has_shared); it.r = i; return it; }
-            i -= 2;
-        }
-        if (i < l.g_n) { it.kind = G53_IT_G; it.t = t; it.s = g53_tslot(t, K, has_shared); it.r = l.g_lo + i; return it; }
-        i -= l.g_n;
-        if (u >= 0) {
-            if (i < l.n_rg) { it.kind = G53_IT_D; it.t = u; it.s = g53_tslot(u, K, has_shared); it.r = l.rg_lo + i; return it; }
-            i -= l.n_rg;
-        }
+    const int per = 2 + l.n_rg;
+    if (i < l.i_s) { it.kind = G53_IT_R; it.r = b + i * G; return it; }
+    if (i < l.i_sd) { it.kind = G53_IT_G; it.s = l.K; it.t = 0; it.r = l.g_lo + i - l.i_s; return it; }
+    if (i < l.i_g) {
+        const int j = i - l.i_sd;
+        it.s = l.K; it.t = 0;
+        if (j < 2) { it.kind = G53_IT_A; it.r = j; } else { it.kind = G53_IT_D; it.r = l.rg_lo + j - 2; }
+        return it;
     }
-    for (int u = l.T > G53_DEC_LAG ? l.T - G53_DEC_LAG : 0; u < l.T; u++) {
-        if (i < 2) { it.kind = G53_IT_A; it.t = u; it.s = g53_tslot(u, K, has_shared); it.r = i; return it; }
-        i -= 2;
-        if (i < l.n_rg) { it.kind = G53_IT_D; it.t = u; it.s = g53_tslot(u, K, has_shared); it.r = l.rg_lo + i; return it; }
-        i -= l.n_rg;
+    if (i < l.i_rd) {
+        const int j = i - l.i_g;
+        it.kind = G53_IT_G; it.s = j / l.g_n; it.t = it.s + l.hs; it.r = l.g_lo + j % l.g_n;
+        return it;
+    }
+    if (i < l.n) {
+        const int j = i - l.i_rd, q = j % per;
+        it.s = j / per; it.t = it.s + l.hs;
+        if (q < 2) { it.kind = G53_IT_A; it.r = q; } else { it.kind = G53_IT_D; it.r = l.rg_lo + q - 2; }
     }
     return it;
 }
 
-/* Addresses of one item's codes (this lane's 128 bytes) and block scale. Items that read
- * nothing point at the input vector instead, so that the loop issues its loads from one place
- * with no branch around them (a branch makes the compiler wait for the loads where the paths
- * join). Returns whether the item's codes are real. The matrices have 128 x 128 blocks, so
- * the scale row of output row r is r >> 7. */
+/* Addresses of one item's loads and this lane's block scale. Codes are read coalesced: load k
+ * of lane l reads 16 bytes at p + k * stride, so each load instruction of the wave covers
+ * consecutive HBM bytes (a G item: 512 bytes of the gate row from lanes 0-31 and 512 of the
+ * up row from lanes 32-63, stride 512; a D item: 1 KB of its four consecutive rows, stride
+ * 1024), and the lanes then trade 16-byte chunks through LDS so that each holds the 128
+ * bytes of its own block (g53_xpose). A and R items read 128 consecutive bytes per lane
+ * (stride 16).
+ * Items that read nothing point at the input vector instead, so that the loop issues its
+ * loads from one place with no branch around them (a branch makes the compiler wait for the
+ * loads where the paths join). Returns whether the item's codes are real. The matrices have
+ * 128 x 128 blocks, so the scale row of output row r is r >> 7. */
 __device__ __forceinline__ bool g53_addr(const G53Item &it, const G53hExpert *st, const g53_u64 *act,
-                                         const float *dummy, int lane, const uint8_t *&p, const float *&ps)
+                                         const uint16_t *router, const float *dummy, int lane, const uint8_t *&p,
+                                         const float *&ps, int &stride)
 {
     p = (const uint8_t *)dummy + lane * 128;
     ps = dummy;
+    stride = 16;
+    if (it.kind == G53_IT_R) {                /* 64 bf16 weights per lane */
+        p = (const uint8_t *)(router + (size_t)it.r * G53_DEC_E + lane * 64);
+        return true;
+    }
     if (it.kind == G53_IT_A) {                /* 16 tagged activations per lane */
         p = (const uint8_t *)(act + (size_t)it.s * G53_DEC_I + it.r * 1024 + lane * 16);
         return true;
@@ -368,8 +395,9 @@ __device__ __forceinline__ bool g53_addr(const G53Item &it, const G53hExpert *st
         if (!ex.gate.w) return false;
         const G53hMat &m = lane < 32 ? ex.gate : ex.up;
         const int b = lane & 31;
-        p = m.w + (size_t)it.r * G53_DEC_E + b * 128;
+        p = m.w + (size_t)it.r * G53_DEC_E + b * 16;
         ps = m.s + (size_t)(it.r >> 7) * m.scols + b;
+        stride = 512;
         return true;
     }
     if (it.kind == G53_IT_D) {
@@ -377,100 +405,176 @@ __device__ __forceinline__ bool g53_addr(const G53Item &it, const G53hExpert *st
         if (!ex.gate.w) return false;
         const G53hMat &m = ex.down;
         const int b = lane & 15, d = it.r * G53_DEC_RPD + (lane >> 4);
-        p = m.w + (size_t)d * G53_DEC_I + b * 128;
+        p = m.w + (size_t)it.r * G53_DEC_RPD * G53_DEC_I + lane * 16;
         ps = m.s + (size_t)(d >> 7) * m.scols + b;
+        stride = 1024;
         return true;
     }
     return false;
 }
 
-__global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
+/* A use of every register of a code buffer: the compiler then waits for the buffer's loads
+ * here on every path, so that no load into the buffer is still outstanding when the next one
+ * is issued into it (which would otherwise make that issue wait for the other buffer's loads
+ * too, loads completing in order). */
+__device__ __forceinline__ void g53_touch(const g53_u4 (&c)[8], float sc)
+{
+#pragma unroll
+    for (int k = 0; k < 8; k++) asm volatile("" ::"v"(c[k]));
+    asm volatile("" ::"v"(sc));
+}
+
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __attribute__((address_space(1))) const g53_u4 g53_gv4;
+#else
+typedef const g53_u4 g53_gv4;
+#endif
+__device__ __forceinline__ void g53_ld_str(g53_u4 (&c)[8], const uint8_t *p, int stride)
+{
+    g53_gv4 *q = (g53_gv4 *)p;
+    const int st = stride >> 4;
+#pragma unroll
+    for (int k = 0; k < 8; k++) c[k] = q[k * st];
+}
+
+/* The chunk trade of a coalesced G or D item through the wave's 8 KB of LDS. Chunk n (16
+ * bytes) of the item is chunk n % 8 of block n / 8 in the lane order of the block-per-lane
+ * layout (a G item: blocks 0-31 the gate row, 32-63 the up row; a D item: 16 blocks per row,
+ * four rows), stored at chunk position n ^ ((n >> 3) & 15): every 16 lanes of a store (16
+ * consecutive n) and of a load (chunk q of 16 consecutive blocks) then cover all 64 banks. */
+__device__ __forceinline__ void g53_xpose(g53_u4 (&c)[8], g53_u4 *xw, bool gitem, int lane)
+{
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int n = gitem ? ((lane >> 5) * 256 + k * 32 + (lane & 31)) : (k * 64 + lane);
+        xw[n ^ ((n >> 3) & 15)] = c[k];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = 0; q < 8; q++) c[q] = xw[(8 * lane + q) ^ (lane & 15)];
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+}
+
+__global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
 {
     __shared__ __attribute__((aligned(16))) float xs[G53_DEC_NBE * G53_PADB];        /* padded x   */
     __shared__ __attribute__((aligned(16))) float actl[G53_DEC_NENT][G53_DEC_NBI * G53_PADB];
-    __shared__ __attribute__((aligned(16))) double pw[4][64];                         /* row terms  */
+    __shared__ __attribute__((aligned(16))) double pw[G53_DEC_NT / 64][64];           /* row terms  */
+    __shared__ g53_u4 xpw[G53_DEC_NT / 64][512];                                      /* chunk trade */
     __shared__ G53hExpert st[G53_DEC_MAXK + 1];
-    __shared__ float sw[16];
-    __shared__ int sidx[16];
+    __shared__ float biasl[G53_DEC_MAXNE];
+    __shared__ float sw[64];
+    __shared__ int sidx[16], ebuf[64];
+    __shared__ uint32_t kbuf[64];
     __shared__ uint64_t etab[32];                      /* the exponential's table */
     __shared__ float cvals[G53_DEC_MAXRG][G53_DEC_RPD][G53_DEC_MAXK + 1];
-    /* ent_ver[e]: activation halves copied into entry e so far; ent_used[e]: D items done with it */
+    /* ent_ver[e]: activation halves copied into entry e so far; ent_used[e]: D items done with
+     * it; routed: the routing and the routed slots' descriptors are in st[] and sw[] */
     __shared__ int qctr, ndone, routed, ent_ver[G53_DEC_NENT], ent_used[G53_DEC_NENT];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, hs = a.shared ? 1 : 0, nslots = K + hs;
     const int G = gridDim.x, b = blockIdx.x;
 
     G53List l;
-    l.T = nslots;
+    l.K = K;
+    l.hs = hs;
+    l.nR = a.NE > b ? (a.NE - 1 - b) / G + 1 : 0;
     l.g_lo = (int)((long)G53_DEC_I * b / G);
     l.g_n = (int)((long)G53_DEC_I * (b + 1) / G) - l.g_lo;
     l.rg_lo = (int)((long)G53_DEC_NGRP * b / G);
     l.n_rg = (int)((long)G53_DEC_NGRP * (b + 1) / G) - l.rg_lo;
-    l.n = nslots * (l.g_n + 2 + l.n_rg);
+    l.i_s = l.nR;
+    l.i_sd = l.i_s + hs * l.g_n;
+    l.i_g = l.i_sd + hs * (2 + l.n_rg);
+    l.i_rd = l.i_g + K * l.g_n;
+    l.n = l.i_rd + K * (2 + l.n_rg);
     const int ndone_all = nslots * l.n_rg;
 
     G53_TRACE(0);
-    /* routing first, by wave 0: its loads go out before anything else */
-    constexpr int NV = 5;                              /* scores per lane on the fast path */
-    float scv[NV], bl[NV];
-    const bool fast_route = a.NE <= 64 * NV;
-    if (w == 0 && fast_route) g53_topk_load<NV>(a.score, a.bias, a.NE, scv, bl, lane);
-    if (threadIdx.x < (int)(sizeof(G53hExpert) / 4) && a.shared)
-        ((int *)&st[K])[threadIdx.x] = ((const int *)a.shared)[threadIdx.x];
+    const int words = (int)(sizeof(G53hExpert) / 4);
+    if (threadIdx.x < words) ((int *)&st[K])[threadIdx.x] = hs ? ((const int *)a.shared)[threadIdx.x] : 0;
+    for (int e = threadIdx.x; e < a.NE; e += G53_DEC_NT) biasl[e] = a.bias[e];
     if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; }
     if (threadIdx.x < 32) etab[threadIdx.x] = g53_exp2_tab_dev[threadIdx.x];
     if (threadIdx.x < G53_DEC_NENT) { ent_ver[threadIdx.x] = 0; ent_used[threadIdx.x] = 0; }
-    g53_vec_to_lds_pad<G53_DEC_E, 256>(xs, a.x, threadIdx.x);
+    for (int q = threadIdx.x; q < G53_DEC_E / 4; q += G53_DEC_NT) {
+        const float4 v = ((const float4 *)a.x)[q];
+        *(float4 *)(xs + (q >> 5) * G53_PADB + 4 * (q & 31)) = v;
+    }
     __syncthreads();
     if (threadIdx.x == 0 && hs && st[K].gate.w && !g53_desc_ok(st[K])) {
         st[K].gate.w = nullptr;                        /* unusable: flagged, contributes zero */
-        g53_flag_err(a.err, 8);
+        if (b == 0) g53_flag_err(a.err, 8);
     }
-    if (w == 0) {
-        /* the routing: top-k, weights, the routed slots' descriptors; the other waves start on
-         * the shared expert meanwhile */
-        G53_TRACE(11);
-        int bad;
-        if (fast_route) {
-            bad = g53_topk_weights<NV>(scv, bl, a.NE, K, a.norm_topk, a.routed_scale, sidx, sw, lane);
-        } else {
-            float sc16[G53_DEC_MAXNE / 64], b16[G53_DEC_MAXNE / 64];
-            g53_topk_load<G53_DEC_MAXNE / 64>(a.score, a.bias, a.NE, sc16, b16, lane);
-            bad = g53_topk_weights<G53_DEC_MAXNE / 64>(sc16, b16, a.NE, K, a.norm_topk, a.routed_scale, sidx, sw, lane);
-        }
-        if (bad && lane == 0) g53_flag_err(a.err, 2);
-        G53_TRACE(13);
-        if (b == 0 && lane < K) {
-            if (a.idx_out) a.idx_out[lane] = sidx[lane];
-            if (a.w_out) a.w_out[lane] = sw[lane];
-        }
-        const int words = (int)(sizeof(G53hExpert) / 4);
-        for (int q = lane; q < K * words; q += 64) {
-            const int j = q / words, ex = sidx[j];
-            ((int *)st)[q] = (ex >= 0 && ex < a.NE) ? ((const int *)&a.experts[ex])[q % words] : 0;
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
-        if (lane < K && st[lane].gate.w && !g53_desc_ok(st[lane])) {
-            st[lane].gate.w = nullptr;
-            g53_flag_err(a.err, 8);
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
-        G53_CBAR();
-        if (lane == 0) g53_lds_add(&routed, 1);
-        G53_TRACE(14);
-    }
+    __syncthreads();
+    G53_TRACE(8);
 
-    g53_u64 tw_act = 0, tw_comp = 0, n_items = 0, n_stale = 0, n_stale2 = 0;
+    g53_u64 tw_act = 0, tw_comp = 0, n_items = 0, n_stale = 0, n_stale2 = 0, tw_sh = 0, tw_use = 0, tw_d = 0, tw_mem = 0;
     auto claim = [&]() -> int {
         int i = 0;
         if (lane == 0) i = g53_lds_add(&qctr, 1);
         return __builtin_amdgcn_readfirstlane(i);
     };
 
+    /* the routing item: top-k, weights, the chosen experts' descriptors (reference
+     * src/core/glm53f_ops.c:945-976) */
+    auto route = [&]() {
+        G53_TRACE(11);
+        bool ok;
+        g53_u64 t_seen = 0, t_tau = 0, t_rank = 0;
+        int n_polls = 0;
+        if (a.NE <= 64 * 5)
+            ok = g53_route_wave<5>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx, sw, kbuf, ebuf,
+                                   a.err, lane, t_seen, n_polls, t_tau, t_rank);
+        else
+            ok = g53_route_wave<G53_DEC_MAXNE / 64>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx,
+                                                    sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank);
+        if (a.trace && lane == 0) { a.trace[(size_t)blockIdx.x * 32 + 15] = t_seen; a.trace[(size_t)blockIdx.x * 32 + 7] = n_polls; a.trace[(size_t)blockIdx.x * 32 + 1] = t_tau; a.trace[(size_t)blockIdx.x * 32 + 9] = t_rank; }
+        if (!ok) {                                     /* scores missing: no routed slots */
+            if (lane == 0) g53_flag_err(a.err, 1);
+            if (lane < K) { sidx[lane] = -1; sw[lane] = 0.0f; }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+        }
+        G53_TRACE(13);
+        {                                              /* every load in flight at once */
+            constexpr int NQ = (G53_DEC_MAXK * (int)(sizeof(G53hExpert) / 4) + 63) / 64;
+            int dv[NQ];
+#pragma unroll
+            for (int i = 0; i < NQ; i++) {
+                const int q = lane + 64 * i, j = min(q / words, K - 1), ex = sidx[j];
+                dv[i] = (q < K * words && ex >= 0 && ex < a.NE) ? ((const int *)&a.experts[ex])[q % words] : 0;
+            }
+#pragma unroll
+            for (int i = 0; i < NQ; i++)
+                if (lane + 64 * i < K * words) ((int *)st)[lane + 64 * i] = dv[i];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < K && st[lane].gate.w && !g53_desc_ok(st[lane])) {
+            st[lane].gate.w = nullptr;                 /* unusable: flagged, contributes zero */
+            g53_flag_err(a.err, 8);
+        }
+        if (b == 0 && lane < K) {
+            if (a.idx_out) a.idx_out[lane] = sidx[lane];
+            if (a.w_out) a.w_out[lane] = sw[lane];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        G53_CBAR();
+        if (lane == 0) g53_lds_add(&routed, 1);
+        G53_TRACE(14);
+    };
+
     /* multiply one item whose codes are in c[] */
-    auto compute = [&](const G53Item &it, const uint4 (&c)[8], float sc, bool loaded) {
+    auto compute = [&](const G53Item &it, const g53_u4 (&c)[8], float sc, bool loaded) {
+        if (it.kind == G53_IT_R) {
+            const double d = g53_router_row(c, xs, lane);
+            if (lane == 0) g53_st_tag(a.score + it.r, g53_tag(a.epoch, g53_sigmoidf_tab((float)d, etab)));
+            return;
+        }
         if (it.kind == G53_IT_G) {
             if (!loaded) return;                             /* expert not there */
             const float v = g53_gateup_pair(c, sc, xs, pw[w], a.limit, etab, lane);
@@ -494,7 +598,11 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
                 if (c[k].y != a.epoch) pending |= 1u << (2 * k);
                 if (c[k].w != a.epoch) pending |= 1u << (2 * k + 1);
             }
-            if (use > 0 && !g53_wait_lds(&ent_used[e], use * l.n_rg) && lane == 0) g53_flag_err(a.err, 1);
+            if (use > 0 && g53_lds_ld(&ent_used[e]) < use * l.n_rg) {
+                const g53_u64 t0 = __builtin_amdgcn_s_memrealtime();
+                if (!g53_wait_lds(&ent_used[e], use * l.n_rg) && lane == 0) g53_flag_err(a.err, 1);
+                tw_use += __builtin_amdgcn_s_memrealtime() - t0;
+            }
             const int i0 = it.r * 1024 + lane * 16;          /* 16 values within one block */
             float *dst = actl[e] + (i0 >> 7) * G53_PADB + (i0 & 127);
 #pragma unroll
@@ -530,7 +638,8 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
                     if (spins == 1) n_stale2 += __popc(pending);
                     if (__ballot(pending != 0)) g53_backoff();
                 }
-                tw_act += __builtin_amdgcn_s_memrealtime() - t0;
+                if (it.s == K) tw_sh += __builtin_amdgcn_s_memrealtime() - t0;
+                else tw_act += __builtin_amdgcn_s_memrealtime() - t0;
             }
             __builtin_amdgcn_s_waitcnt(0xc07f);
             __builtin_amdgcn_wave_barrier();
@@ -545,7 +654,7 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
             if (g53_lds_ld(&ent_ver[e]) < want) {
                 const g53_u64 t0 = __builtin_amdgcn_s_memrealtime();
                 if (!g53_wait_lds(&ent_ver[e], want) && lane == 0) g53_flag_err(a.err, 1);
-                tw_act += __builtin_amdgcn_s_memrealtime() - t0;
+                tw_d += __builtin_amdgcn_s_memrealtime() - t0;
             }
             const int bb = lane & 15;
             v = (float)g53_row_sum<16>(g53_blk_pad(c, actl[e] + bb * G53_PADB) * (double)sc, pw[w], lane);
@@ -578,57 +687,79 @@ __global__ void __launch_bounds__(256, 2) k_dec_experts(G53ExpertsArgs a)
      * Two code buffers alternate: each half-pass claims an item and issues its loads into the
      * free buffer (from one place, so the compiler keeps them in flight), then multiplies the
      * item in the other buffer. While a wave waits for one item's codes, the next item's are
-     * already on their way. An item that needs the routing waits for it before its loads are
-     * issued (wave 0 computes it while the others work on the shared expert). */
-    uint4 ca[8], cb[8];
-    float sa = 0.0f, sb = 0.0f;
-    bool la, lb;
+     * already on their way. An item of a routed slot waits for the routing before its loads
+     * are issued. */
     auto next_item = [&]() -> G53Item {
-        const int ni = claim();
-        return ni < l.n ? g53_item(l, ni, K, hs) : G53Item{G53_IT_NONE, 0, 0, 0};
+        const int i = claim();
+        G53Item it = i < l.n ? g53_item(l, i, b, G) : G53Item{G53_IT_NONE, 0, 0, 0};
+        /* uniform by construction; said so, so that the loop's branches stay scalar */
+        it.kind = __builtin_amdgcn_readfirstlane(it.kind);
+        it.s = __builtin_amdgcn_readfirstlane(it.s);
+        it.r = __builtin_amdgcn_readfirstlane(it.r);
+        it.t = __builtin_amdgcn_readfirstlane(it.t);
+        return it;
     };
-    auto issue = [&](const G53Item &nt, uint4 (&c)[8], float &scv) -> bool {
-        if ((nt.kind == G53_IT_G || nt.kind == G53_IT_D) && nt.s < K && g53_lds_ld(&routed) == 0) {
+    auto issue = [&](const G53Item &nt, g53_u4 (&c)[8], float &scv) -> bool {
+        if ((nt.kind == G53_IT_G || nt.kind == G53_IT_A || nt.kind == G53_IT_D) && nt.s < K &&
+            g53_lds_ld(&routed) == 0) {
             if (!g53_wait_lds(&routed, 1) && lane == 0) g53_flag_err(a.err, 1);
         }
         const uint8_t *p;
         const float *ps;
-        const bool r = g53_addr(nt, st, a.act, a.x, lane, p, ps);
-        g53_ld_blk(c, p);
+        int stride;
+        const bool r = g53_addr(nt, st, a.act, a.router, a.x, lane, p, ps, stride);
+        g53_ld_str(c, p, stride);
         scv = *(const g53_gf *)ps;
-        return r;
+        return __builtin_amdgcn_readfirstlane((int)r) != 0;   /* uniform: no exec-masked paths */
     };
-    auto run = [&](const G53Item &it, const uint4 (&c)[8], float scv, bool loaded) {
+    auto run = [&](const G53Item &it, g53_u4 (&c)[8], float scv, bool loaded) {
+        const g53_u64 tw0 = __builtin_amdgcn_s_memrealtime();
+        g53_touch(c, scv);
+        if (it.kind == G53_IT_NONE) return;
         const g53_u64 tc0 = __builtin_amdgcn_s_memrealtime();
+        tw_mem += tc0 - tw0;
+        if (loaded && (it.kind == G53_IT_G || it.kind == G53_IT_D)) g53_xpose(c, xpw[w], it.kind == G53_IT_G, lane);
         compute(it, c, scv, loaded);
         tw_comp += __builtin_amdgcn_s_memrealtime() - tc0;
         n_items++;
     };
-    if (w == 0) G53_TRACE(8);
-    G53Item ia = next_item(), ib;
-    la = issue(ia, ca, sa);
-    for (;;) {
-        ib = next_item();
-        lb = issue(ib, cb, sb);
-        if (ia.kind == G53_IT_NONE) break;
+    if (w == G53_DEC_NT / 64 - 1) route();
+    /* only a few waves stream before the routing is known, so that the loads, the
+     * publications and the coherent reads of the routing are not queued behind a saturated
+     * memory system */
+    if (w >= G53_DEC_EARLY && g53_lds_ld(&routed) == 0) {
+        if (!g53_wait_lds(&routed, 1) && lane == 0) g53_flag_err(a.err, 1);
+    }
+    g53_u4 ca[8], cb[8];
+    float sa = 0.0f, sb = 0.0f;
+    G53Item ia = next_item();
+    bool la = issue(ia, ca, sa);
+    G53Item ib = next_item();
+    bool lb = issue(ib, cb, sb);
+    /* One exit, at the top, and no branch around either half: the items are claimed in order,
+     * so once one is none every later one is, and a none item only waits for its (dummy)
+     * loads. Every path through the body then leaves buffer a's loads older than buffer b's,
+     * so the compiler waits for exactly one buffer at a time. */
+    while (ia.kind != G53_IT_NONE) {
         run(ia, ca, sa, la);
         ia = next_item();
         la = issue(ia, ca, sa);
-        if (ib.kind == G53_IT_NONE) break;
         run(ib, cb, sb, lb);
+        ib = next_item();
+        lb = issue(ib, cb, sb);
     }
-    G53_TRACE(2 + w);
-    if (a.trace && lane == 0) {
+    if (w < 4) G53_TRACE(2 + w);
+    if (a.trace && lane == 0 && w < 4) {
         g53_u64 *tr = a.trace + (size_t)blockIdx.x * 32;
-        tr[16 + w] = n_stale; tr[20 + w] = tw_act; tr[6] = n_stale2; tr[24 + w] = tw_comp; tr[28 + w] = n_items;
+        tr[16 + w] = tw_mem; tr[20 + w] = tw_comp; tr[6] = n_stale2; tr[24 + w] = n_items; tr[28 + w] = tw_d + tw_sh + tw_act + tw_use; (void)n_stale;
     }
 }
 
 /* ------------------------------------------------------------------ host side ---- */
-static int g_dec_grid1 = -1;             /* workgroups of k_dec_experts, 0 = unavailable   */
+static int g_dec_grid1 = -1;             /* workgroups of k_dec_layer, 0 = unavailable     */
 static unsigned g_dec_epoch = 0;         /* epoch of the last launch                        */
 static int *g_dec_state = nullptr;       /* [0] error flags                                 */
-static void *g_dec_buf = nullptr;        /* scores | tagged activations                     */
+static void *g_dec_buf = nullptr;        /* tagged scores | tagged activations              */
 static size_t g_dec_buf_bytes = 0;
 static int g_dec_enabled = 1;
 static g53_u64 *g_dec_trace = nullptr;
@@ -660,12 +791,12 @@ int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *id
     const int cus = g53h_num_cus();
     if (g_dec_grid1 < 0) {
         int per = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_dec_experts, 256, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_dec_layer, G53_DEC_NT, 0) != hipSuccess ||
             per < 1) {
             (void)hipGetLastError();
             g_dec_grid1 = 0;
         } else {
-            g_dec_grid1 = (per > 2 ? 2 : per) * cus;
+            g_dec_grid1 = cus;
             /* every workgroup owns at most G53_DEC_MAXRG row groups */
             if ((G53_DEC_NGRP + g_dec_grid1 - 1) / g_dec_grid1 > G53_DEC_MAXRG) g_dec_grid1 = 0;
         }
@@ -676,10 +807,10 @@ int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *id
         }
     }
     if (!g_dec_grid1) return 1;
-    /* scores [MAXNE] | tagged act [ROT][MAXK + 1][I], allocated and cleared once, so that no
-     * tagged word carries a live epoch. The tagged activations rotate over ROT copies by
-     * epoch, so a copy is reused only ROT launches later. */
-    const size_t off_act = (size_t)G53_DEC_MAXNE * 4;
+    /* tagged scores [MAXNE] | tagged act [ROT][MAXK + 1][I], allocated and cleared once, so
+     * that no tagged word carries a live epoch. The tagged activations rotate over ROT copies
+     * by epoch, so a copy is reused only ROT launches later. */
+    const size_t off_act = (size_t)G53_DEC_MAXNE * 8;
     const size_t act_copy = (size_t)(G53_DEC_MAXK + 1) * G53_DEC_I * 8;
     const size_t bytes = off_act + G53_DEC_ROT * act_copy;
     if (!g_dec_buf) {
@@ -696,21 +827,17 @@ int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *id
         g_dec_epoch = 1;
     }
     char *buf = (char *)g_dec_buf;
-    G53RouteArgs r;
-    r.x = x; r.router = (const uint16_t *)L->router; r.score = (float *)buf; r.NE = NE; r.trace = g_dec_trace;
-    G53ExpertsArgs e;
-    e.out = out; e.x = x; e.experts = L->experts; e.shared = L->shared;
-    e.score = r.score; e.bias = L->bias;
+    G53LayerArgs e;
+    e.out = out; e.x = x; e.router = (const uint16_t *)L->router; e.bias = L->bias;
+    e.experts = L->experts; e.shared = L->shared;
+    e.score = (g53_u64 *)buf;
     e.act = (g53_u64 *)(buf + off_act + (g_dec_epoch % G53_DEC_ROT) * act_copy);
     e.err = g_dec_state; e.idx_out = idx_out; e.w_out = w_out;
     e.NE = NE; e.K = K; e.norm_topk = L->norm_topk; e.epoch = g_dec_epoch;
     e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dec_trace;
     g53h_prof_mark(G53_PROF_START);
-    hipLaunchKernelGGL(k_dec_route, dim3(NE), dim3(64), 0, g53h_stream(), r);
-    G53_LAUNCHED("k_dec_route");
-    g53h_prof_mark(G53_PROF_ROUTER);
-    hipLaunchKernelGGL(k_dec_experts, dim3(g_dec_grid1), dim3(256), 0, g53h_stream(), e);
-    G53_LAUNCHED("k_dec_experts");
+    hipLaunchKernelGGL(k_dec_layer, dim3(g_dec_grid1), dim3(G53_DEC_NT), 0, g53h_stream(), e);
+    G53_LAUNCHED("k_dec_layer");
     g53h_prof_mark(G53_PROF_FUSED);
     return 0;
 }

@@ -65,7 +65,8 @@ __device__ __forceinline__ double g53_blk_lds(const uint4 (&c)[8], const float *
  * offsets. */
 #define G53_PADB 132
 
-__device__ __forceinline__ double g53_blk_pad(const uint4 (&c)[8], const float *xb)
+template <class V>
+__device__ __forceinline__ double g53_blk_pad(const V (&c)[8], const float *xb)
 {
     float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll

@@ -152,10 +152,11 @@ int g53h_grouped_errors(void);
 int g53h_set_grouped_trace(void *dev_buf);
 
 /* Single-token decode runs as one persistent launch when the layer has the released shapes
- * (hidden 4096, inter 2048, 128x128 blocks, topk <= 16); g53h_set_fused_decode(0) selects the
+ * (hidden 4096, inter 2048, 128x128 blocks, topk <= 15); g53h_set_fused_decode(0) selects the
  * multi-kernel path instead (returns the previous setting). g53h_decode_errors waits for the
  * stream and returns, then clears, the fused kernel's error flags (1: a grid wait timed out,
- * 2: a token had fewer than topk selectable experts), 0 if none. g53h_decode_grid returns the
+ * 2: a token had fewer than topk selectable experts, 8: an unusable expert descriptor, which
+ * then contributes zero), 0 if none. g53h_decode_grid returns the
  * fused kernel's workgroup count (0: unavailable, -1: not yet sized). */
 int g53h_set_fused_decode(int on);
 int g53h_decode_errors(void);
