@@ -237,41 +237,45 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
         const float ch = e < NE ? scv[v] + bias[e] : -INFINITY;
         key[v] = (ch > -INFINITY) ? g53_fkey(ch) : 0u;    /* 0: never chosen */
     }
-    /* K rounds of arg-max: each lane keeps the largest of its remaining keys (the lowest v
-     * among equals, so the lowest expert index of the lane); the wave maximum picks the round's
-     * key and, among lanes holding it, the lowest expert index wins */
-    uint32_t lm = 0;
-    int lv = 0;
+    /* K rounds of arg-max. Each lane first sorts its keys, largest first and, among equal keys,
+     * the lowest expert index first (a stable sort: the lane's experts are lane + 64 v in
+     * increasing v). A round takes the wave maximum of the lanes' first keys; among lanes
+     * holding it, the lowest expert index wins, and the winner shifts its list. */
+    int vid[NV];
+    float vsc[NV];
 #pragma unroll
-    for (int v = 0; v < NV; v++)
-        if (key[v] > lm) { lm = key[v]; lv = v; }
+    for (int v = 0; v < NV; v++) { vid[v] = lane + 64 * v; vsc[v] = scv[v]; }
+#pragma unroll
+    for (int pass = 0; pass < NV; pass++)
+#pragma unroll
+        for (int q = pass & 1; q + 1 < NV; q += 2) {
+            const bool sw_ = key[q + 1] > key[q];
+            const uint32_t k0 = key[q], k1 = key[q + 1];
+            const int i0 = vid[q], i1 = vid[q + 1];
+            const float s0 = vsc[q], s1 = vsc[q + 1];
+            key[q] = sw_ ? k1 : k0; key[q + 1] = sw_ ? k0 : k1;
+            vid[q] = sw_ ? i1 : i0; vid[q + 1] = sw_ ? i0 : i1;
+            vsc[q] = sw_ ? s1 : s0; vsc[q + 1] = sw_ ? s0 : s1;
+        }
     int pos = 0;
     for (int j = 0; j < K; j++) {
-        const uint32_t m = __ockl_wfred_max_u32(lm);
+        const uint32_t m = __ockl_wfred_max_u32(key[0]);
         if (m == 0) break;                                /* fewer than K selectable */
-        const uint64_t cand = __ballot(lm == m);
+        const uint64_t cand = __ballot(key[0] == m);
         int win;
-        if (__popcll(cand) == 1) {
-            win = (int)__builtin_ctzll(cand);
-        } else {                                          /* equal keys: the lowest index */
-            const uint32_t ix = __ockl_wfred_min_u32(lm == m ? (uint32_t)(lane + 64 * lv) : 0xffffffffu);
-            win = (int)(ix & 63);
+        if (__popcll(cand) == 1) win = (int)__builtin_ctzll(cand);
+        else win = (int)(__ockl_wfred_min_u32(key[0] == m ? (uint32_t)vid[0] : 0xffffffffu) & 63);
+        const int e = __builtin_amdgcn_readlane(vid[0], win);
+        const float wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(vsc[0]), win));
+        if (lane == 0) { sidx[j] = e; sw[j] = wsc; }
+        const bool me = lane == win;                      /* the winner drops its first key */
+#pragma unroll
+        for (int q = 0; q + 1 < NV; q++) {
+            key[q] = me ? key[q + 1] : key[q];
+            vid[q] = me ? vid[q + 1] : vid[q];
+            vsc[q] = me ? vsc[q + 1] : vsc[q];
         }
-        const int wv = __builtin_amdgcn_readlane(lv, win);
-        float wsc = 0.0f;
-#pragma unroll
-        for (int v = 0; v < NV; v++) if (v == wv) wsc = scv[v];
-        wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wsc), win));
-        if (lane == 0) { sidx[j] = win + 64 * wv; sw[j] = wsc; }
-        if (lane == win) {                                /* the winner drops the key */
-#pragma unroll
-            for (int v = 0; v < NV; v++) if (v == wv) key[v] = 0u;
-            lm = 0;
-            lv = 0;
-#pragma unroll
-            for (int v = 0; v < NV; v++)
-                if (key[v] > lm) { lm = key[v]; lv = v; }
-        }
+        key[NV - 1] = me ? 0u : key[NV - 1];
         pos++;
     }
     t_tau = __builtin_amdgcn_s_memrealtime();
@@ -324,17 +328,18 @@ struct G53Item {
 };
 
 /* The workgroup's list (workgroup b of G, one per CU):
- *   R      router rows b, b + G, ... (score of one expert each)
+ *   R      router rows b, b + G, ... (score of one expert each), taken by the first waves
+ *          before the list starts
  *   S      gate/up rows [g_lo, g_lo + g_n) of the shared expert (G items of slot K)
+ *   G      gate/up rows [g_lo, g_lo + g_n) of every routed slot, slot by slot
  *   A A D  the shared expert's activations (two halves into LDS entry 0) and its down row
  *          groups [rg_lo, rg_lo + n_rg)
- *   G      gate/up rows [g_lo, g_lo + g_n) of every routed slot, slot by slot
  *   A A D  per routed slot, in top-k order (entry t % NENT)
  * Its waves take items in this order through an LDS counter. The last wave first computes
  * the routing (the top-k, once the scores of every workgroup are in, and the chosen
- * experts' descriptors), the one dependency on other workgroups at the start; the other
- * waves meanwhile keep the memory busy with the router and shared-expert rows. By the time a workgroup reaches a slot's A items, every workgroup has
- * long finished that slot's gate/up rows. */
+ * experts' descriptors), the one dependency on other workgroups at the start; a few waves
+ * meanwhile keep the memory busy with the shared expert's rows. By the time a workgroup
+ * reaches a slot's A items, every workgroup has long finished that slot's gate/up rows. */
 struct G53List {
     int nR, g_lo, g_n, rg_lo, n_rg, K, hs, i_s, i_sd, i_g, i_rd, n;
 };
@@ -343,17 +348,16 @@ __device__ __forceinline__ G53Item g53_item(const G53List &l, int i, int b, int 
 {
     G53Item it{G53_IT_NONE, 0, 0, 0};
     const int per = 2 + l.n_rg;
-    if (i < l.i_s) { it.kind = G53_IT_R; it.r = b + i * G; return it; }
     if (i < l.i_sd) { it.kind = G53_IT_G; it.s = l.K; it.t = 0; it.r = l.g_lo + i - l.i_s; return it; }
     if (i < l.i_g) {
         const int j = i - l.i_sd;
-        it.s = l.K; it.t = 0;
-        if (j < 2) { it.kind = G53_IT_A; it.r = j; } else { it.kind = G53_IT_D; it.r = l.rg_lo + j - 2; }
+        it.kind = G53_IT_G; it.s = j / l.g_n; it.t = it.s + l.hs; it.r = l.g_lo + j % l.g_n;
         return it;
     }
     if (i < l.i_rd) {
         const int j = i - l.i_g;
-        it.kind = G53_IT_G; it.s = j / l.g_n; it.t = it.s + l.hs; it.r = l.g_lo + j % l.g_n;
+        it.s = l.K; it.t = 0;
+        if (j < 2) { it.kind = G53_IT_A; it.r = j; } else { it.kind = G53_IT_D; it.r = l.rg_lo + j - 2; }
         return it;
     }
     if (i < l.n) {
@@ -382,10 +386,6 @@ __device__ __forceinline__ bool g53_addr(const G53Item &it, const G53hExpert *st
     p = (const uint8_t *)dummy + lane * 128;
     ps = dummy;
     stride = 16;
-    if (it.kind == G53_IT_R) {                /* 64 bf16 weights per lane */
-        p = (const uint8_t *)(router + (size_t)it.r * G53_DEC_E + lane * 64);
-        return true;
-    }
     if (it.kind == G53_IT_A) {                /* 16 tagged activations per lane */
         p = (const uint8_t *)(act + (size_t)it.s * G53_DEC_I + it.r * 1024 + lane * 16);
         return true;
@@ -485,14 +485,17 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
     l.g_n = (int)((long)G53_DEC_I * (b + 1) / G) - l.g_lo;
     l.rg_lo = (int)((long)G53_DEC_NGRP * b / G);
     l.n_rg = (int)((long)G53_DEC_NGRP * (b + 1) / G) - l.rg_lo;
-    l.i_s = l.nR;
+    l.i_s = 0;
     l.i_sd = l.i_s + hs * l.g_n;
-    l.i_g = l.i_sd + hs * (2 + l.n_rg);
-    l.i_rd = l.i_g + K * l.g_n;
+    l.i_g = l.i_sd + K * l.g_n;
+    l.i_rd = l.i_g + hs * (2 + l.n_rg);
     l.n = l.i_rd + K * (2 + l.n_rg);
     const int ndone_all = nslots * l.n_rg;
 
     G53_TRACE(0);
+    /* the router rows go out first: waves 0 .. nR-1 take rows b, b + G, ... */
+    g53_u4 cr[8];
+    if (w < l.nR) g53_ld_str(cr, (const uint8_t *)(a.router + (size_t)(b + w * G) * G53_DEC_E + lane * 64), 16);
     const int words = (int)(sizeof(G53hExpert) / 4);
     if (threadIdx.x < words) ((int *)&st[K])[threadIdx.x] = hs ? ((const int *)a.shared)[threadIdx.x] : 0;
     for (int e = threadIdx.x; e < a.NE; e += G53_DEC_NT) biasl[e] = a.bias[e];
@@ -570,11 +573,6 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
 
     /* multiply one item whose codes are in c[] */
     auto compute = [&](const G53Item &it, const g53_u4 (&c)[8], float sc, bool loaded) {
-        if (it.kind == G53_IT_R) {
-            const double d = g53_router_row(c, xs, lane);
-            if (lane == 0) g53_st_tag(a.score + it.r, g53_tag(a.epoch, g53_sigmoidf_tab((float)d, etab)));
-            return;
-        }
         if (it.kind == G53_IT_G) {
             if (!loaded) return;                             /* expert not there */
             const float v = g53_gateup_pair(c, sc, xs, pw[w], a.limit, etab, lane);
@@ -723,10 +721,27 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
         tw_comp += __builtin_amdgcn_s_memrealtime() - tc0;
         n_items++;
     };
+    if (w < l.nR) {                                    /* the score of router row b + w G */
+        const double d = g53_router_row(cr, xs, lane);
+        if (lane == 0) g53_st_tag(a.score + b + w * G, g53_tag(a.epoch, g53_sigmoidf_tab((float)d, etab)));
+    }
     if (w == G53_DEC_NT / 64 - 1) route();
     /* only a few waves stream before the routing is known, so that the loads, the
      * publications and the coherent reads of the routing are not queued behind a saturated
      * memory system */
+    if (w >= G53_DEC_EARLY && w < G53_DEC_NT / 64 - 1) {
+        /* waves that wait for the routing first touch the expert descriptor table, so that the
+         * routing wave finds the chosen descriptors in this XCD's L2 */
+        constexpr int NP = G53_DEC_NT / 64 - 1 - G53_DEC_EARLY;
+        const int n8 = a.NE * (int)(sizeof(G53hExpert) / 8);
+        const uint2 *t8 = (const uint2 *)a.experts;
+        for (int q = (w - G53_DEC_EARLY) * 64 + lane; q < n8; q += 4 * NP * 64) {
+            uint2 v0 = t8[q], v1 = q + NP * 64 < n8 ? t8[q + NP * 64] : v0;
+            uint2 v2 = q + 2 * NP * 64 < n8 ? t8[q + 2 * NP * 64] : v0;
+            uint2 v3 = q + 3 * NP * 64 < n8 ? t8[q + 3 * NP * 64] : v0;
+            asm volatile("" ::"v"(v0.x), "v"(v1.x), "v"(v2.x), "v"(v3.x));
+        }
+    }
     if (w >= G53_DEC_EARLY && g53_lds_ld(&routed) == 0) {
         if (!g53_wait_lds(&routed, 1) && lane == 0) g53_flag_err(a.err, 1);
     }
