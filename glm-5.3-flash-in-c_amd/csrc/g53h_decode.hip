@@ -332,37 +332,37 @@ struct G53Item {
  *          before the list starts
  *   S      gate/up rows [g_lo, g_lo + g_n) of the shared expert (G items of slot K)
  *   G      gate/up rows [g_lo, g_lo + g_n) of every routed slot, slot by slot
- *   A A D  the shared expert's activations (two halves into LDS entry 0) and its down row
- *          groups [rg_lo, rg_lo + n_rg)
- *   A A D  per routed slot, in top-k order (entry t % NENT)
+ *   A, D   per slot (the shared expert first, then the routed slots in top-k order): the two
+ *          halves of its activation vector (A, into LDS entry t % NENT) and its down row
+ *          groups [rg_lo, rg_lo + n_rg) (D), a slot's A items one slot ahead of its D items
  * Its waves take items in this order through an LDS counter. The last wave first computes
  * the routing (the top-k, once the scores of every workgroup are in, and the chosen
  * experts' descriptors), the one dependency on other workgroups at the start; a few waves
  * meanwhile keep the memory busy with the shared expert's rows. By the time a workgroup
  * reaches a slot's A items, every workgroup has long finished that slot's gate/up rows. */
 struct G53List {
-    int nR, g_lo, g_n, rg_lo, n_rg, K, hs, i_s, i_sd, i_g, i_rd, n;
+    int nR, g_lo, g_n, rg_lo, n_rg, K, hs, i_s, i_sd, i_g, n;
 };
 
 __device__ __forceinline__ G53Item g53_item(const G53List &l, int i, int b, int G)
 {
     G53Item it{G53_IT_NONE, 0, 0, 0};
-    const int per = 2 + l.n_rg;
     if (i < l.i_sd) { it.kind = G53_IT_G; it.s = l.K; it.t = 0; it.r = l.g_lo + i - l.i_s; return it; }
     if (i < l.i_g) {
         const int j = i - l.i_sd;
         it.kind = G53_IT_G; it.s = j / l.g_n; it.t = it.s + l.hs; it.r = l.g_lo + j % l.g_n;
         return it;
     }
-    if (i < l.i_rd) {
-        const int j = i - l.i_g;
-        it.s = l.K; it.t = 0;
-        if (j < 2) { it.kind = G53_IT_A; it.r = j; } else { it.kind = G53_IT_D; it.r = l.rg_lo + j - 2; }
-        return it;
-    }
     if (i < l.n) {
-        const int j = i - l.i_rd, q = j % per;
-        it.s = j / per; it.t = it.s + l.hs;
+        /* the down phase, slot by slot in time order t (t = 0 the shared expert when there is
+         * one): A(0) A(0), then A(t) A(t) D(t-1)... for t = 1 .. T-1, then D(T-1)...; a slot's
+         * activations are copied one slot ahead of its down rows */
+        const int T = l.K + l.hs, per = 2 + l.n_rg;
+        int j = i - l.i_g, t, q;
+        if (j < 2) { t = 0; q = j; }
+        else { j -= 2; const int k = j / per + 1; q = j % per; if (k < T) { t = q < 2 ? k : k - 1; } else { t = T - 1; q += 2; } }
+        it.t = t;
+        it.s = l.hs ? (t == 0 ? l.K : t - 1) : t;
         if (q < 2) { it.kind = G53_IT_A; it.r = q; } else { it.kind = G53_IT_D; it.r = l.rg_lo + q - 2; }
     }
     return it;
@@ -488,8 +488,7 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
     l.i_s = 0;
     l.i_sd = l.i_s + hs * l.g_n;
     l.i_g = l.i_sd + K * l.g_n;
-    l.i_rd = l.i_g + hs * (2 + l.n_rg);
-    l.n = l.i_rd + K * (2 + l.n_rg);
+    l.n = l.i_g + nslots * (2 + l.n_rg);
     const int ndone_all = nslots * l.n_rg;
 
     G53_TRACE(0);
@@ -766,7 +765,7 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
     if (w < 4) G53_TRACE(2 + w);
     if (a.trace && lane == 0 && w < 4) {
         g53_u64 *tr = a.trace + (size_t)blockIdx.x * 32;
-        tr[16 + w] = tw_mem; tr[20 + w] = tw_comp; tr[6] = n_stale2; tr[24 + w] = n_items; tr[28 + w] = tw_d + tw_sh + tw_act + tw_use; (void)n_stale;
+        tr[16 + w] = tw_sh + tw_act; tr[20 + w] = tw_use; tr[6] = n_stale2; tr[24 + w] = tw_d; tr[28 + w] = tw_mem; (void)n_stale; (void)tw_comp; (void)n_items;
     }
 }
 
