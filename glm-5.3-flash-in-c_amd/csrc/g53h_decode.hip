@@ -257,25 +257,27 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
             vid[q] = sw_ ? i1 : i0; vid[q + 1] = sw_ ? i0 : i1;
             vsc[q] = sw_ ? s1 : s0; vsc[q + 1] = sw_ ? s0 : s1;
         }
+    /* the lane's head: its first key not yet taken (index hp into the sorted list) */
+    int hp = 0;
+    uint32_t hk = key[0];
+    int hv = vid[0];
+    float hs = vsc[0];
     int pos = 0;
     for (int j = 0; j < K; j++) {
-        const uint32_t m = __ockl_wfred_max_u32(key[0]);
+        const uint32_t m = __ockl_wfred_max_u32(hk);
         if (m == 0) break;                                /* fewer than K selectable */
-        const uint64_t cand = __ballot(key[0] == m);
+        const uint64_t cand = __ballot(hk == m);
         int win;
         if (__popcll(cand) == 1) win = (int)__builtin_ctzll(cand);
-        else win = (int)(__ockl_wfred_min_u32(key[0] == m ? (uint32_t)vid[0] : 0xffffffffu) & 63);
-        const int e = __builtin_amdgcn_readlane(vid[0], win);
-        const float wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(vsc[0]), win));
+        else win = (int)(__ockl_wfred_min_u32(hk == m ? (uint32_t)hv : 0xffffffffu) & 63);
+        const int e = __builtin_amdgcn_readlane(hv, win);
+        const float wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(hs), win));
         if (lane == 0) { sidx[j] = e; sw[j] = wsc; }
-        const bool me = lane == win;                      /* the winner drops its first key */
+        hp += lane == win;                                /* the winner moves to its next key */
+        hk = 0u;
 #pragma unroll
-        for (int q = 0; q + 1 < NV; q++) {
-            key[q] = me ? key[q + 1] : key[q];
-            vid[q] = me ? vid[q + 1] : vid[q];
-            vsc[q] = me ? vsc[q + 1] : vsc[q];
-        }
-        key[NV - 1] = me ? 0u : key[NV - 1];
+        for (int q = 0; q < NV; q++)
+            if (q == hp) { hk = key[q]; hv = vid[q]; hs = vsc[q]; }
         pos++;
     }
     t_tau = __builtin_amdgcn_s_memrealtime();
