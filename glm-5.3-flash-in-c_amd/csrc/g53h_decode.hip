@@ -53,7 +53,9 @@
 #define G53_DEC_NGRP (G53_DEC_E / G53_DEC_RPD)
 #define G53_DEC_MAXRG 4            /* row groups one workgroup owns (grid >= 256)         */
 #define G53_DEC_NT 768             /* threads of a k_dec_layer workgroup (one per CU)     */
+#ifndef G53_DEC_EARLY
 #define G53_DEC_EARLY 3            /* waves that stream before the routing is known       */
+#endif
 #define G53_DEC_NENT 3             /* activation copies a workgroup keeps in LDS          */
 #define G53_DEC_ROT 16             /* copies of the tagged activations, used in rotation  */
 #define G53_SPIN_LIMIT (1 << 20)   /* polls before a wait gives up                       */
