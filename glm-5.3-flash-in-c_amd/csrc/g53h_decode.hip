@@ -587,6 +587,13 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
             /* half of slot s's activations: check the epochs (re-reading stale values) and
              * store the values into entry t % NENT once its previous slot is done with it */
             const int use = it.t / G53_DEC_NENT;
+            /* the entry's previous slot must be done with it, also when this slot is absent:
+             * its count of copied halves must not run ahead of the previous slot's copies */
+            if (use > 0 && g53_lds_ld(&ent_used[e]) < use * l.n_rg) {
+                const g53_u64 t0 = __builtin_amdgcn_s_memrealtime();
+                if (!g53_wait_lds(&ent_used[e], use * l.n_rg) && lane == 0) g53_flag_err(a.err, 1);
+                tw_use += __builtin_amdgcn_s_memrealtime() - t0;
+            }
             if (!st[it.s].gate.w) {                          /* not used by any D item */
                 G53_CBAR();
                 if (lane == 0) g53_lds_add(&ent_ver[e], 1);
@@ -598,11 +605,6 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
             for (int k = 0; k < 8; k++) {
                 if (c[k].y != a.epoch) pending |= 1u << (2 * k);
                 if (c[k].w != a.epoch) pending |= 1u << (2 * k + 1);
-            }
-            if (use > 0 && g53_lds_ld(&ent_used[e]) < use * l.n_rg) {
-                const g53_u64 t0 = __builtin_amdgcn_s_memrealtime();
-                if (!g53_wait_lds(&ent_used[e], use * l.n_rg) && lane == 0) g53_flag_err(a.err, 1);
-                tw_use += __builtin_amdgcn_s_memrealtime() - t0;
             }
             const int i0 = it.r * 1024 + lane * 16;          /* 16 values within one block */
             float *dst = actl[e] + (i0 >> 7) * G53_PADB + (i0 & 127);
