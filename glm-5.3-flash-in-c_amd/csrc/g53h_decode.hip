@@ -53,6 +53,7 @@
 #define G53_DEC_NGRP (G53_DEC_E / G53_DEC_RPD)
 #define G53_DEC_MAXRG 4            /* row groups one workgroup owns (grid >= 256)         */
 #define G53_DEC_NT 768             /* threads of a k_dec_layer workgroup (one per CU)     */
+#define G53_DEC_DTAB ((G53_DEC_NT / 64 - 1 - G53_DEC_EARLY) * 8192)   /* staging bytes */
 #ifndef G53_DEC_EARLY
 #define G53_DEC_EARLY 3            /* waves that stream before the routing is known       */
 #endif
@@ -476,7 +477,7 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
     __shared__ float cvals[G53_DEC_MAXRG][G53_DEC_RPD][G53_DEC_MAXK + 1];
     /* ent_ver[e]: activation halves copied into entry e so far; ent_used[e]: D items done with
      * it; routed: the routing and the routed slots' descriptors are in st[] and sw[] */
-    __shared__ int qctr, ndone, routed, ent_ver[G53_DEC_NENT], ent_used[G53_DEC_NENT];
+    __shared__ int qctr, ndone, routed, dready, ent_ver[G53_DEC_NENT], ent_used[G53_DEC_NENT];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, hs = a.shared ? 1 : 0, nslots = K + hs;
     const int G = gridDim.x, b = blockIdx.x;
@@ -500,9 +501,12 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
     g53_u4 cr[8];
     if (w < l.nR) g53_ld_str(cr, (const uint8_t *)(a.router + (size_t)(b + w * G) * G53_DEC_E + lane * 64), 16);
     const int words = (int)(sizeof(G53hExpert) / 4);
+    /* the descriptor table staged in the waiting waves' chunk-trade LDS, when it fits */
+    uint2 *dtab = (uint2 *)xpw[G53_DEC_EARLY];
+    const bool dstage = a.NE * (int)sizeof(G53hExpert) <= G53_DEC_DTAB;
     if (threadIdx.x < words) ((int *)&st[K])[threadIdx.x] = hs ? ((const int *)a.shared)[threadIdx.x] : 0;
     for (int e = threadIdx.x; e < a.NE; e += G53_DEC_NT) biasl[e] = a.bias[e];
-    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; }
+    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; dready = 0; }
     if (threadIdx.x < 32) etab[threadIdx.x] = g53_exp2_tab_dev[threadIdx.x];
     if (threadIdx.x < G53_DEC_NENT) { ent_ver[threadIdx.x] = 0; ent_used[threadIdx.x] = 0; }
     for (int q = threadIdx.x; q < G53_DEC_E / 4; q += G53_DEC_NT) {
@@ -545,7 +549,13 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
             __builtin_amdgcn_wave_barrier();
         }
         G53_TRACE(13);
-        {                                              /* every load in flight at once */
+        if (dstage) {                                  /* staged by the waiting waves */
+            if (!g53_wait_lds(&dready, G53_DEC_NT / 64 - 1 - G53_DEC_EARLY) && lane == 0) g53_flag_err(a.err, 1);
+            for (int q = lane; q < K * words; q += 64) {
+                const int j = q / words, ex = sidx[j];
+                ((int *)st)[q] = (ex >= 0 && ex < a.NE) ? ((const int *)dtab)[ex * words + q % words] : 0;
+            }
+        } else {                                       /* every load in flight at once */
             constexpr int NQ = (G53_DEC_MAXK * (int)(sizeof(G53hExpert) / 4) + 63) / 64;
             int dv[NQ];
 #pragma unroll
@@ -735,16 +745,32 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
      * publications and the coherent reads of the routing are not queued behind a saturated
      * memory system */
     if (w >= G53_DEC_EARLY && w < G53_DEC_NT / 64 - 1) {
-        /* waves that wait for the routing first touch the expert descriptor table, so that the
-         * routing wave finds the chosen descriptors in this XCD's L2 */
+        /* waves that wait for the routing first copy the expert descriptor table into their
+         * (still unused) chunk-trade LDS, so that the routing wave picks the chosen ones from
+         * there; for a table too large for it they only touch it into this XCD's L2 */
         constexpr int NP = G53_DEC_NT / 64 - 1 - G53_DEC_EARLY;
+        constexpr int PER = (G53_DEC_DTAB / 8 + NP * 64 - 1) / (NP * 64);
         const int n8 = a.NE * (int)(sizeof(G53hExpert) / 8);
         const uint2 *t8 = (const uint2 *)a.experts;
-        for (int q = (w - G53_DEC_EARLY) * 64 + lane; q < n8; q += 4 * NP * 64) {
-            uint2 v0 = t8[q], v1 = q + NP * 64 < n8 ? t8[q + NP * 64] : v0;
-            uint2 v2 = q + 2 * NP * 64 < n8 ? t8[q + 2 * NP * 64] : v0;
-            uint2 v3 = q + 3 * NP * 64 < n8 ? t8[q + 3 * NP * 64] : v0;
-            asm volatile("" ::"v"(v0.x), "v"(v1.x), "v"(v2.x), "v"(v3.x));
+        const int base = (w - G53_DEC_EARLY) * 64 + lane;
+        if (dstage) {
+            uint2 v[PER];
+#pragma unroll
+            for (int k = 0; k < PER; k++) v[k] = base + k * NP * 64 < n8 ? t8[base + k * NP * 64] : make_uint2(0u, 0u);
+#pragma unroll
+            for (int k = 0; k < PER; k++)
+                if (base + k * NP * 64 < n8) dtab[base + k * NP * 64] = v[k];
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+            G53_CBAR();
+            if (lane == 0) g53_lds_add(&dready, 1);
+        } else {
+            for (int q = base; q < n8; q += 4 * NP * 64) {
+                uint2 v0 = t8[q], v1 = q + NP * 64 < n8 ? t8[q + NP * 64] : v0;
+                uint2 v2 = q + 2 * NP * 64 < n8 ? t8[q + 2 * NP * 64] : v0;
+                uint2 v3 = q + 3 * NP * 64 < n8 ? t8[q + 3 * NP * 64] : v0;
+                asm volatile("" ::"v"(v0.x), "v"(v1.x), "v"(v2.x), "v"(v3.x));
+            }
         }
     }
     if (w >= G53_DEC_EARLY && g53_lds_ld(&routed) == 0) {
