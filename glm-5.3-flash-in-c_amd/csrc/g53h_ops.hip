@@ -176,7 +176,8 @@ typedef double g53_v4d __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, float *__restrict__ choice,
                                                      const float *__restrict__ x, int T,
                                                      const uint16_t *__restrict__ gate,
-                                                     const float *__restrict__ bias, int NE, int E)
+                                                     const float *__restrict__ bias, int NE, int E, int klen,
+                                                     double *__restrict__ psum)
 {
     __shared__ __attribute__((aligned(16))) float xs[16 * G53_RM_XST];
     __shared__ g53_v4d part[3][64];
@@ -187,7 +188,8 @@ __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, 
     const uint16_t *wrow = gate + (size_t)er * E + w * 64 + g * 16;
     const float *xl = xs + i * G53_RM_XST + w * 64 + g * 16;
     g53_v4d acc = {0.0, 0.0, 0.0, 0.0};
-    for (int k0 = 0; k0 < E; k0 += 256) {
+    const int kb = blockIdx.z * klen;                        /* this workgroup's column range */
+    for (int k0 = kb; k0 < kb + klen; k0 += 256) {
         const uint4 wv0 = *(const uint4 *)(wrow + k0), wv1 = *(const uint4 *)(wrow + k0 + 8);
         __syncthreads();
         for (int q = threadIdx.x; q < 16 * 64; q += 256) {
@@ -212,7 +214,9 @@ __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, 
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int e = e0 + 4 * r + g;
-        if (t < T && e < NE) {
+        if (t < T && e < NE && psum) {                        /* a column range: its sum */
+            psum[((size_t)blockIdx.z * T + t) * NE + e] = acc[r];
+        } else if (t < T && e < NE) {
             const float s = g53_sigmoidf((float)acc[r]);
             score[(size_t)t * NE + e] = s;
             if (choice) choice[(size_t)t * NE + e] = s + bias[e];
@@ -303,6 +307,44 @@ int g53h_resolve_slots(G53hExpert *slots, const G53hExpert *experts, const int *
     return 0;
 }
 
+/* The router logits of a split column range: the S partial sums of each (token, expert) added
+ * in column order, then the sigmoid and the biased choice as in k_router_mfma. */
+__global__ void k_router_finish(float *__restrict__ score, float *__restrict__ choice,
+                                const double *__restrict__ part, const float *__restrict__ bias, int T, int NE,
+                                int S)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * NE) return;
+    double d = part[i];
+    for (int s = 1; s < S; s++) d = d + part[(long)s * T * NE + i];
+    const float v = g53_sigmoidf((float)d);
+    score[i] = v;
+    if (choice) choice[i] = v + bias[i % NE];
+}
+
+/* Library-owned buffer of the split router's partial sums (grown as needed, kept). */
+static void *g_router_part = nullptr;
+static size_t g_router_part_bytes = 0;
+static void *g53_router_part(size_t bytes)
+{
+    if (bytes <= g_router_part_bytes) return g_router_part;
+    if (g_router_part) {
+        if (hipStreamSynchronize(g53h_stream()) != hipSuccess || hipFree(g_router_part) != hipSuccess) {
+            g53h_fail("g53h_router: cannot release the partial-sum buffer");
+            return nullptr;
+        }
+        g_router_part = nullptr;
+        g_router_part_bytes = 0;
+    }
+    if (hipMalloc(&g_router_part, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        g53h_fail("g53h_router: cannot allocate %zu bytes of partial sums", bytes);
+        return nullptr;
+    }
+    g_router_part_bytes = bytes;
+    return g_router_part;
+}
+
 int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate, int gate_dt,
                      const float *bias, int NE, int E, int K, int norm_topk, float routed_scale,
                      int *nan_flag, float *scratch, const G53hExpert *experts, const G53hExpert *shared,
@@ -312,9 +354,25 @@ int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate
     if (K < 1 || K > NE || K > GLM53F_MAX_TOPK_DEV) return g53h_fail("g53h_router: topk %d", K);
     float *score = scratch, *choice = scratch + (size_t)T * NE;
     if (T >= 2 && gate_dt == 1 && E % 256 == 0) {           /* batches: the matrix-core form */
-        hipLaunchKernelGGL(k_router_mfma, dim3((NE + 15) / 16, (T + 15) / 16), dim3(256), 0, g53h_stream(), score,
-                           choice, x, T, (const uint16_t *)gate, bias, NE, E);
+        /* few tiles (small T): the columns are split over up to 8 workgroups per tile so that
+         * enough loads are in flight; the partial sums are added in column order after */
+        const int tiles = ((NE + 15) / 16) * ((T + 15) / 16);
+        int S = 1;
+        while (S < 8 && tiles * S * 2 <= 640 && (E / (S * 2)) % 256 == 0) S *= 2;
+        double *part = nullptr;
+        if (S > 1) {
+            part = (double *)g53_router_part((size_t)S * T * NE * sizeof(double));
+            if (!part) return -1;
+        }
+        hipLaunchKernelGGL(k_router_mfma, dim3((NE + 15) / 16, (T + 15) / 16, S), dim3(256), 0, g53h_stream(),
+                           score, choice, x, T, (const uint16_t *)gate, bias, NE, E, E / S, part);
         G53_LAUNCHED("k_router_mfma");
+        if (S > 1) {
+            const long n = (long)T * NE;
+            hipLaunchKernelGGL(k_router_finish, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, g53h_stream(),
+                               score, choice, part, bias, T, NE, S);
+            G53_LAUNCHED("k_router_finish");
+        }
     } else {
         hipLaunchKernelGGL(k_router_scores, dim3(NE, T), dim3(64), 0, g53h_stream(), score, choice, x, T, gate,
                            gate_dt, bias, NE, E);
