@@ -40,8 +40,8 @@ int         g53h_mark(void);
 float       g53h_elapsed_ms(void);
 /* Per-kernel timing of the layer entry points: with profiling on, each kernel launch is
  * followed by an event; g53h_prof_collect waits and returns, per tag (1 router, 2 gate/up,
- * 3 down+combine, 4 generic path, 5 grouped path), the summed milliseconds and the number
- * of launches since the last collect. */
+ * 3 down, 4 generic path, 5 grouped path, 6 combine, 7 one-launch decode layer), the summed
+ * milliseconds and the number of launches since the last collect, in arrays of ntags entries indexed by tag. */
 int         g53h_prof_enable(int on);
 int         g53h_prof_collect(float *ms, int *count, int ntags);
 /* HBM size and free bytes of the current device. */
