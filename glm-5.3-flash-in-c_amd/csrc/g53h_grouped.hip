@@ -297,7 +297,9 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const
 {
     constexpr int SL = NP * G53_GRP_NT * G53_GRP_XST;           /* one slice in LDS        */
     constexpr int PL = G53_GRP_NT * G53_GRP_XST;                /* one plane of a slice    */
-    constexpr int RPT = G53GrpLd<NW>::RPT;
+    /* only the rows the NH halves read are loaded: positions >= 32 * NH are never used */
+    constexpr int RPT0 = G53GrpLd<NW>::RPT, RPN = (NH * 32 + 8 * NW - 1) / (8 * NW);
+    constexpr int RPT = RPN < RPT0 ? RPN : RPT0;
     constexpr int LX = G53_GRP_LXS;                             /* slice slots             */
     constexpr int R0 = G53_GRP_RS;                              /* weight slots            */
     constexpr int R = NKB < R0 ? NKB : R0;
