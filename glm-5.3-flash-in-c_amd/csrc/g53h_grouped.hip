@@ -65,6 +65,9 @@ typedef __attribute__((address_space(1))) const float g53_gflt;
 #ifndef G53_GRP_WPC
 #define G53_GRP_WPC   1       /* GEMM workgroups resident per CU                             */
 #endif
+#ifndef G53_GRP_PERS
+#define G53_GRP_PERS  1       /* workgroups per CU in the grid: each loops over its items  */
+#endif
 #ifndef G53_GRP_RS
 #define G53_GRP_RS    4       /* weight blocks in a lane's ring                              */
 #endif
@@ -133,6 +136,7 @@ k_grp_plan(const int *__restrict__ idx, int T, int K, int NE, int has_sh, int *_
             ct += __shfl(it, 63);
         }
         if (tid == 0) { off[nseg] = cp; tb[nseg] = ct; meta[0] = ct; }
+        if (tid < 16) meta[2 + tid] = 0;         /* the GEMMs' item counters */
     }
     __syncthreads();
     const int ps = K + 1;
@@ -410,23 +414,26 @@ struct G53GrpArgs {
     float limit, aq_scale, aq_inv;
     int partial;                   /* 1: experts without weights are outside this batch and
                                       left alone, unless marked dropped (gate.pad_ == 1)    */
+    int *ctr;                      /* [16] item counters: 0-7 gate/up, 8-15 down; each
+                                      kernel starts with its own at zero and clears the
+                                      other kernel's                                      */
     uint64_t *trace;               /* optional: [grid][8] timestamps of each workgroup    */
 };
 
 /* Diagnostics: 100 MHz timestamps of workgroup phases into a.trace when it is set. */
 #define G53_GTRACE(k, v) do { if (a.trace && threadIdx.x == 0) a.trace[(size_t)blockIdx.x * 8 + (k)] = (v); } while (0)
 
-/* The workgroup's (tile, row block): the dispatcher deals workgroups round-robin over the 8
- * XCDs, so XCD x takes items x*per .. x*per + per - 1 in order. Items are numbered segment by
+/* Item loc of the workgroup's group: the dispatcher deals workgroups round-robin over the 8
+ * XCDs, so the workgroups of XCD x (blockIdx.x % 8 == x) share the items x*per .. x*per +
+ * per - 1, which they claim in order from the group's counter. Items are numbered segment by
  * segment, and inside a segment row block by row block, all tiles of a block in a row: the
- * tiles of one expert that re-read the same weight rows run next to each other on one XCD and
- * find them in its L2. Returns false when the workgroup has no item. */
-__device__ __forceinline__ bool g53_grp_item(const int4 *tiles, int ntile, int MB, int4 &tl, int &mb)
+ * tiles of one expert that re-read the same weight rows run next to each other on one XCD
+ * and find them in its L2. Returns false past the group's last item. */
+__device__ __forceinline__ bool g53_grp_item(const int4 *tiles, int ntile, int MB, int loc, int4 &tl, int &mb)
 {
     const int nitems = ntile * MB;
     const int per = (nitems + 7) >> 3;
-    const int x = blockIdx.x & 7, loc = blockIdx.x >> 3;
-    const int item = x * per + loc;
+    const int item = (blockIdx.x & 7) * per + loc;
     if (loc >= per || item >= nitems) return false;
     const int w = tiles[item / MB].w;                    /* a tile of the item's segment */
     const int ts0 = w & 0xffff, nts = w >> 16;
@@ -434,6 +441,13 @@ __device__ __forceinline__ bool g53_grp_item(const int4 *tiles, int ntile, int M
     mb = q / nts;
     tl = tiles[ts0 + q % nts];
     return true;
+}
+
+/* Claim the group's next item (a relaxed device-scope counter, one claim per item, issued an
+ * item ahead so that its latency hides behind the current item). */
+__device__ __forceinline__ int g53_grp_claim(int *ctr)
+{
+    return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* Gate/up + SwiGLU for (tile, block mb of 16*NW intermediate rows). Wave w: A rows 0-15 = gate
@@ -445,75 +459,87 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
     __shared__ __attribute__((aligned(16))) uint8_t xs[G53_GRP_NS * G53_GRP_NPX * G53_GRP_NT * G53_GRP_XST];
     __shared__ uint64_t etab[32];                        /* the exponential's table (LDS) */
     __shared__ int flags[2 * G53_GRP_NS];
-    int4 tl;
-    int mb;
-    G53_GTRACE(0, __builtin_amdgcn_s_memrealtime());
-    if (!g53_grp_item(a.tiles, a.meta[0], a.I / (16 * NW), tl, mb)) return;
+    __shared__ int claim[2];
+    int *ctr = a.ctr + (blockIdx.x & 7);
     if (threadIdx.x < 32) etab[threadIdx.x] = g53_exp2_tab_dev[threadIdx.x];
-    G53_GTRACE(4, (uint64_t)__smid() << 32 | (uint32_t)(tl.y << 8 | tl.z));
-    const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
-    if (!ex || ex->gate.w == nullptr) return;            /* absent expert: down writes zeros */
-    if (!g53_grp_desc_ok(*ex, a.E, a.I)) {
-        if (threadIdx.x == 0) atomicOr(&a.meta_w[1], G53_GRP_EDESC);
-        return;
-    }
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int n = tl.z, pos0 = tl.y;
-    G53GrpLd<NW> ld;
-#pragma unroll
-    for (int j = 0; j < G53GrpLd<NW>::RPT; j++) {
-        const int lp = (tid >> 3) + j * 8 * NW, piece = tid & 7;
-        ld.src[j] = a.xq + (size_t)a.tok_of[pos0 + (lp < n ? lp : 0)] * a.E + piece * 16;
-        ld.dst[j] = lp * G53_GRP_XST + piece * 16;
-    }
-    const size_t xps = (size_t)a.T * a.E;
-    /* this lane's weight row */
-    const int i = lane & 31, g = lane >> 5;
-    const int r0 = mb * 16 * NW + w * 16;                /* first intermediate row of the wave */
-    const G53hMat &m = i < 16 ? ex->gate : ex->up;
-    const uint8_t *arow = m.w + (size_t)(r0 + (i & 15)) * a.E + g * 64;
-    const float *s0 = (const float *)ex->gate.s + (size_t)(r0 / 128) * ex->gate.scols;
-    const float *s1 = (const float *)ex->up.s + (size_t)(r0 / 128) * ex->up.scols;
-    g53_v16f acc[G53_GRP_NH] = {};
-    /* the token scales of this lane's positions, loaded before the weights stream */
-    float xi[G53_GRP_NH];
-#pragma unroll
-    for (int h = 0; h < G53_GRP_NH; h++) xi[h] = a.xinv[a.tok_of[pos0 + (h * 32 + i < n ? h * 32 + i : 0)]];
-    G53_GTRACE(1, __builtin_amdgcn_s_memrealtime());
-    if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
-    __syncthreads();
-    int spin_err = 0;
-    switch ((n + 31) >> 5) {
-    case 1: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 1>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
-    case 2: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 2>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
-    case 3: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 3>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
-    default: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 4>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
-    }
-    if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
-    G53_GTRACE(2, __builtin_amdgcn_s_memrealtime());
-    /* epilogue: SwiGLU and the activation planes */
-#pragma unroll
-    for (int h = 0; h < G53_GRP_NH; h++) {
-        const int j = h * 32 + i;
-        if (j >= n) continue;
-        const int pos = pos0 + j;
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            float v[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int r = q * 4 + k;
-                v[k] = g53_swiglu1_tab(acc[h][r] * xi[h], acc[h][r + 8] * xi[h], a.limit, etab) * a.aq_scale;
-            }
-            uint32_t pk[G53_GRP_NPA];
-            g53_split_planes<G53_GRP_NPA>(v, pk);
-            const int row = r0 + q * 8 + g * 4;
-#pragma unroll
-            for (int p = 0; p < G53_GRP_NPA; p++)
-                *(uint32_t *)(a.aq + ((size_t)p * a.P + pos) * a.I + row) = pk[p];
+    if (threadIdx.x == 0) claim[0] = g53_grp_claim(ctr);
+    if (blockIdx.x == 0 && threadIdx.x < 8) a.ctr[8 + threadIdx.x] = 0;   /* the down kernel's */
+    const int ntile = a.meta[0];
+    for (int kk = 0;; kk++) {
+        __syncthreads();                     /* claim[] written; the previous item is done with LDS */
+        int4 tl;
+        int mb;
+        G53_GTRACE(0, __builtin_amdgcn_s_memrealtime());
+        if (!g53_grp_item(a.tiles, ntile, a.I / (16 * NW), claim[kk & 1], tl, mb)) break;
+        int nxt = 0;
+        if (threadIdx.x == 0) nxt = g53_grp_claim(ctr);
+        G53_GTRACE(4, (uint64_t)__smid() << 32 | (uint32_t)(tl.y << 8 | tl.z));
+        const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
+        const bool usable = ex && ex->gate.w != nullptr && g53_grp_desc_ok(*ex, a.E, a.I);
+        if (!usable) {                                       /* absent expert: down writes zeros */
+            if (ex && ex->gate.w && threadIdx.x == 0) atomicOr(&a.meta_w[1], G53_GRP_EDESC);
+            if (threadIdx.x == 0) claim[(kk + 1) & 1] = nxt;
+            continue;
         }
+        const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+        const int n = tl.z, pos0 = tl.y;
+        G53GrpLd<NW> ld;
+#pragma unroll
+        for (int j = 0; j < G53GrpLd<NW>::RPT; j++) {
+            const int lp = (tid >> 3) + j * 8 * NW, piece = tid & 7;
+            ld.src[j] = a.xq + (size_t)a.tok_of[pos0 + (lp < n ? lp : 0)] * a.E + piece * 16;
+            ld.dst[j] = lp * G53_GRP_XST + piece * 16;
+        }
+        const size_t xps = (size_t)a.T * a.E;
+        /* this lane's weight row */
+        const int i = lane & 31, g = lane >> 5;
+        const int r0 = mb * 16 * NW + w * 16;                /* first intermediate row of the wave */
+        const G53hMat &m = i < 16 ? ex->gate : ex->up;
+        const uint8_t *arow = m.w + (size_t)(r0 + (i & 15)) * a.E + g * 64;
+        const float *s0 = (const float *)ex->gate.s + (size_t)(r0 / 128) * ex->gate.scols;
+        const float *s1 = (const float *)ex->up.s + (size_t)(r0 / 128) * ex->up.scols;
+        g53_v16f acc[G53_GRP_NH] = {};
+        /* the token scales of this lane's positions, loaded before the weights stream */
+        float xi[G53_GRP_NH];
+#pragma unroll
+        for (int h = 0; h < G53_GRP_NH; h++) xi[h] = a.xinv[a.tok_of[pos0 + (h * 32 + i < n ? h * 32 + i : 0)]];
+        G53_GTRACE(1, __builtin_amdgcn_s_memrealtime());
+        if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
+        if (threadIdx.x == 0) claim[(kk + 1) & 1] = nxt;
+        __syncthreads();
+        int spin_err = 0;
+        switch ((n + 31) >> 5) {
+        case 1: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 1>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        case 2: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 2>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        case 3: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 3>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        default: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 4>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        }
+        if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
+        G53_GTRACE(2, __builtin_amdgcn_s_memrealtime());
+        /* epilogue: SwiGLU and the activation planes */
+#pragma unroll
+        for (int h = 0; h < G53_GRP_NH; h++) {
+            const int j = h * 32 + i;
+            if (j >= n) continue;
+            const int pos = pos0 + j;
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                float v[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int r = q * 4 + k;
+                    v[k] = g53_swiglu1_tab(acc[h][r] * xi[h], acc[h][r + 8] * xi[h], a.limit, etab) * a.aq_scale;
+                }
+                uint32_t pk[G53_GRP_NPA];
+                g53_split_planes<G53_GRP_NPA>(v, pk);
+                const int row = r0 + q * 8 + g * 4;
+#pragma unroll
+                for (int p = 0; p < G53_GRP_NPA; p++)
+                    *(uint32_t *)(a.aq + ((size_t)p * a.P + pos) * a.I + row) = pk[p];
+            }
+        }
+        G53_GTRACE(3, __builtin_amdgcn_s_memrealtime());
     }
-    G53_GTRACE(3, __builtin_amdgcn_s_memrealtime());
 }
 
 /* Down for (tile, block mb of 32*NW rows): wave w owns rows mb*32*NW + w*32 + 0..31 of the down
@@ -523,55 +549,70 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
 {
     __shared__ __attribute__((aligned(16))) uint8_t xs[G53_GRP_NS * G53_GRP_NPA * G53_GRP_NT * G53_GRP_XST];
     __shared__ int flags[2 * G53_GRP_NS];
+    __shared__ int claim[2];
     constexpr int MR = 32 * NW;
-    int4 tl;
-    int mb;
-    if (!g53_grp_item(a.tiles, a.meta[0], a.E / MR, tl, mb)) return;
-    const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int n = tl.z, pos0 = tl.y;
-    const int i = lane & 31, g = lane >> 5;
-    const bool present = ex && ex->gate.w != nullptr;
-    if (!present && a.partial && !(ex && ex->gate.pad_ == G53_DROPPED)) return;   /* another batch */
-    const bool ok = present && g53_grp_desc_ok(*ex, a.E, a.I);
-    if (!ok) {                                           /* zero contributions */
-        for (int q = tid; q < n * (MR / 4); q += 64 * NW) {
-            const int j = q / (MR / 4), c = (q % (MR / 4)) * 4;
-            *(float4 *)(a.contrib + (size_t)(pos0 + j) * a.E + mb * MR + c) = make_float4(0.f, 0.f, 0.f, 0.f);
+    int *ctr = a.ctr + 8 + (blockIdx.x & 7);
+    if (threadIdx.x == 0) claim[0] = g53_grp_claim(ctr);
+    if (blockIdx.x == 0 && threadIdx.x < 8) a.ctr[threadIdx.x] = 0;        /* the gate/up kernel's */
+    const int ntile = a.meta[0];
+    for (int kk = 0;; kk++) {
+        __syncthreads();                     /* claim[] written; the previous item is done with LDS */
+        int4 tl;
+        int mb;
+        if (!g53_grp_item(a.tiles, ntile, a.E / MR, claim[kk & 1], tl, mb)) break;
+        int nxt = 0;
+        if (threadIdx.x == 0) nxt = g53_grp_claim(ctr);
+        const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
+        const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+        const int n = tl.z, pos0 = tl.y;
+        const int i = lane & 31, g = lane >> 5;
+        const bool present = ex && ex->gate.w != nullptr;
+        if (!present && a.partial && !(ex && ex->gate.pad_ == G53_DROPPED)) {   /* another batch */
+            if (tid == 0) claim[(kk + 1) & 1] = nxt;
+            continue;
         }
-        return;
-    }
-    G53GrpLd<NW> ld;
+        const bool ok = present && g53_grp_desc_ok(*ex, a.E, a.I);
+        if (!ok) {                                           /* zero contributions */
+            for (int q = tid; q < n * (MR / 4); q += 64 * NW) {
+                const int j = q / (MR / 4), c = (q % (MR / 4)) * 4;
+                *(float4 *)(a.contrib + (size_t)(pos0 + j) * a.E + mb * MR + c) = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            if (tid == 0) claim[(kk + 1) & 1] = nxt;
+            continue;
+        }
+        G53GrpLd<NW> ld;
 #pragma unroll
-    for (int j = 0; j < G53GrpLd<NW>::RPT; j++) {
-        const int lp = (tid >> 3) + j * 8 * NW, piece = tid & 7;
-        ld.src[j] = a.aq + (size_t)(pos0 + (lp < n ? lp : 0)) * a.I + piece * 16;
-        ld.dst[j] = lp * G53_GRP_XST + piece * 16;
-    }
-    const size_t xps = (size_t)a.P * a.I;
-    const int r0 = mb * MR + w * 32;
-    const uint8_t *arow = ex->down.w + (size_t)(r0 + i) * a.I + g * 64;
-    const float *s0 = (const float *)ex->down.s + (size_t)(r0 / 128) * ex->down.scols;
-    g53_v16f acc[G53_GRP_NH] = {};
-    if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
-    __syncthreads();
-    int spin_err = 0;
-    switch ((n + 31) >> 5) {
-    case 1: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 1>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
-    case 2: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 2>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
-    case 3: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 3>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
-    default: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 4>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
-    }
-    if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
+        for (int j = 0; j < G53GrpLd<NW>::RPT; j++) {
+            const int lp = (tid >> 3) + j * 8 * NW, piece = tid & 7;
+            ld.src[j] = a.aq + (size_t)(pos0 + (lp < n ? lp : 0)) * a.I + piece * 16;
+            ld.dst[j] = lp * G53_GRP_XST + piece * 16;
+        }
+        const size_t xps = (size_t)a.P * a.I;
+        const int r0 = mb * MR + w * 32;
+        const uint8_t *arow = ex->down.w + (size_t)(r0 + i) * a.I + g * 64;
+        const float *s0 = (const float *)ex->down.s + (size_t)(r0 / 128) * ex->down.scols;
+        g53_v16f acc[G53_GRP_NH] = {};
+        if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
+        if (threadIdx.x == 0) claim[(kk + 1) & 1] = nxt;
+        __syncthreads();
+        int spin_err = 0;
+        switch ((n + 31) >> 5) {
+        case 1: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 1>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        case 2: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 2>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        case 3: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 3>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        default: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 4>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        }
+        if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
 #pragma unroll
-    for (int h = 0; h < G53_GRP_NH; h++) {
-        const int j = h * 32 + i;
-        if (j >= n) continue;
-        float *dst = a.contrib + (size_t)(pos0 + j) * a.E + r0 + g * 4;
+        for (int h = 0; h < G53_GRP_NH; h++) {
+            const int j = h * 32 + i;
+            if (j >= n) continue;
+            float *dst = a.contrib + (size_t)(pos0 + j) * a.E + r0 + g * 4;
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            *(float4 *)(dst + q * 8) = make_float4(acc[h][q * 4] * a.aq_inv, acc[h][q * 4 + 1] * a.aq_inv,
-                                                   acc[h][q * 4 + 2] * a.aq_inv, acc[h][q * 4 + 3] * a.aq_inv);
+            for (int q = 0; q < 4; q++)
+                *(float4 *)(dst + q * 8) = make_float4(acc[h][q * 4] * a.aq_inv, acc[h][q * 4 + 1] * a.aq_inv,
+                                                       acc[h][q * 4 + 2] * a.aq_inv, acc[h][q * 4 + 3] * a.aq_inv);
+        }
     }
 }
 
@@ -697,7 +738,7 @@ static int g53_grp_plan_pass(const float *x, int tc, const G53hMoeLayer *L, cons
     int ex = 0;
     (void)frexpf(bound, &ex);                      /* |act| <= bound < 2^ex */
     G53GrpArgs &a = g_pass.a;
-    a.experts = L->experts; a.shared = L->shared; a.tiles = tiles; a.meta = meta; a.meta_w = meta;
+    a.experts = L->experts; a.shared = L->shared; a.tiles = tiles; a.meta = meta; a.meta_w = meta; a.ctr = meta + 2;
     a.tok_of = tok_of; a.xq = xq; a.xinv = xinv; a.aq = aq; a.contrib = contrib;
     a.T = tc; a.P = P; a.E = E; a.I = I; a.NE = NE;
     a.limit = L->swiglu_limit; a.aq_scale = ldexpf(1.0f, 8 - ex); a.aq_inv = ldexpf(1.0f, ex - 8);
@@ -715,8 +756,14 @@ static int g53_grp_run_pass(const G53hExpert *experts, const G53hExpert *shared,
     const int E = a.E, I = a.I, maxtiles = g_pass.maxtiles;
     hipStream_t st = g53h_stream();
     constexpr int NW = G53_GRP_NW;
-    const unsigned g1 = (unsigned)((maxtiles * (I / (16 * NW)) + 7) / 8 * 8);
-    const unsigned g2 = (unsigned)((maxtiles * (E / (32 * NW))) + 7) / 8 * 8;
+    unsigned g1 = (unsigned)((maxtiles * (I / (16 * NW)) + 7) / 8 * 8);
+    unsigned g2 = (unsigned)((maxtiles * (E / (32 * NW))) + 7) / 8 * 8;
+#if G53_GRP_PERS
+    {
+        const unsigned cap = (unsigned)(g53h_num_cus() * G53_GRP_WPC * G53_GRP_PERS) / 8 * 8;
+        if (cap >= 8) { g1 = g1 < cap ? g1 : cap; g2 = g2 < cap ? g2 : cap; }
+    }
+#endif
 #define G53_GU(N) case N: hipLaunchKernelGGL((k_grp_gateup<NW, N>), dim3(g1), dim3(64 * NW), 0, st, a); break
 #define G53_DN(N) case N: hipLaunchKernelGGL((k_grp_down<NW, N>), dim3(g2), dim3(64 * NW), 0, st, a); break
     switch (E / 128) { G53_GU(4); G53_GU(8); G53_GU(16); G53_GU(32);
