@@ -197,8 +197,8 @@ extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
  * "first strictly greater" arg-max, so the larger value first, the lower index among equal
  * values, NaN and -inf never), then the weights (:970-975). The scores are the tagged words
  * other workgroups of this launch publish; they are read coherently, and re-read until every
- * tag carries this launch's epoch. The K-th largest key is found by a binary search over the
- * keys with wave ballots, then the chosen experts are ranked among themselves. sidx[j] = -1
+ * tag carries this launch's epoch. Each lane sorts its keys; K rounds then take the wave
+ * maximum of the lanes' first untaken keys (the lowest expert index among equal ones). sidx[j] = -1
  * where fewer than K experts are selectable (the reference aborts there; bit 2 of the error
  * flags is then set). Returns false when the scores did not all arrive in time. */
 template <int NV>
