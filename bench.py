@@ -199,7 +199,7 @@ def bench_grouped(a):
     check(L.g53h_mark(), "mark")
     ms = L.g53h_elapsed_ms() / steps
     glm53h.sync()
-    per = prof_run(L, step, min(steps, 40), [(1, "k_router_mfma"), (5, "k_grp_plan+k_grp_xq"), (2, "k_grp_gateup"),
+    per = prof_run(L, step, min(steps, 40), [(1, "router"), (5, "k_grp_plan+k_grp_xq"), (2, "k_grp_gateup"),
                                               (3, "k_grp_down"), (6, "k_grp_combine")])
     D = float(np.mean(uniq))
     eb = sp.expert_bytes()

@@ -194,76 +194,4 @@ __device__ __forceinline__ uint32_t g53_fkey(float f)
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-/* Top-k of choice[0..NE) by one wave, equal to the reference's k rounds of "first strictly
- * greater" argmax (src/core/glm53f_ops.c:957-969): larger value first, the lower index first
- * among equal values, NaN and -inf never chosen. sel_out[0..K) receives the indices in that
- * order (-1 where fewer than K experts are selectable). NE <= 1024, K <= 64. The threshold
- * (the K-th largest key) is found by a binary search over keys with wave ballots, then the
- * chosen K are ranked among themselves. Must be called by all 64 lanes of one wave. */
-__device__ __forceinline__ void g53_topk_wave(const float *choice, int NE, int K, int *sel_out,
-                                              uint32_t *kbuf, int *ebuf)
-{
-    const int lane = threadIdx.x & 63;
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    uint32_t key[16];
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int e = lane + 64 * v;
-        const float f = e < NE ? choice[e] : -INFINITY;
-        key[v] = (f > -INFINITY) ? g53_fkey(f) : 0u;       /* 0: not selectable */
-    }
-    /* tau = the largest key with at least K keys >= tau (1 if fewer than K are selectable) */
-    uint32_t lo = 1u, hi = 0xffffffffu;
-    while (lo < hi) {
-        const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
-        int c = 0;
-#pragma unroll
-        for (int v = 0; v < 16; v++) c += __popcll(__ballot(key[v] >= mid));
-        if (c >= K) lo = mid; else hi = mid - 1;
-    }
-    const uint32_t tau = lo;
-    int gt = 0;
-#pragma unroll
-    for (int v = 0; v < 16; v++) gt += __popcll(__ballot(key[v] > tau));
-    int need = K - gt;                                    /* ties at tau, lowest index first */
-    int pos = 0;
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-        bool chosen = key[v] > tau;
-        const uint64_t tm = __ballot(key[v] == tau && key[v] != 0u);
-        if (need > 0 && tm) {
-            uint64_t take = tm;
-            const int n = __popcll(tm);
-            if (n > need) {                                /* keep the lowest `need` lanes */
-                uint64_t m = tm;
-                for (int i = 0; i < need; i++) m &= m - 1;  /* drop the lowest `need` bits ... */
-                take = tm & ~m;                             /* ... what was dropped is taken  */
-            }
-            chosen = chosen || ((take >> lane) & 1ull);
-            need -= __popcll(take);
-        }
-        const uint64_t cm = __ballot(chosen);
-        if (chosen) {
-            const int p = pos + __popcll(cm & lt);
-            kbuf[p] = key[v];
-            ebuf[p] = lane + 64 * v;
-        }
-        pos += __popcll(cm);
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < K) sel_out[lane] = -1;
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < pos) {
-        const uint32_t kv = kbuf[lane];
-        const int ev = ebuf[lane];
-        int rank = 0;
-        for (int j = 0; j < pos; j++) rank += (kbuf[j] > kv) || (kbuf[j] == kv && ebuf[j] < ev);
-        sel_out[rank] = ev;
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-}
-
 #endif /* G53H_GEMV_H */

@@ -1,7 +1,7 @@
 /* g53h_moe.hip - the routed-expert MoE layer on gfx950.
  *
  * Decode path (bit-exact with the reference, src/core/glm53f_ops.c:1144-1342):
- *   1. router          k_router_scores + k_router_select (g53h_ops.hip)
+ *   1. router          k_router_scores + k_router_select_w (g53h_ops.hip)
  *   2. k_gateup        gate and up products of every slot (top-k experts + shared), SwiGLU
  *   3. k_down_combine  down product of every slot; the last workgroup to finish a row tile
  *                      combines the slots in double in top-k order and adds the shared expert

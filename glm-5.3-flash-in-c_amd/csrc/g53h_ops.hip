@@ -6,7 +6,7 @@
  *                     g53h_moe.hip for the expert shapes.
  *   k_swiglu          clamped SwiGLU.
  *   k_router_scores   sigmoid(W x) and sigmoid + bias for T tokens, one wave per expert.
- *   k_router_select   top-k by repeated argmax (strict >, lowest index), renormalise, scale.
+ *   k_router_select_w top-k by repeated argmax (strict >, lowest index), renormalise, scale.
  *   k_route_topn      next-layer prediction.
  */
 #include <hip/hip_runtime.h>
@@ -172,6 +172,12 @@ __global__ void __launch_bounds__(64) k_router_scores(float *__restrict__ score,
  * r holds C[4r + l/16][l % 16]. x chunks are staged in LDS. bf16 router rows, E a multiple of
  * 256. */
 typedef double g53_v4d __attribute__((ext_vector_type(4)));
+#ifndef G53_RM32_S
+#define G53_RM32_S    8         /* column ranges of the large-batch router               */
+#endif
+#ifndef G53_RM32_MINT
+#define G53_RM32_MINT 512       /* tokens from which the large-batch router is used       */
+#endif
 #define G53_RM_XST 260                                  /* LDS floats per token row       */
 __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, float *__restrict__ choice,
                                                      const float *__restrict__ x, int T,
@@ -224,59 +230,182 @@ __global__ void __launch_bounds__(256) k_router_mfma(float *__restrict__ score, 
     }
 }
 
-/* Top-k by rank, equal to the reference's k rounds of "first strictly greater" argmax: an
- * expert's rank is the number of experts with a larger choice, plus those with an equal choice
- * and a lower index; rank j goes to slot j. NaN and -inf are never selected (the reference's
- * scan starts from -inf and only moves on a strict >); a token with fewer than k selectable
- * experts sets *nan_flag. Then the weights: the unbiased scores of the chosen experts,
- * renormalised in double if norm_topk, times routed_scale. When experts != NULL the chosen
- * experts' descriptors (and the shared expert's, if any) are copied to slots[t][*], so the
- * expert kernels find their matrices with one load. One workgroup per token. */
-__global__ void __launch_bounds__(1024) k_router_select(int *__restrict__ idx, float *__restrict__ w,
-                                                        const float *__restrict__ score,
-                                                        const float *__restrict__ choice, int NE, int K,
-                                                        int norm_topk, float routed_scale,
-                                                        int *__restrict__ nan_flag,
-                                                        const G53hExpert *__restrict__ experts,
-                                                        const G53hExpert *__restrict__ shared,
-                                                        G53hExpert *__restrict__ slots)
+/* The same partial sums for large batches: one wave per workgroup owns a 32 x 32 tile
+ * (experts e0 = 32 * bx .., tokens t0 = 32 * by ..) over the column range bz * klen .. + klen, as 2 x 2 blocks of v_mfma_f64_16x16x4f64, so that each operand
+ * converted to double feeds two instructions. Both operands come straight from memory (L2):
+ * per 64-column chunk, lane l reads 16 consecutive columns 16 (l / 16) .. of its two expert rows
+ * (l % 16, 16 + l % 16) and of its two token rows; step s of the chunk uses column
+ * 16 (l / 16) + s, the same K assignment for A and B. The next chunk's loads are issued before
+ * the current chunk's arithmetic. The sums go to psum[bz][t][e]; the selection kernel adds
+ * the ranges in column order. bf16 router rows, klen a multiple of 64. */
+__global__ void __launch_bounds__(64) k_router_mfma32(const float *__restrict__ x, int T,
+                                                      const uint16_t *__restrict__ gate, int NE, int E,
+                                                      int klen, int S, double *__restrict__ psum)
 {
-    __shared__ __attribute__((aligned(16))) float c[1024];
-    __shared__ int sel[GLM53F_MAX_TOPK_DEV];
-    __shared__ float sw[GLM53F_MAX_TOPK_DEV];
-    __shared__ uint32_t kbuf[GLM53F_MAX_TOPK_DEV];
-    __shared__ int ebuf[GLM53F_MAX_TOPK_DEV];
-    const int t = blockIdx.x, i = threadIdx.x;
-    const int NE4 = (NE + 3) & ~3;
-    const float *ct = choice + (size_t)t * NE;
-    for (int e = i; e < NE4; e += blockDim.x) c[e] = e < NE ? ct[e] : -INFINITY;
-    __syncthreads();
-    if (i < 64) g53_topk_wave(c, NE, K, sel, kbuf, ebuf);
-    __syncthreads();
-    if (i == 0) {
-        int bad = 0;
-        for (int j = 0; j < K; j++) {
-            if (sel[j] < 0) { bad = 1; sel[j] = 0; }
-            sw[j] = score[(size_t)t * NE + sel[j]];
+    /* workgroups are dealt round-robin over the 8 XCDs: XCD x takes the contiguous tile range
+     * x * per .., expert tiles fastest, so the expert tiles that read one token tile's
+     * activations share one L2 */
+    const int ET = (NE + 31) >> 5, TT = (T + 31) >> 5, n = ET * TT * S, per = (int)(gridDim.x >> 3);
+    const int j = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (j >= n) return;
+    const int bx = j % ET, by = (j / ET) % TT, bz = j / (ET * TT);
+    const int lane = threadIdx.x, i = lane & 15, g = lane >> 4;
+    const int e0 = bx * 32, t0 = by * 32;
+    const int kb = bz * klen;
+    const uint16_t *wr[2];
+    const float *xr[2];
+#pragma unroll
+    for (int f = 0; f < 2; f++) {
+        const int e = min(e0 + 16 * f + i, NE - 1), t = min(t0 + 16 * f + i, T - 1);   /* past the end: discarded */
+        wr[f] = gate + (size_t)e * E + kb + 16 * g;
+        xr[f] = x + (size_t)t * E + kb + 16 * g;
+    }
+    g53_v4d acc[2][2] = {};
+    uint4 wa[2][2], wb[2][2];
+    float4 xa[2][4], xb[2][4];
+#define G53_RM32_LD(W, X, c) do { _Pragma("unroll") for (int f = 0; f < 2; f++) {                               \
+        W[f][0] = *(const uint4 *)(wr[f] + (c)); W[f][1] = *(const uint4 *)(wr[f] + (c) + 8);                   \
+        _Pragma("unroll") for (int q = 0; q < 4; q++) X[f][q] = *(const float4 *)(xr[f] + (c) + 4 * q); } } while (0)
+#define G53_RM32_MUL(W, X) do {                                                                                 \
+        _Pragma("unroll") for (int s = 0; s < 16; s++) {                                                        \
+            double a[2], b[2];                                                                                  \
+            _Pragma("unroll") for (int f = 0; f < 2; f++) {                                                     \
+                const uint32_t wd = ((const uint32_t *)&W[f][s >> 3])[(s & 7) >> 1];                            \
+                a[f] = (double)g53_bitsf((s & 1) ? (wd & 0xffff0000u) : (wd << 16));                            \
+                b[f] = (double)((const float *)&X[f][s >> 2])[s & 3];                                           \
+            }                                                                                                   \
+            _Pragma("unroll") for (int f = 0; f < 2; f++)                                                       \
+                _Pragma("unroll") for (int h = 0; h < 2; h++)                                                   \
+                    acc[f][h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[f], b[h], acc[f][h], 0, 0, 0);           \
+        } } while (0)
+    G53_RM32_LD(wa, xa, 0);
+    for (int c = 0; c < klen; c += 128) {
+        if (c + 64 < klen) G53_RM32_LD(wb, xb, c + 64);
+        G53_RM32_MUL(wa, xa);
+        if (c + 64 >= klen) break;
+        if (c + 128 < klen) G53_RM32_LD(wa, xa, c + 128);
+        G53_RM32_MUL(wb, xb);
+    }
+#undef G53_RM32_LD
+#undef G53_RM32_MUL
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int t = t0 + 16 * h + i;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int e = e0 + 16 * f + 4 * r + g;
+                if (t < T && e < NE) psum[((size_t)bz * T + t) * NE + e] = acc[f][h][r];
+            }
         }
-        if (bad && nan_flag) atomicOr(nan_flag, 1);
-        if (norm_topk) {
-            double s = 0.0;
-            for (int j = 0; j < K; j++) s += (double)sw[j];
-            for (int j = 0; j < K; j++) sw[j] = (float)((double)sw[j] / (s + 1e-20));
+}
+
+extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
+
+/* Top-k and weights of each token: one wave per token, four per workgroup, and the top-k as K
+ * rounds of arg-max over keys each lane holds sorted (the reference's rounds of "first
+ * strictly greater", src/core/glm53f_ops.c:957-969: the larger choice first, the lower index
+ * among equal ones, NaN and -inf never). With part != NULL the logits are first summed from
+ * the S column ranges in column order and the scores and choices written. A token with fewer
+ * than K selectable experts gets index 0 with expert 0's score in the missing slots and sets
+ * *nan_flag (the reference aborts there). Then the weights: the unbiased scores of the chosen
+ * experts, renormalised in double if norm_topk (:970-975), times routed_scale. When experts !=
+ * NULL the chosen experts' descriptors (and the shared expert's) are copied to slots[t][*], so
+ * the expert kernels find their matrices with one load. NE <= 64 * NV. */
+template <int NV>
+__global__ void __launch_bounds__(256) k_router_select_w(int *__restrict__ idx, float *__restrict__ w,
+                                                         float *__restrict__ score, float *__restrict__ choice,
+                                                         const double *__restrict__ part, int S,
+                                                         const float *__restrict__ bias, int T, int NE, int K,
+                                                         int norm_topk, float routed_scale,
+                                                         int *__restrict__ nan_flag,
+                                                         const G53hExpert *__restrict__ experts,
+                                                         const G53hExpert *__restrict__ shared,
+                                                         G53hExpert *__restrict__ slots)
+{
+    const int lane = threadIdx.x & 63;
+    const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (t >= T) return;
+    uint32_t key[NV];
+    int vid[NV];
+    float vsc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+        const int e = lane + 64 * v;
+        float sc = 0.0f, ch = -INFINITY;
+        if (e < NE) {
+            const size_t o = (size_t)t * NE + e;
+            if (part) {
+                double d = part[o];
+                for (int q = 1; q < S; q++) d = d + part[(size_t)q * T * NE + o];
+                sc = g53_sigmoidf((float)d);
+                ch = sc + bias[e];
+                score[o] = sc;
+                choice[o] = ch;
+            } else {
+                sc = score[o];
+                ch = choice[o];
+            }
         }
-        for (int j = 0; j < K; j++) {
-            idx[(size_t)t * K + j] = sel[j];
-            w[(size_t)t * K + j] = sw[j] * routed_scale;
+        key[v] = (ch > -INFINITY) ? g53_fkey(ch) : 0u;        /* 0: never chosen */
+        vid[v] = e;
+        vsc[v] = sc;
+    }
+    const float sc0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(vsc[0]), 0));   /* expert 0's */
+    /* each lane sorts its keys, largest first, the lower index first among equal keys */
+#pragma unroll
+    for (int pass = 0; pass < NV; pass++)
+#pragma unroll
+        for (int q = pass & 1; q + 1 < NV; q += 2) {
+            const bool sw_ = key[q + 1] > key[q];
+            const uint32_t k0 = key[q], k1 = key[q + 1];
+            const int i0 = vid[q], i1 = vid[q + 1];
+            const float s0 = vsc[q], s1 = vsc[q + 1];
+            key[q] = sw_ ? k1 : k0; key[q + 1] = sw_ ? k0 : k1;
+            vid[q] = sw_ ? i1 : i0; vid[q + 1] = sw_ ? i0 : i1;
+            vsc[q] = sw_ ? s1 : s0; vsc[q + 1] = sw_ ? s0 : s1;
         }
+    int pos = 0, my_e = 0;                                    /* lane j keeps round j's winner */
+    float my_s = sc0;
+    for (int j = 0; j < K; j++) {
+        const uint32_t m = __ockl_wfred_max_u32(key[0]);
+        if (m == 0) break;                                    /* fewer than K selectable */
+        const uint64_t cand = __ballot(key[0] == m);
+        int win;
+        if (__popcll(cand) == 1) win = (int)__builtin_ctzll(cand);
+        else win = (int)(__ockl_wfred_min_u32(key[0] == m ? (uint32_t)vid[0] : 0xffffffffu) & 63);
+        const int e = __builtin_amdgcn_readlane(vid[0], win);
+        const float ws = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(vsc[0]), win));
+        if (lane == j) { my_e = e; my_s = ws; }
+        const bool me = lane == win;                          /* the winner shifts its list */
+#pragma unroll
+        for (int q = 0; q + 1 < NV; q++) {
+            key[q] = me ? key[q + 1] : key[q];
+            vid[q] = me ? vid[q + 1] : vid[q];
+            vsc[q] = me ? vsc[q + 1] : vsc[q];
+        }
+        key[NV - 1] = me ? 0u : key[NV - 1];
+        pos++;
+    }
+    if (pos < K && lane == 0 && nan_flag) atomicOr(nan_flag, 1);
+    float wj = my_s;
+    if (norm_topk) {
+        double sum = 0.0;
+        for (int j = 0; j < K; j++) sum += (double)__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_s), j));
+        wj = (float)((double)my_s / (sum + 1e-20));
+    }
+    if (lane < K) {
+        idx[(size_t)t * K + lane] = my_e;
+        w[(size_t)t * K + lane] = wj * routed_scale;
     }
     if (experts) {
-        __syncthreads();
         const int nslots = K + (shared ? 1 : 0);
         const int words = (int)(sizeof(G53hExpert) / 4);
-        for (int q = i; q < nslots * words; q += blockDim.x) {
+        for (int q = lane; q < nslots * words; q += 64) {
             const int j = q / words, k = q % words;
-            const G53hExpert *src = j < K ? &experts[sel[j]] : shared;
+            const int ej = __shfl(my_e, j < K ? j : 0);
+            const G53hExpert *src = j < K ? &experts[ej] : shared;
             ((int *)&slots[(size_t)t * nslots + j])[k] = ((const int *)src)[k];
         }
     }
@@ -305,21 +434,6 @@ int g53h_resolve_slots(G53hExpert *slots, const G53hExpert *experts, const int *
                        experts, idx, shared, T, K, nslots);
     G53_LAUNCHED("k_resolve_slots");
     return 0;
-}
-
-/* The router logits of a split column range: the S partial sums of each (token, expert) added
- * in column order, then the sigmoid and the biased choice as in k_router_mfma. */
-__global__ void k_router_finish(float *__restrict__ score, float *__restrict__ choice,
-                                const double *__restrict__ part, const float *__restrict__ bias, int T, int NE,
-                                int S)
-{
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)T * NE) return;
-    double d = part[i];
-    for (int s = 1; s < S; s++) d = d + part[(long)s * T * NE + i];
-    const float v = g53_sigmoidf((float)d);
-    score[i] = v;
-    if (choice) choice[i] = v + bias[i % NE];
 }
 
 /* Library-owned buffer of the split router's partial sums (grown as needed, kept). */
@@ -353,7 +467,19 @@ int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate
     if (NE < 1 || NE > 1024) return g53h_fail("g53h_router: %d experts (max 1024)", NE);
     if (K < 1 || K > NE || K > GLM53F_MAX_TOPK_DEV) return g53h_fail("g53h_router: topk %d", K);
     float *score = scratch, *choice = scratch + (size_t)T * NE;
-    if (T >= 2 && gate_dt == 1 && E % 256 == 0) {           /* batches: the matrix-core form */
+    const double *psum = nullptr;                            /* split logits, summed by the selection */
+    int nsum = 1;
+    if (T >= G53_RM32_MINT && gate_dt == 1 && E % (64 * G53_RM32_S) == 0) {   /* large batches */
+        const int S = G53_RM32_S;
+        double *part = (double *)g53_router_part((size_t)S * T * NE * sizeof(double));
+        if (!part) return -1;
+        const unsigned n32 = (unsigned)(((NE + 31) / 32) * ((T + 31) / 32) * S + 7) / 8 * 8;
+        hipLaunchKernelGGL(k_router_mfma32, dim3(n32), dim3(64), 0, g53h_stream(), x, T, (const uint16_t *)gate, NE,
+                           E, E / S, S, part);
+        G53_LAUNCHED("k_router_mfma32");
+        psum = part;
+        nsum = S;
+    } else if (T >= 2 && gate_dt == 1 && E % 256 == 0) {    /* batches: the matrix-core form */
         /* few tiles (small T): the columns are split over up to 8 workgroups per tile so that
          * enough loads are in flight; the partial sums are added in column order after */
         const int tiles = ((NE + 15) / 16) * ((T + 15) / 16);
@@ -367,21 +493,21 @@ int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate
         hipLaunchKernelGGL(k_router_mfma, dim3((NE + 15) / 16, (T + 15) / 16, S), dim3(256), 0, g53h_stream(),
                            score, choice, x, T, (const uint16_t *)gate, bias, NE, E, E / S, part);
         G53_LAUNCHED("k_router_mfma");
-        if (S > 1) {
-            const long n = (long)T * NE;
-            hipLaunchKernelGGL(k_router_finish, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, g53h_stream(),
-                               score, choice, part, bias, T, NE, S);
-            G53_LAUNCHED("k_router_finish");
-        }
+        if (S > 1) { psum = part; nsum = S; }
     } else {
         hipLaunchKernelGGL(k_router_scores, dim3(NE, T), dim3(64), 0, g53h_stream(), score, choice, x, T, gate,
                            gate_dt, bias, NE, E);
         G53_LAUNCHED("k_router_scores");
     }
-    const int nthr = NE < 64 ? 64 : (NE > 1024 ? 1024 : (NE + 63) / 64 * 64);
-    hipLaunchKernelGGL(k_router_select, dim3(T), dim3(nthr), 0, g53h_stream(), idx, w, score, choice, NE, K,
-                       norm_topk, routed_scale, nan_flag, experts, shared, slots);
-    G53_LAUNCHED("k_router_select");
+    /* the selection, after the sum of the column ranges when the logits were split */
+    const dim3 gs((unsigned)((T + 3) / 4));
+    if (NE <= 320)
+        hipLaunchKernelGGL(k_router_select_w<5>, gs, dim3(256), 0, g53h_stream(), idx, w, score, choice, psum, nsum,
+                           bias, T, NE, K, norm_topk, routed_scale, nan_flag, experts, shared, slots);
+    else
+        hipLaunchKernelGGL(k_router_select_w<16>, gs, dim3(256), 0, g53h_stream(), idx, w, score, choice, psum, nsum,
+                           bias, T, NE, K, norm_topk, routed_scale, nan_flag, experts, shared, slots);
+    G53_LAUNCHED("k_router_select_w");
     return 0;
 }
 

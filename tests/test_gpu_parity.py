@@ -90,8 +90,10 @@ def test_matvec_known_answer_cases(L):
 
 
 def test_router_config2(L, c2layer):
+    """Batches on both matrix-core forms: 16 x 16 tiles (64, 256 tokens) and 32 x 32 tiles over
+    column ranges (600 tokens, a partial last tile; 2048, config 4)."""
     sp = c2layer.sp
-    for batch, T in [(0, 64), (5, 256)]:
+    for batch, T in [(0, 64), (5, 256), (7, 600), (6, 2048)]:
         say("router config 2", batch, T)
         x = S.x_host(sp, T, batch=batch)
         xd = DevBuf.from_array(x)
