@@ -84,13 +84,33 @@ typedef __attribute__((address_space(1))) const float g53_gflt;
 #define G53_GRP_ESPIN 2       /* a wait on the slice ring timed out                          */
 
 /* ------------------------------------------------------------------ planning ---- */
+/* meta[]: [0] tiles, [1] error flags, [2..17] the GEMMs' item counters, then the first item of
+ * each XCD's range (9 entries: XCD x takes items [b[x], b[x+1])) for gate/up and for down */
+#define G53_GRP_BGU   18
+#define G53_GRP_BDN   27
+
+/* Estimated cost of one row of a segment's items (one item per tile) with n positions, in
+ * tenths of the time of a tile of at most 64 positions. Measured item times at 1, 2, 3 and 4
+ * 32-position halves were 47, 51, 63 and 70 us: up to two halves the weight stream alone sets
+ * the time, beyond that the matrix work adds about a third per half. */
+__device__ __forceinline__ int g53_grp_tile_cost(int n)
+{
+    const int h = (n + 31) / 32;
+    return h <= 2 ? 10 : 10 + 3 * (h - 2) - (h == 4 ? 1 : 0);
+}
+__device__ __forceinline__ int g53_grp_seg_cost(int n)
+{
+    const int full = n / G53_GRP_NT, rem = n % G53_GRP_NT;
+    return full * g53_grp_tile_cost(G53_GRP_NT) + (rem ? g53_grp_tile_cost(rem) : 0);
+}
+
 /* Counting sort of the T*K (token, slot) pairs by expert, stable in token order. For each
  * chunk c of 64 tokens and expert e, mask[c][e] has bit t%64 set when token t chose e; the
  * position of (t, e) is off[e] + (tokens of e in earlier chunks) + popcount(mask bits below
  * t). One workgroup of 1024 threads; dynamic LDS sized by the host. */
 __global__ void __launch_bounds__(1024)
 k_grp_plan(const int *__restrict__ idx, int T, int K, int NE, int has_sh, int *__restrict__ tok_of,
-           int *__restrict__ pos_of, int4 *__restrict__ tiles, int *__restrict__ meta)
+           int *__restrict__ pos_of, int4 *__restrict__ tiles, int *__restrict__ meta, int mb_gu, int mb_dn)
 {
     extern __shared__ __attribute__((aligned(16))) uint64_t pl_lds[];
     const int nch = (T + 63) >> 6, nm = nch * NE, tid = threadIdx.x;
@@ -98,6 +118,7 @@ k_grp_plan(const int *__restrict__ idx, int T, int K, int NE, int has_sh, int *_
     int *pre = (int *)(mask + nm);                 /* [nch][NE]                              */
     int *off = pre + nm;                           /* [NE + 2]: segment offsets              */
     int *tb = off + NE + 2;                        /* [NE + 2]: first tile of each segment   */
+    int *pc = tb + NE + 2;                         /* [NE + 2]: cost of the segments before  */
     const int nseg = NE + (has_sh ? 1 : 0);
     for (int i = tid; i < nm; i += 1024) mask[i] = 0;
     __syncthreads();
@@ -122,21 +143,50 @@ k_grp_plan(const int *__restrict__ idx, int T, int K, int NE, int has_sh, int *_
     __syncthreads();
     /* exclusive scans of counts and tile counts by the first wave, 64 segments per round */
     if (tid < 64) {
-        int cp = 0, ct = 0;
+        int cp = 0, ct = 0, cc = 0;
         for (int b = 0; b < nseg; b += 64) {
             const int s = b + tid;
             const int n = s < nseg ? off[s] : 0;
-            int ip = n, it = (n + G53_GRP_NT - 1) / G53_GRP_NT;
+            const int c = g53_grp_seg_cost(n);
+            int ip = n, it = (n + G53_GRP_NT - 1) / G53_GRP_NT, ic = c;
             for (int d = 1; d < 64; d <<= 1) {
-                const int up = __shfl_up(ip, d), ut = __shfl_up(it, d);
-                if (tid >= d) { ip += up; it += ut; }
+                const int up = __shfl_up(ip, d), ut = __shfl_up(it, d), uc = __shfl_up(ic, d);
+                if (tid >= d) { ip += up; it += ut; ic += uc; }
             }
-            if (s < nseg) { off[s] = cp + ip - n; tb[s] = ct + it - (n + G53_GRP_NT - 1) / G53_GRP_NT; }
+            if (s < nseg) {
+                off[s] = cp + ip - n;
+                tb[s] = ct + it - (n + G53_GRP_NT - 1) / G53_GRP_NT;
+                pc[s] = cc + ic - c;
+            }
             cp += __shfl(ip, 63);
             ct += __shfl(it, 63);
+            cc += __shfl(ic, 63);
         }
-        if (tid == 0) { off[nseg] = cp; tb[nseg] = ct; meta[0] = ct; }
+        if (tid == 0) { off[nseg] = cp; tb[nseg] = ct; pc[nseg] = cc; meta[0] = ct; }
         if (tid < 16) meta[2 + tid] = 0;         /* the GEMMs' item counters */
+    }
+    __syncthreads();
+    /* each XCD's item range, of equal estimated cost: lanes 0-8 for gate/up, 16-24 for down */
+    if (tid < 32 && (tid & 15) <= 8) {
+        const int x = tid & 15, MB = tid < 16 ? mb_gu : mb_dn;
+        int item;
+        if (x == 0) item = 0;
+        else if (x == 8) item = tb[nseg] * MB;
+        else {
+            const long long tau = (long long)pc[nseg] * x / 8;   /* target, in units of one row of items */
+            int lo = 0, hi = nseg;                                /* the last segment with pc <= tau */
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (pc[mid] <= tau) lo = mid; else hi = mid - 1;
+            }
+            item = tb[lo] * MB;
+            if (lo < nseg) {
+                const int rc = pc[lo + 1] - pc[lo], nts = tb[lo + 1] - tb[lo];
+                const long long j = rc > 0 ? ((tau - pc[lo]) * MB) / rc : 0;   /* whole rows of items */
+                item += (int)(j < MB ? j : MB) * nts;
+            }
+        }
+        meta[(tid < 16 ? G53_GRP_BGU : G53_GRP_BDN) + x] = item;
     }
     __syncthreads();
     const int ps = K + 1;
@@ -424,17 +474,16 @@ struct G53GrpArgs {
 #define G53_GTRACE(k, v) do { if (a.trace && threadIdx.x == 0) a.trace[(size_t)blockIdx.x * 8 + (k)] = (v); } while (0)
 
 /* Item loc of the workgroup's group: the dispatcher deals workgroups round-robin over the 8
- * XCDs, so the workgroups of XCD x (blockIdx.x % 8 == x) share the items x*per .. x*per +
- * per - 1, which they claim in order from the group's counter. Items are numbered segment by
- * segment, and inside a segment row block by row block, all tiles of a block in a row: the
- * tiles of one expert that re-read the same weight rows run next to each other on one XCD
- * and find them in its L2. Returns false past the group's last item. */
-__device__ __forceinline__ bool g53_grp_item(const int4 *tiles, int ntile, int MB, int loc, int4 &tl, int &mb)
+ * XCDs, so the workgroups of XCD x (blockIdx.x % 8 == x) share the items blo .. bhi - 1 (a
+ * range of equal estimated cost, from the planner), which they claim in order from the
+ * group's counter. Items are numbered segment by segment, and inside a segment row block by
+ * row block, all tiles of a block in a row: the tiles of one expert that re-read the same
+ * weight rows run next to each other on one XCD and find them in its L2. Returns false past
+ * the group's last item. */
+__device__ __forceinline__ bool g53_grp_item(const int4 *tiles, int blo, int bhi, int MB, int loc, int4 &tl, int &mb)
 {
-    const int nitems = ntile * MB;
-    const int per = (nitems + 7) >> 3;
-    const int item = (blockIdx.x & 7) * per + loc;
-    if (loc >= per || item >= nitems) return false;
+    const int item = blo + loc;
+    if (item >= bhi) return false;
     const int w = tiles[item / MB].w;                    /* a tile of the item's segment */
     const int ts0 = w & 0xffff, nts = w >> 16;
     const int q = item - ts0 * MB;
@@ -464,13 +513,13 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
     if (threadIdx.x < 32) etab[threadIdx.x] = g53_exp2_tab_dev[threadIdx.x];
     if (threadIdx.x == 0) claim[0] = g53_grp_claim(ctr);
     if (blockIdx.x == 0 && threadIdx.x < 8) a.ctr[8 + threadIdx.x] = 0;   /* the down kernel's */
-    const int ntile = a.meta[0];
+    const int blo = a.meta[G53_GRP_BGU + (blockIdx.x & 7)], bhi = a.meta[G53_GRP_BGU + (blockIdx.x & 7) + 1];
     for (int kk = 0;; kk++) {
         __syncthreads();                     /* claim[] written; the previous item is done with LDS */
         int4 tl;
         int mb;
         G53_GTRACE(0, __builtin_amdgcn_s_memrealtime());
-        if (!g53_grp_item(a.tiles, ntile, a.I / (16 * NW), claim[kk & 1], tl, mb)) break;
+        if (!g53_grp_item(a.tiles, blo, bhi, a.I / (16 * NW), claim[kk & 1], tl, mb)) break;
         int nxt = 0;
         if (threadIdx.x == 0) nxt = g53_grp_claim(ctr);
         G53_GTRACE(4, (uint64_t)__smid() << 32 | (uint32_t)(tl.y << 8 | tl.z));
@@ -554,12 +603,12 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
     int *ctr = a.ctr + 8 + (blockIdx.x & 7);
     if (threadIdx.x == 0) claim[0] = g53_grp_claim(ctr);
     if (blockIdx.x == 0 && threadIdx.x < 8) a.ctr[threadIdx.x] = 0;        /* the gate/up kernel's */
-    const int ntile = a.meta[0];
+    const int blo = a.meta[G53_GRP_BDN + (blockIdx.x & 7)], bhi = a.meta[G53_GRP_BDN + (blockIdx.x & 7) + 1];
     for (int kk = 0;; kk++) {
         __syncthreads();                     /* claim[] written; the previous item is done with LDS */
         int4 tl;
         int mb;
-        if (!g53_grp_item(a.tiles, ntile, a.E / MR, claim[kk & 1], tl, mb)) break;
+        if (!g53_grp_item(a.tiles, blo, bhi, a.E / MR, claim[kk & 1], tl, mb)) break;
         int nxt = 0;
         if (threadIdx.x == 0) nxt = g53_grp_claim(ctr);
         const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
@@ -725,10 +774,11 @@ static int g53_grp_plan_pass(const float *x, int tc, const G53hMoeLayer *L, cons
     uint8_t *aq = (uint8_t *)p; p += al256((size_t)G53_GRP_NPA * P * I);
     float *contrib = (float *)p;
     const int nch = (tc + 63) / 64;
-    const size_t lds = (size_t)nch * NE * 12 + (size_t)(NE + 2) * 8;
+    const size_t lds = (size_t)nch * NE * 12 + (size_t)(NE + 2) * 12;
     if (lds > 160 * 1024) return g53h_fail("g53h_moe_grouped: %zu bytes of planner LDS", lds);
     if (lds > 65536) G53_TRY(hipFuncSetAttribute((const void *)k_grp_plan, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(k_grp_plan, dim3(1), dim3(1024), lds, st, idx, tc, K, NE, hs, tok_of, pos_of, tiles, meta);
+    hipLaunchKernelGGL(k_grp_plan, dim3(1), dim3(1024), lds, st, idx, tc, K, NE, hs, tok_of, pos_of, tiles, meta,
+                       I / (16 * G53_GRP_NW), E / (32 * G53_GRP_NW));
     G53_LAUNCHED("k_grp_plan");
     hipLaunchKernelGGL(k_grp_xq<G53_GRP_NPX>, dim3(tc), dim3(256), 0, st, x, E, tc, xq, xinv);
     G53_LAUNCHED("k_grp_xq");
