@@ -175,6 +175,7 @@ typedef double g53_v4d __attribute__((ext_vector_type(4)));
 #ifndef G53_RM32_S
 #define G53_RM32_S    8         /* column ranges of the large-batch router               */
 #endif
+static_assert(G53_RM32_S >= 1 && G53_RM32_S <= 8, "the selection sums at most 8 column ranges");
 #ifndef G53_RM32_MINT
 #define G53_RM32_MINT 512       /* tokens from which the large-batch router is used       */
 #endif
@@ -330,6 +331,31 @@ __global__ void __launch_bounds__(256) k_router_select_w(int *__restrict__ idx, 
     uint32_t key[NV];
     int vid[NV];
     float vsc[NV];
+    double d[NV];
+    if (part) {
+        const int ec = NE - 1;
+        if constexpr (NV <= 8) {                              /* every range's loads in flight at once */
+            double pv[8][NV];
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+#pragma unroll
+                for (int v = 0; v < NV; v++)
+                    pv[q][v] = part[((size_t)min(q, S - 1) * T + t) * NE + min(lane + 64 * v, ec)];
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                d[v] = pv[0][v];
+#pragma unroll
+                for (int q = 1; q < 8; q++)
+                    if (q < S) d[v] = d[v] + pv[q][v];
+            }
+        } else {                                              /* range by range: NV loads in flight */
+#pragma unroll
+            for (int v = 0; v < NV; v++) d[v] = part[(size_t)t * NE + min(lane + 64 * v, ec)];
+            for (int q = 1; q < S; q++)
+#pragma unroll
+                for (int v = 0; v < NV; v++) d[v] = d[v] + part[((size_t)q * T + t) * NE + min(lane + 64 * v, ec)];
+        }
+    }
 #pragma unroll
     for (int v = 0; v < NV; v++) {
         const int e = lane + 64 * v;
@@ -337,9 +363,7 @@ __global__ void __launch_bounds__(256) k_router_select_w(int *__restrict__ idx, 
         if (e < NE) {
             const size_t o = (size_t)t * NE + e;
             if (part) {
-                double d = part[o];
-                for (int q = 1; q < S; q++) d = d + part[(size_t)q * T * NE + o];
-                sc = g53_sigmoidf((float)d);
+                sc = g53_sigmoidf((float)d[v]);
                 ch = sc + bias[e];
                 score[o] = sc;
                 choice[o] = ch;
