@@ -129,17 +129,17 @@ __device__ __forceinline__ bool g53_desc_ok(const G53hExpert &e)
            e.gate.scols >= G53_DEC_NBE && e.up.scols >= G53_DEC_NBE && e.down.scols >= G53_DEC_NBI;
 }
 
-/* Router dot product of one bf16 row (8 KB) whose 128 bytes for this lane are in c[], x in LDS
- * (padded blocks): columns lane*64 .. lane*64+63, every product exact in double, summed in
+/* Router dot product of one bf16 row (8 KB) whose 128 bytes for this lane are in c[], x read
+ * from memory: columns lane*64 .. lane*64+63, every product exact in double, summed in
  * order per lane and then across the wave (the order of g53_router_dot). */
-__device__ __forceinline__ double g53_router_row(const g53_u4 (&c)[8], const float *xs, int lane)
+__device__ __forceinline__ double g53_router_row(const g53_u4 (&c)[8], const float *x, int lane)
 {
     double acc = 0.0;
     const uint32_t d[32] = {c[0].x, c[0].y, c[0].z, c[0].w, c[1].x, c[1].y, c[1].z, c[1].w,
                             c[2].x, c[2].y, c[2].z, c[2].w, c[3].x, c[3].y, c[3].z, c[3].w,
                             c[4].x, c[4].y, c[4].z, c[4].w, c[5].x, c[5].y, c[5].z, c[5].w,
                             c[6].x, c[6].y, c[6].z, c[6].w, c[7].x, c[7].y, c[7].z, c[7].w};
-    const float *xl = xs + (lane >> 1) * G53_PADB + (lane & 1) * 64;
+    const float *xl = x + 64 * lane;                     /* this lane's 64 columns of x */
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         const float4 xq = *(const float4 *)(xl + 4 * k);
@@ -513,6 +513,12 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
         const float4 v = ((const float4 *)a.x)[q];
         *(float4 *)(xs + (q >> 5) * G53_PADB + 4 * (q & 31)) = v;
     }
+    if (w < l.nR) {
+        /* the score of router row b + w G, published before the barrier: x is read straight
+         * from memory, so the routing does not wait for the other waves' staging */
+        const double d = g53_router_row(cr, a.x, lane);
+        if (lane == 0) g53_st_tag(a.score + b + w * G, g53_tag(a.epoch, g53_sigmoidf_tab((float)d, g53_exp2_tab_dev)));
+    }
     __syncthreads();
     if (threadIdx.x == 0 && hs && st[K].gate.w && !g53_desc_ok(st[K])) {
         st[K].gate.w = nullptr;                        /* unusable: flagged, contributes zero */
@@ -736,10 +742,6 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
         tw_comp += __builtin_amdgcn_s_memrealtime() - tc0;
         n_items++;
     };
-    if (w < l.nR) {                                    /* the score of router row b + w G */
-        const double d = g53_router_row(cr, xs, lane);
-        if (lane == 0) g53_st_tag(a.score + b + w * G, g53_tag(a.epoch, g53_sigmoidf_tab((float)d, etab)));
-    }
     if (w == G53_DEC_NT / 64 - 1) route();
     /* only a few waves stream before the routing is known, so that the loads, the
      * publications and the coherent reads of the routing are not queued behind a saturated
