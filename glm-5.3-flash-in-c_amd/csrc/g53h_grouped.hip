@@ -669,8 +669,16 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
  * src/core/glm53f_ops.c:1329-1340. Four consecutive d per thread. */
 __global__ void __launch_bounds__(256)
 k_grp_combine(float *__restrict__ out, const float *__restrict__ contrib, const float *__restrict__ wts,
-              const int *__restrict__ pos_of, int T, int E, int K, int has_sh)
+              const int *__restrict__ pos_of, int T, int E, int K, int has_sh, int *__restrict__ err,
+              int *__restrict__ meta)
 {
+    /* the pass's error flags into the library's, and the tile count and flags cleared for the
+     * next pass (every kernel that reads or sets them has finished) */
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (meta[1]) atomicOr(err, meta[1]);
+        meta[0] = 0;
+        meta[1] = 0;
+    }
     const long q = (long)blockIdx.x * 256 + threadIdx.x;
     if (q * 4 >= (long)T * E) return;
     const int t = (int)(q * 4 / E), d = (int)(q * 4 % E);
@@ -742,11 +750,6 @@ extern "C" int g53h_grouped_errors(void)
     if (g53h_check(hipMemcpy(&v, g_grp_err, 4, hipMemcpyDeviceToHost), "d2h", __FILE__, __LINE__)) return -1;
     if (v && g53h_check(hipMemset(g_grp_err, 0, 4), "memset", __FILE__, __LINE__)) return -1;
     return v;
-}
-
-__global__ void k_grp_errfold(int *err, int *meta)
-{
-    if (threadIdx.x == 0) { if (meta[1]) atomicOr(err, meta[1]); meta[0] = 0; meta[1] = 0; }
 }
 
 /* One planning pass of tc <= G53_GRP_MAXT tokens, in three phases: plan (sort, tiles, input
@@ -835,10 +838,8 @@ static int g53_grp_combine_pass(float *out, const float *wts)
     const int tc = g_pass.tc, E = g_pass.a.E;
     const long nq = (long)tc * E / 4;
     hipLaunchKernelGGL(k_grp_combine, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, out, g_pass.contrib, wts,
-                       g_pass.pos_of, tc, E, g_pass.K, g_pass.hs);
+                       g_pass.pos_of, tc, E, g_pass.K, g_pass.hs, g_grp_err, g_pass.meta);
     G53_LAUNCHED("k_grp_combine");
-    hipLaunchKernelGGL(k_grp_errfold, dim3(1), dim3(64), 0, st, g_grp_err, g_pass.meta);
-    G53_LAUNCHED("k_grp_errfold");
     g53h_prof_mark(G53_PROF_COMBINE);
     g_pass.active = 0;
     return 0;
