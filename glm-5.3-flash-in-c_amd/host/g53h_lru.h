@@ -1,19 +1,24 @@
 /* g53h_lru.h - bookkeeping of the HBM expert cache: which expert key (layer * n_experts +
- * expert) sits in which slot, LRU order, pins, reads in flight and the prefetch queue.
+ * expert) sits in which slot, the eviction order, pins, reads in flight and the prefetch queue.
  *
  * Pure C with no device calls, so the policy is testable on the CPU against the reference's
  * own cache (src/cache/glm53f_cache.c, compiled from its sources) on scripted traces. The
- * semantics restate the reference's:
- *   pick_victim   src/cache/glm53f_cache.c:55-66   (an EMPTY slot first, else the least
- *                                                   recently used one not pinned or in flight)
- *   reserve       src/cache/glm53f_cache.c:68-80
- *   land          src/cache/glm53f_cache.c:82-99
- *   get (hit)     src/cache/glm53f_cache.c:145-154
- *   release       src/cache/glm53f_cache.c:185-193
- *   hint          src/cache/glm53f_cache.c:251-293 (queue ordered by layer, stale entries of
- *                                                   layers below the floor and unlisted
- *                                                   entries of the hinted layer cancelled)
- *   pop           src/cache/glm53f_cache.c:299-306
+ * decisions are the reference's (src/cache/glm53f_cache.c:55-99 victim choice, reservation and
+ * landing; :145-154 hit; :185-193 release; :251-293 hint; :299-306 the reader's dequeue); the
+ * data structures are this file's own, sized for an HBM cache of thousands of slots:
+ *
+ *   victim choice   an EMPTY slot first, lowest index: a two-level bitmap, found in two
+ *                   count-trailing-zero steps; otherwise the least recently used slot that is
+ *                   neither pinned nor being filled: an indexed binary min-heap keyed by the
+ *                   slot's use stamp, holding exactly the resident, unpinned slots. A slot
+ *                   leaves the heap when it is pinned or chosen and re-enters when its last pin
+ *                   is released or its read lands, so every operation is O(log nslot) instead
+ *                   of a scan over all slots.
+ *   prefetch queue  one FIFO per layer (singly linked nodes from a fixed pool), read lowest
+ *                   layer first: appending a hint is O(1), cancelling a layer below the floor
+ *                   drops its whole list, and filtering the hinted layer's list by the new ids
+ *                   uses a per-expert mark instead of a search of the id list.
+ *
  * The caller serialises every call (one mutex in the device cache). */
 #ifndef G53H_LRU_H
 #define G53H_LRU_H
@@ -30,9 +35,21 @@ typedef struct {
     int32_t  *key_of;         /* [nslot] -> key, G53_LRU_EMPTY or G53_LRU_INFLIGHT        */
     int32_t  *pins;           /* [nslot] users; a pinned slot is never a victim           */
     unsigned char *prefetched;/* [nslot] filled by prefetch and not yet used              */
-    uint64_t *used_at;        /* [nslot] LRU stamp                                       */
+    uint64_t *used_at;        /* [nslot] use stamp                                       */
     uint64_t  clock;
-    int32_t  *queue;          /* prefetch keys, ordered by layer                          */
+    /* victims */
+    uint64_t *empty_w;        /* bit s: slot s is EMPTY                                   */
+    uint64_t *empty_s;        /* bit w: word w of empty_w is non-zero                     */
+    int32_t  *heap;           /* evictable slots, heap-ordered by used_at                 */
+    int32_t  *heap_at;        /* [nslot] position in heap, or -1                          */
+    int       heap_n;
+    /* prefetch queue */
+    int32_t  *q_key, *q_next; /* node pool [qcap]                                          */
+    int32_t  *q_head, *q_tail;/* [n_layers] per-layer lists, -1 when empty                 */
+    int32_t   q_free;         /* free-node list                                            */
+    int       q_lo;           /* no layer below q_lo has queued entries                    */
+    int32_t  *mark;           /* [n_experts] hint stamp of the ids being hinted            */
+    int32_t   mark_gen;
     int       qcap, qlen, hint_floor, last_hint;
     unsigned char *queued;    /* [n_layers * n_experts]                                  */
     uint64_t  hits, misses, evictions, prefetch_reads, bg_reads, bg_used;
@@ -40,6 +57,7 @@ typedef struct {
 
 int  g53_lru_init(G53hLru *c, int n_layers, int n_experts, int nslot, int qcap);
 void g53_lru_free(G53hLru *c);
+/* The slot the next reservation would take, or -1 when every slot is pinned or in flight. */
 int  g53_lru_pick_victim(const G53hLru *c);
 /* Slot reserved for key (marked in flight), or -1 when every slot is pinned or in flight. */
 int  g53_lru_reserve(G53hLru *c, int32_t key);
@@ -51,5 +69,7 @@ void g53_lru_release(G53hLru *c, int32_t key);
 void g53_lru_hint(G53hLru *c, int layer, const int *ids, int n);
 /* Next queued key that still needs a read (removed from the queue), or -1. */
 int32_t g53_lru_pop(G53hLru *c);
+/* The queued keys in the order they would be read; returns how many were written (<= cap). */
+int  g53_lru_queue(const G53hLru *c, int32_t *keys, int cap);
 
 #endif /* G53H_LRU_H */

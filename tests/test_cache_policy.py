@@ -59,6 +59,13 @@ def test_policy_matches_live_reference():
         out, st = lib_trace(ops, nslot)
         assert np.array_equal(out, want), seed
         assert np.array_equal(st, wst), seed
+    for seed in range(200, 206):                 # long traces: deep eviction heaps, long queues
+        nslot = [3, 5, 8, 12, 20, 30][seed % 6]
+        ops = CT.trace(seed, 80, nslot, True, seed % 2 == 0)
+        want, wst = MT.ref_trace(O.ref(), ops, nslot)
+        out, st = lib_trace(ops, nslot)
+        assert np.array_equal(out, want), seed
+        assert np.array_equal(st, wst), seed
 
 
 def test_lru_victim_order_closed_form():
