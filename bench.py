@@ -75,7 +75,7 @@ class Copies:
                 check(L.g53h_d2d(s.ptr, m.s, s.nbytes), "d2d")
                 copies.append((w, s, m))
                 self.keep += [w, s]
-            desc = G53hExpert(*[type(m)(w.ptr, s.ptr, m.rows, m.cols, m.br, m.bc, m.scols, 0)
+            desc = G53hExpert(*[type(m)(w.ptr, s.ptr, m.rows, m.cols, m.br, m.bc, m.scols, m.flags)
                                 for w, s, m in copies])
             dbuf = DevBuf.from_array(np.frombuffer(bytes(desc), np.uint8))
             self.keep += [router, dbuf]
@@ -421,6 +421,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--layout", default="tiled", choices=["tiled", "rowmajor"],
+                    help="expert code layout in HBM (config 2): octet-tiled (k_dec_tiled) or row-major (k_dec_layer)")
     a = ap.parse_args()
     if a.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (expert-parallel "
@@ -433,7 +435,9 @@ def main():
         return bench_stack(a)
     L = glm53h.init(0)
     sp = S.spec(2)
-    layer = S.DeviceLayer.build(sp)
+    tiled = a.layout == "tiled"
+    kname = "k_dec_tiled" if tiled else "k_dec_layer"
+    layer = S.DeviceLayer.build(sp, tiled=tiled)
     cp = Copies(layer)
     x = S.x_host(sp, NTOK, batch=0)
     xs = DevBuf.from_array(x)
@@ -463,7 +467,7 @@ def main():
     cnt = (C.c_int * 8)()
     check(L.g53h_prof_collect(tms, cnt, 8), "collect")
     check(L.g53h_prof_enable(0), "prof")
-    per = {name: (tms[i] / cnt[i] * 1e3 if cnt[i] else None) for i, name in [(7, "k_dec_layer_us")]}
+    per = {name: (tms[i] / cnt[i] * 1e3 if cnt[i] else None) for i, name in [(7, kname + "_us")]}
     errs = L.g53h_decode_errors()
     if errs:
         sys.exit(f"the decode kernels reported error flags {errs}")
@@ -473,12 +477,15 @@ def main():
     layer_bytes = layer.algorithmic_bytes(sp.K) + sp.E * 4 * 2           # + x in, out
     gbps = layer_bytes / (us_layer * 1e-6) / 1e9
     dom_bytes = (sp.K + 1) * eb + router_bytes                           # router, 8 routed + shared
-    dom_us = per["k_dec_layer_us"]
+    # the timed region launches exactly one kernel per step, back to back on one stream, so its
+    # per-step time is the kernel's average duration (the per-kernel events of the separate
+    # profiled run add a gap after every launch and are reported beside it)
+    dom_us = us_layer
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
     traffic = None                      # HBM bytes per launch from the committed counter summary
-    tp = os.path.join(ROOT, "profiles", "k_dec_layer_config2_traffic.json")
+    tp = os.path.join(ROOT, "profiles", f"{kname}_config2_traffic.json")
     if os.path.exists(tp):
         with open(tp) as f:
             traffic = json.load(f).get("traffic_bytes")
@@ -497,12 +504,13 @@ def main():
         "data": "synthetic (seeded FP8 E4M3 experts N(0,0.02) absmax-quantised per 128x128 block; bf16 x ~N(0,1))",
         "config": {"workload": "BASELINE config 2: single-token decode of one MoE layer, hidden 4096, "
                                "moe_inter 2048, 288 experts resident in HBM, top-8 + 1 shared",
-                   "tokens_cycled": NTOK, "router_shared_copies": NCOPY, "parallelism": "single GPU"},
+                   "tokens_cycled": NTOK, "router_shared_copies": NCOPY, "expert_layout": a.layout,
+                   "parallelism": "single GPU"},
         "hbm_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes_per_layer": layer_bytes,
         "kernels_us": {k: (round(v, 2) if v else v) for k, v in per.items()},
-        "roofline": {"bound": "hbm", "kernel": "k_dec_layer", "achieved": round(dom_gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(dom_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 2)},
         "cpu_baseline": cpu,

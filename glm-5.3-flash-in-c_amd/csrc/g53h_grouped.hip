@@ -463,7 +463,7 @@ struct G53GrpArgs {
     int T, P, E, I, NE;
     float limit, aq_scale, aq_inv;
     int partial;                   /* 1: experts without weights are outside this batch and
-                                      left alone, unless marked dropped (gate.pad_ == 1)    */
+                                      left alone, unless marked dropped (gate.flags & G53H_MAT_DROPPED)    */
     int *ctr;                      /* [16] item counters: 0-7 gate/up, 8-15 down; each
                                       kernel starts with its own at zero and clears the
                                       other kernel's                                      */
@@ -616,7 +616,7 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
         const int n = tl.z, pos0 = tl.y;
         const int i = lane & 31, g = lane >> 5;
         const bool present = ex && ex->gate.w != nullptr;
-        if (!present && a.partial && !(ex && ex->gate.pad_ == G53_DROPPED)) {   /* another batch */
+        if (!present && a.partial && !(ex && (ex->gate.flags & G53H_MAT_DROPPED))) {   /* another batch */
             if (tid == 0) claim[(kk + 1) & 1] = nxt;
             continue;
         }

@@ -5,8 +5,6 @@
 #include "g53h.h"
 
 #define GLM53F_MAX_TOPK_DEV 64
-/* G53hMat.pad_ of an expert's gate matrix: the expert failed to load (contributions zero). */
-#define G53_DROPPED 1
 
 int g53h_slot_mm_generic(float *y, const float *x, int T, int K, int nslots,
                          const G53hExpert *experts, const int *idx, const G53hExpert *shared,
@@ -19,6 +17,9 @@ int g53h_router_into(int *idx, float *w, const float *x, int T, const void *gate
                      int *nan_flag, float *scratch, const G53hExpert *experts, const G53hExpert *shared,
                      G53hExpert *slots);
 int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out);
+int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out);
+int g53h_decode_tiled_errors(void);
+int g53h_decode_tiled_grid(void);
 int g53h_grouped_use(const G53hMoeLayer *L, int T);
 int g53h_swiglu_split(float *y, const float *g, const float *u, long m, float limit);
 

@@ -176,7 +176,7 @@ k_down(float *__restrict__ contrib, const float *__restrict__ act, int E, int I,
             const double *pr = pw + lane * PST;
             for (int bb = 0; bb < NBLK; bb++) accd = accd + pr[bb];
             contrib[((size_t)t * nslots + s) * E + d] = (float)accd;
-        } else if (st[s].gate.pad_ == G53_DROPPED) {
+        } else if ((st[s].gate.flags & G53H_MAT_DROPPED)) {
             contrib[((size_t)t * nslots + s) * E + d] = 0.0f;
         }
     }
@@ -363,7 +363,7 @@ extern "C" int g53h_moe(float *out, const float *x, int T, const G53hMoeLayer *L
     if (T == 0) return 0;
     if (!L->router || !L->bias) return g53h_fail("g53h_moe: no router");
     if (T == 1) {                                    /* single-token decode: one fused launch */
-        const int r = g53h_decode_fused(out, x, L, idx_out, w_out);
+        const int r = L->tiled ? g53h_decode_tiled(out, x, L, idx_out, w_out) : g53h_decode_fused(out, x, L, idx_out, w_out);
         if (r <= 0) return r;
     }
     if (g53h_grouped_use(L, T)) return g53h_moe_grouped(out, x, T, L, idx_out, w_out);

@@ -88,7 +88,7 @@ __global__ void k_slot_mm_generic(float *__restrict__ y, const float *__restrict
     const float *xt = x + ((size_t)t * (x_per_slot ? nslots : 1) + (x_per_slot ? s : 0)) * cols;
     float v = 0.0f;
     if (e->gate.w) v = g53_row_dot(m, o, xt);
-    else if (e->gate.pad_ != G53_DROPPED) return;      /* absent from this batch */
+    else if (!(e->gate.flags & G53H_MAT_DROPPED)) return;      /* absent from this batch */
     y[((size_t)t * nslots + s) * rows + o] = v;
 }
 

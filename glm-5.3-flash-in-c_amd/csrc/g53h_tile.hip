@@ -1,0 +1,100 @@
+/* g53h_tile.hip - conversion of FP8 code matrices between the row-major layout of the
+ * checkpoint (src/io/glm53f_load.c:171-179 keeps experts row-major) and the octet-tiled layout
+ * the decode kernel streams (include/g53h.h, G53H_MAT_TILED).
+ *
+ * Output-major: thread q writes the 16-byte run q of the tiled matrix, whose bytes come from one
+ * row's 128-column block (16 codes 8 columns apart). The source block is read once per run
+ * through the caches; the conversion runs once per expert, when it enters HBM. */
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include "g53h.h"
+#include "g53h_runtime.h"
+
+namespace {
+
+/* Run q of the tiled matrix: unit q / 64 (row octet u / nb, block u % nb), row (q % 64) / 8 of
+ * the octet, run p = q % 8 holding accumulator a = g53h_tile_acc(p). */
+__host__ __device__ inline void g53_tile_run(int q, int nb, int &row, int &col0)
+{
+    const int u = q >> 6, l = q & 63, p = l & 7;
+    row = (u / nb) * 8 + (l >> 3);
+    col0 = (u % nb) * 128 + (((p & 1) << 2) | (p & 2) | (p >> 2));   /* g53h_tile_acc(p) */
+}
+
+__global__ void __launch_bounds__(256) k_tile_f8(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                 int cols, long nrun)
+{
+    const long q = (long)blockIdx.x * 256 + threadIdx.x;
+    if (q >= nrun) return;
+    int row, c0;
+    g53_tile_run((int)q, cols / 128, row, c0);
+    const uint8_t *s = src + (size_t)row * cols + c0;
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        w[k] = (uint32_t)s[32 * k] | ((uint32_t)s[32 * k + 8] << 8) | ((uint32_t)s[32 * k + 16] << 16) |
+               ((uint32_t)s[32 * k + 24] << 24);
+    *(uint4 *)(dst + 16 * q) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__global__ void __launch_bounds__(256) k_untile_f8(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                   int cols, long nrun)
+{
+    const long q = (long)blockIdx.x * 256 + threadIdx.x;
+    if (q >= nrun) return;
+    int row, c0;
+    g53_tile_run((int)q, cols / 128, row, c0);
+    const uint4 v = *(const uint4 *)(src + 16 * q);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint8_t *d = dst + (size_t)row * cols + c0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) d[8 * i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+}
+
+int g53_tile_shape(int rows, int cols)
+{
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128)
+        return g53h_fail("g53h_tile_f8: a %d x %d matrix cannot be octet-tiled (rows a multiple of 8, "
+                         "columns of 128)", rows, cols);
+    return 0;
+}
+
+} /* namespace */
+
+extern "C" int g53h_tile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols)
+{
+    if (g53h_ready() || g53_tile_shape(rows, cols)) return -1;
+    if (dst_d == src_d) return g53h_fail("g53h_tile_f8: in-place conversion is not supported");
+    const long nrun = (long)rows * cols / 16;
+    hipLaunchKernelGGL(k_tile_f8, dim3((unsigned)((nrun + 255) / 256)), dim3(256), 0, g53h_stream(), dst_d, src_d,
+                       cols, nrun);
+    G53_LAUNCHED("k_tile_f8");
+    return 0;
+}
+
+extern "C" int g53h_untile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols)
+{
+    if (g53h_ready() || g53_tile_shape(rows, cols)) return -1;
+    if (dst_d == src_d) return g53h_fail("g53h_untile_f8: in-place conversion is not supported");
+    const long nrun = (long)rows * cols / 16;
+    hipLaunchKernelGGL(k_untile_f8, dim3((unsigned)((nrun + 255) / 256)), dim3(256), 0, g53h_stream(), dst_d,
+                       src_d, cols, nrun);
+    G53_LAUNCHED("k_untile_f8");
+    return 0;
+}
+
+extern "C" int g53h_tile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse)
+{
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128 || dst == src) return -1;
+    const long nrun = (long)rows * cols / 16;
+    for (long q = 0; q < nrun; q++) {
+        int row, c0;
+        g53_tile_run((int)q, cols / 128, row, c0);
+        for (int i = 0; i < 16; i++) {
+            if (inverse) dst[(size_t)row * cols + c0 + 8 * i] = src[16 * q + i];
+            else dst[16 * q + i] = src[(size_t)row * cols + c0 + 8 * i];
+        }
+    }
+    return 0;
+}

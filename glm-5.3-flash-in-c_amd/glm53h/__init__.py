@@ -30,7 +30,7 @@ class G53hError(RuntimeError):
 # ----------------------------------------------------------------- structs (g53h.h) ----
 class G53hMat(C.Structure):
     _fields_ = [("w", C.c_void_p), ("s", C.c_void_p), ("rows", C.c_int), ("cols", C.c_int),
-                ("br", C.c_int), ("bc", C.c_int), ("scols", C.c_int), ("pad_", C.c_int)]
+                ("br", C.c_int), ("bc", C.c_int), ("scols", C.c_int), ("flags", C.c_int)]
 
 
 class G53hExpert(C.Structure):
@@ -42,7 +42,7 @@ class G53hMoeLayer(C.Structure):
                 ("topk", C.c_int), ("norm_topk", C.c_int), ("routed_scale", C.c_float),
                 ("swiglu_limit", C.c_float), ("router", C.c_void_p), ("router_dt", C.c_int),
                 ("bias", C.c_void_p), ("experts", C.c_void_p), ("shared", C.c_void_p),
-                ("block_c", C.c_int)]
+                ("block_c", C.c_int), ("tiled", C.c_int)]
 
 
 # -------------------------------------------------------------- structs (glm53f.h) ----
@@ -166,6 +166,10 @@ _SIGS = {
     "g53h_decode_errors": (C.c_int, []),
     "g53h_decode_grid": (C.c_int, []),
     "g53h_set_decode_trace": (C.c_int, [C.c_void_p]),
+    "g53h_set_tiled_decode_trace": (C.c_int, [C.c_void_p]),
+    "g53h_tile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
+    "g53h_untile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
+    "g53h_tile_f8_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "g53h_expf": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_expf_range": (C.c_int, [C.c_void_p, C.c_uint32, C.c_size_t]),
     "g53h_expf_host": (None, [C.c_void_p, C.c_void_p, C.c_size_t]),

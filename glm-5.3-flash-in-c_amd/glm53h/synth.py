@@ -128,9 +128,14 @@ class DeviceLayer:
     router_f32: np.ndarray = None
     bias_f32: np.ndarray = None
 
+    tiled: bool = False
+
     @classmethod
-    def build(cls, sp: LayerSpec, n_experts_present=None):
+    def build(cls, sp: LayerSpec, n_experts_present=None, tiled=False):
+        """tiled: store every expert's codes octet-tiled (G53H_MAT_TILED), the layout the decode
+        kernel k_dec_tiled streams; the values are the same seeded codes either way."""
         self = cls(sp)
+        self.tiled = bool(tiled)
         E, I, NE = sp.E, sp.I, sp.NE
         shapes = _mat_shapes(sp)
         code_off, sc_off, off = [], [], 0
@@ -145,15 +150,19 @@ class DeviceLayer:
         self.arena = DevBuf(self.slot_bytes * nslots)
         L = lib()
         descs = (G53hExpert * (NE + 1))()
+        stage = DevBuf(max(r * c for r, c in shapes)) if self.tiled else None
         for i in range(nslots):
             base = self.arena.ptr + i * self.slot_bytes
             mats = []
             for m, (r, c) in enumerate(shapes):
                 strm = stream(K_SHARED, sp.layer, m) if i == NE else stream(K_EXPERT, sp.layer, i * 3 + m)
                 w, s = base + code_off[m], base + sc_off[m]
-                check(L.g53h_synth_f8(w, s, r, c, sp.br, sp.bc, sp.seed, strm, C.c_float(sp.expert_sigma)),
+                gen = stage.ptr if self.tiled else w
+                check(L.g53h_synth_f8(gen, s, r, c, sp.br, sp.bc, sp.seed, strm, C.c_float(sp.expert_sigma)),
                       "g53h_synth_f8")
-                mats.append(G53hMat(w, s, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, 0))
+                if self.tiled:
+                    check(L.g53h_tile_f8(w, gen, r, c), "g53h_tile_f8")
+                mats.append(G53hMat(w, s, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, 2 if self.tiled else 0))
             descs[i] = G53hExpert(*mats)
         self.experts = descs
         self.table = DevBuf.from_array(np.frombuffer(bytes(descs), np.uint8))
@@ -167,8 +176,9 @@ class DeviceLayer:
             routed_scale=sp.routed_scale, swiglu_limit=sp.limit, router=self.router.ptr, router_dt=1,
             bias=self.bias.ptr, experts=self.table.ptr,
             shared=(self.table.ptr + NE * C.sizeof(G53hExpert)) if sp.shared else None,
-            block_c=sp.bc)
+            block_c=sp.bc, tiled=1 if self.tiled else 0)
         check(L.g53h_sync(), "g53h_sync")
+        del stage
         return self
 
     def fetch_expert(self, e):
@@ -180,6 +190,10 @@ class DeviceLayer:
             s = np.empty(((m.rows + m.br - 1) // m.br) * m.scols, np.float32)
             check(lib().g53h_d2h(w.ctypes.data, m.w, w.nbytes), "d2h")
             check(lib().g53h_d2h(s.ctypes.data, m.s, s.nbytes), "d2h")
+            if m.flags & 2:                       # tiled in HBM: the row-major codes for the oracle
+                rm = np.empty_like(w)
+                assert lib().g53h_tile_f8_host(rm.ctypes.data, w.ctypes.data, m.rows, m.cols, 1) == 0
+                w = rm
             out.append((w, s))
         return out
 

@@ -592,7 +592,7 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
                 glm53f_expert_drops++;
                 fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this output is CORRUPT\n",
                         w->layer, e);
-                table[e].gate.pad_ = 1;           /* dropped: its contributions are zero */
+                table[e].gate.flags = G53H_MAT_DROPPED;           /* dropped: its contributions are zero */
                 continue;
             }
             held[nh++] = e;

@@ -48,18 +48,38 @@ int         g53h_prof_collect(float *ms, int *count, int ntags);
 int         g53h_mem_info(size_t *free_b, size_t *total_b);
 
 /* -------------------------------------------------------------- FP8 matrices ---- */
-/* One FP8 E4M3 matrix in HBM: codes w [rows][cols] row-major, fp32 block scales s
- * [ceil(rows/br)][scols], scols = ceil(cols/bc). Field order mirrors Glm53fMat. */
+/* One FP8 E4M3 matrix in HBM: codes w, fp32 block scales s [ceil(rows/br)][scols],
+ * scols = ceil(cols/bc). Field order mirrors Glm53fMat.
+ *
+ * Code layouts (flags bit G53H_MAT_TILED):
+ *   row-major   w[r * cols + c];
+ *   octet-tiled (rows a multiple of 8, cols of 128, 128 x 128 blocks): the matrix is cut into
+ *               units of 8 rows x 128 columns (1 KB), stored unit (r / 8, c / 128) at byte
+ *               ((r / 8) * (cols / 128) + c / 128) * 1024, so one row octet's units follow
+ *               each other. Inside a unit, row r % 8 holds 128 bytes: eight 16-byte runs, run
+ *               p holding columns a, a + 8, ..., a + 120 of the block (a = g53h_tile_acc(p)).
+ *               One 64-lane load of 16 bytes per lane then reads a unit whole, and each lane
+ *               receives exactly the codes of one of the reference's eight per-block fp32
+ *               accumulators of one row (src/core/glm53f_ops.c:185-228), in order. */
+#define G53H_MAT_DROPPED 1      /* on an expert's gate: the expert failed to load             */
+#define G53H_MAT_TILED   2      /* codes in the octet-tiled layout                            */
 typedef struct {
     const uint8_t *w;
     const float   *s;
     int rows, cols, br, bc, scols;
-    int pad_;
+    int flags;
 } G53hMat;
 
+/* Accumulator (column offset within a 128-column block, 0..7) held by 16-byte run p of a row in
+ * a tiled unit: runs 0-3 are accumulators 0, 4, 2, 6 and runs 4-7 are 1, 5, 3, 7, so that the
+ * reference's pairwise tree ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) joins neighbours,
+ * then pairs of neighbours, then the two halves. */
+static inline int g53h_tile_acc(int p) { return ((p & 1) << 2) | (p & 2) | (p >> 2); }
+
 /* One expert: gate [I][E], up [I][E], down [E][I]. A NULL gate.w marks an expert that
- * is not there: with gate.pad_ == 1 it could not be loaded (its contributions are zero, as
- * the reference's drop path); otherwise it is outside the current batch (g53h_moe_partial). */
+ * is not there: with G53H_MAT_DROPPED in gate.flags it could not be loaded (its contributions
+ * are zero, as the reference's drop path); otherwise it is outside the current batch
+ * (g53h_moe_partial). */
 typedef struct {
     G53hMat gate, up, down;
 } G53hExpert;
@@ -94,6 +114,8 @@ typedef struct {
     const G53hExpert *shared;       /* device pointer to one descriptor, or NULL           */
     int               block_c;      /* FP8 column block of every expert matrix (128 takes the
                                        tiled kernels; any other value the generic ones)     */
+    int               tiled;        /* 1: every expert matrix (routed and shared) is in the
+                                       octet-tiled layout (G53H_MAT_TILED), 0: row-major     */
 } G53hMoeLayer;
 
 /* Whole MoE layer on the device (replaces src/core/glm53f_ops.c:1144-1342 moe_chunk with
@@ -111,7 +133,7 @@ int g53h_moe_routed_given(float *out_d, const float *x_d, int T, const G53hMoeLa
 /* Partial layer for a host driver that fetches experts in batches (the drop-in path):
  * contributions of the slots whose expert descriptor is present go to contrib_d
  * [T][topk + has_shared][hidden]; slots whose descriptor has gate.w == NULL are left
- * untouched, except that a descriptor with gate.pad_ == 1 (a dropped expert) writes zeros.
+ * untouched, except that a descriptor marked G53H_MAT_DROPPED (a dropped expert) writes zeros.
  * g53h_moe_combine then forms out = (float)(sum_j w_j contrib_j in double) (+ shared). */
 int g53h_moe_partial(float *contrib_d, const float *x_d, int T, const G53hMoeLayer *L,
                      const int *idx_d);
@@ -137,7 +159,7 @@ int g53h_moe_grouped(float *out_d, const float *x_d, int T, const G53hMoeLayer *
  * begin plans T <= g53h_grouped_max_tokens(L) tokens with the routing given (idx_d
  * [T][topk]) and splits x; each batch call multiplies the experts whose descriptors in
  * L->experts (and L->shared) are present, leaves the others for other batches, and gives zero
- * contributions to descriptors marked dropped (gate.w == NULL, gate.pad_ == 1); end combines
+ * contributions to descriptors marked dropped (gate.w == NULL, G53H_MAT_DROPPED); end combines
  * into out_d with the weights w_d [T][topk]. Between begin and end the library's workspace
  * holds the pass: no other g53h layer call may run in between (copies may). */
 int g53h_grouped_max_tokens(const G53hMoeLayer *L);   /* 0: the layer's shapes do not qualify */
@@ -152,8 +174,9 @@ int g53h_grouped_errors(void);
 int g53h_set_grouped_trace(void *dev_buf);
 
 /* Single-token decode runs as one persistent launch when the layer has the released shapes
- * (hidden 4096, inter 2048, 128x128 blocks, topk <= 15); g53h_set_fused_decode(0) selects the
- * multi-kernel path instead (returns the previous setting). g53h_decode_errors waits for the
+ * (hidden 4096, inter 2048, 128x128 blocks, topk <= 15): k_dec_tiled for a layer whose experts
+ * are octet-tiled (L->tiled), k_dec_layer for row-major ones; g53h_set_fused_decode(0) selects
+ * the multi-kernel path instead (returns the previous setting). g53h_decode_errors waits for the
  * stream and returns, then clears, the fused kernel's error flags (1: a grid wait timed out,
  * 2: a token had fewer than topk selectable experts, 8: an unusable expert descriptor, which
  * then contributes zero), 0 if none. g53h_decode_grid returns the
@@ -164,6 +187,15 @@ int g53h_decode_grid(void);
 /* Diagnostics: with dev_buf != NULL (device, grid x 32 uint64), the fused kernel's workgroups
  * record 100 MHz timestamps at their phase boundaries; NULL turns it off. */
 int g53h_set_decode_trace(void *dev_buf);
+int g53h_set_tiled_decode_trace(void *dev_buf);   /* the same for the octet-tiled kernel   */
+
+/* ------------------------------------------------------------- code layouts ---- */
+/* Row-major FP8 codes [rows][cols] -> octet-tiled (see G53hMat), and back; stream-ordered on
+ * the compute stream, dst and src distinct, rows a multiple of 8 and cols of 128. The host
+ * twin converts in host memory (inverse != 0: tiled -> row-major). */
+int g53h_tile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols);
+int g53h_untile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols);
+int g53h_tile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse);
 
 /* -------------------------------------------------------- checks and inputs ---- */
 /* y[i] = expf(x[i]) by the device restatement of glibc's expf (for exhaustive checks). */

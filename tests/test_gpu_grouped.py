@@ -167,7 +167,7 @@ def test_grouped_absent_expert_contributes_zero(L):
     descs = (S.G53hExpert * (sp.NE + 1))()
     C.memmove(descs, layer.experts, C.sizeof(descs))
     descs[drop].gate.w = None
-    descs[drop].gate.pad_ = 1
+    descs[drop].gate.flags = 1
     tab = DevBuf.from_array(np.frombuffer(bytes(descs), np.uint8))
     lay = S.G53hMoeLayer()
     C.memmove(C.byref(lay), C.byref(layer.layer), C.sizeof(lay))

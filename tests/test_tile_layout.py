@@ -1,0 +1,62 @@
+"""The octet-tiled code layout on the CPU (host twin of the conversion kernels): the conversion
+round-trips, and every 16-byte run of a unit holds the codes one of the reference's eight fp32
+accumulators of a 128-column block consumes, in the order it consumes them
+(src/core/glm53f_ops.c:197-205: accumulator l takes columns l, l + 8, ..., l + 120)."""
+import numpy as np
+
+import glm53h
+
+
+def tile(a, rows, cols, inverse=0):
+    out = np.empty_like(a)
+    assert glm53h.lib().g53h_tile_f8_host(out.ctypes.data, a.ctypes.data, rows, cols, inverse) == 0
+    return out
+
+
+def test_round_trip():
+    rng = np.random.default_rng(1)
+    for rows, cols in [(8, 128), (16, 256), (40, 640)]:
+        a = rng.integers(0, 256, rows * cols, dtype=np.uint8)
+        t = tile(a, rows, cols)
+        assert not np.array_equal(t, a)
+        assert np.array_equal(tile(t, rows, cols, 1), a)
+
+
+def test_runs_are_accumulator_columns_in_order():
+    rows, cols = 16, 256
+    col = np.tile(np.arange(cols, dtype=np.int64), rows)
+    row = np.repeat(np.arange(rows, dtype=np.int64), cols)
+    for name, code in (("column", col % 256), ("row", row)):
+        t = tile(code.astype(np.uint8), rows, cols)
+        units = t.reshape(rows // 8, cols // 128, 8, 8, 16)      # octet, block, row, run, code
+        for o8 in range(rows // 8):
+            for b in range(cols // 128):
+                for r in range(8):
+                    accs = set()
+                    for p in range(8):
+                        run = units[o8, b, r, p].astype(np.int64)
+                        if name == "row":
+                            assert np.all(run == o8 * 8 + r)
+                            continue
+                        c = run - b * 128 if b * 128 < 256 else run
+                        assert np.all(np.diff(c) == 8)             # consecutive columns of one accumulator
+                        assert 0 <= c[0] < 8
+                        accs.add(int(c[0]))
+                        assert c[0] == glm53h_tile_acc(p)
+                    if name == "column":
+                        assert accs == set(range(8))
+
+
+def glm53h_tile_acc(p):
+    """The pairing of include/g53h.h: runs 0-3 accumulators 0 4 2 6, runs 4-7 1 5 3 7, so that
+    the tree ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) pairs runs p and p ^ 1, then p and
+    p ^ 2, then the two halves."""
+    return [0, 4, 2, 6, 1, 5, 3, 7][p]
+
+
+def test_tree_pairing():
+    acc = [glm53h_tile_acc(p) for p in range(8)]
+    level1 = {frozenset((acc[p], acc[p ^ 1])) for p in range(8)}
+    assert level1 == {frozenset(s) for s in ((0, 4), (2, 6), (1, 5), (3, 7))}
+    level2 = {frozenset(acc[q] for q in range(8) if q >> 2 == p >> 2) for p in range(8)}
+    assert level2 == {frozenset((0, 4, 2, 6)), frozenset((1, 5, 3, 7))}
