@@ -110,6 +110,7 @@ struct G53LayerArgs {
     int NE, K, norm_topk;
     unsigned epoch;
     float routed_scale, limit;
+    int spin;                      /* polls before a wait on another workgroup gives up */
     g53_u64 *trace;                /* optional: [grid][32] timestamps and counters       */
 };
 
@@ -331,10 +332,10 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
         int n_polls = 0;
         if (a.NE <= 64 * 5)
             ok = g53_route_wave<5>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx, sw, kbuf, ebuf,
-                                   a.err, lane, t_seen, n_polls, t_tau, t_rank);
+                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin);
         else
             ok = g53_route_wave<G53_DEC_MAXNE / 64>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx,
-                                                    sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank);
+                                                    sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin);
         if (a.trace && lane == 0) { a.trace[(size_t)blockIdx.x * 32 + 15] = t_seen; a.trace[(size_t)blockIdx.x * 32 + 7] = n_polls; a.trace[(size_t)blockIdx.x * 32 + 1] = t_tau; a.trace[(size_t)blockIdx.x * 32 + 9] = t_rank; }
         if (!ok) {                                     /* scores missing: no routed slots */
             if (lane == 0) g53_flag_err(a.err, 1);
@@ -427,7 +428,7 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
                 const __amdgpu_buffer_rsrc_t rsrc = g53_rsrc(a.act + (size_t)it.s * G53_DEC_I + it.r * 1024);
                 int spins = 0;
                 while (__ballot(pending != 0)) {
-                    if (++spins > G53_SPIN_LIMIT) { if (lane == 0) g53_flag_err(a.err, 1); break; }
+                    if (++spins > a.spin) { if (lane == 0) g53_flag_err(a.err, 1); break; }
 #pragma unroll
                     for (int h = 0; h < 16; h += 4) {
                         g53_u64 t[4];
@@ -594,7 +595,6 @@ __global__ void __launch_bounds__(G53_DEC_NT, 1) k_dec_layer(G53LayerArgs a)
 /* ------------------------------------------------------------------ host side ---- */
 static int g_dec_grid1 = -1;             /* workgroups of k_dec_layer, 0 = unavailable     */
 static unsigned g_dec_epoch = 0;         /* epoch of the last launch                        */
-static int *g_dec_state = nullptr;       /* [0] error flags                                 */
 static void *g_dec_buf = nullptr;        /* tagged scores | tagged activations              */
 static size_t g_dec_buf_bytes = 0;
 static int g_dec_enabled = 1;
@@ -636,11 +636,6 @@ int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *id
             /* every workgroup owns at most G53_DEC_MAXRG row groups */
             if ((G53_DEC_NGRP + g_dec_grid1 - 1) / g_dec_grid1 > G53_DEC_MAXRG) g_dec_grid1 = 0;
         }
-        if (g_dec_grid1 && (hipMalloc((void **)&g_dec_state, 256) != hipSuccess ||
-                            hipMemset(g_dec_state, 0, 256) != hipSuccess)) {
-            (void)hipGetLastError();
-            g_dec_grid1 = 0;
-        }
     }
     if (!g_dec_grid1) return 1;
     /* tagged scores [MAXNE] | tagged act [ROT][MAXK + 1][I], allocated and cleared once, so
@@ -668,9 +663,9 @@ int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *id
     e.experts = L->experts; e.shared = L->shared;
     e.score = (g53_u64 *)buf;
     e.act = (g53_u64 *)(buf + off_act + (g_dec_epoch % G53_DEC_ROT) * act_copy);
-    e.err = g_dec_state; e.idx_out = idx_out; e.w_out = w_out;
+    e.err = g53h_errblock(); e.idx_out = idx_out; e.w_out = w_out;
     e.NE = NE; e.K = K; e.norm_topk = L->norm_topk; e.epoch = g_dec_epoch;
-    e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dec_trace;
+    e.spin = g53h_spin_limit(); e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dec_trace;
     g53h_prof_mark(G53_PROF_START);
     hipLaunchKernelGGL(k_dec_layer, dim3(g_dec_grid1), dim3(G53_DEC_NT), 0, g53h_stream(), e);
     G53_LAUNCHED("k_dec_layer");
@@ -681,15 +676,11 @@ int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *id
 extern "C" int g53h_decode_errors(void)
 {
     if (g53h_ready()) return 0;
-    const int et = g53h_decode_tiled_errors();
-    if (et < 0) return -1;
-    if (!g_dec_state) return et;
-    int e = et;
+    int e[2] = {0, 0};
     if (hipStreamSynchronize(g53h_stream()) != hipSuccess) return -1;
-    int e1 = 0;
-    if (hipMemcpy(&e1, g_dec_state, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return -1;
-    if (e1) (void)hipMemset(g_dec_state, 0, sizeof(int));
-    return e | e1;
+    if (hipMemcpy(e, g53h_errblock(), sizeof e, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if ((e[0] | e[1]) && hipMemset(g53h_errblock(), 0, sizeof e) != hipSuccess) return -1;
+    return e[0] | e[1];
 }
 
 extern "C" int g53h_decode_grid(void) { return g_dec_grid1; }

@@ -77,9 +77,12 @@ struct G53TiledArgs {
     int *err;
     int *idx_out;
     float *w_out;
+    const int *idx_in;             /* the routing when the caller has done it (or NULL)   */
+    const float *w_in;
     int NE, K, norm_topk;
     unsigned epoch;
     float routed_scale, limit;
+    int spin;                      /* polls before a wait on another workgroup gives up */
     g53_u64 *trace;                /* optional: [grid][32] timestamps                    */
 };
 
@@ -241,7 +244,6 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
     __shared__ float sw[64];
     __shared__ int sidx[16], ebuf[64];
     __shared__ uint32_t kbuf[64];
-    __shared__ float fbuf[64];
     __shared__ uint64_t etab[32];
     __shared__ int qctr, ndone, routed, inited, gdone;
 
@@ -256,7 +258,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
      * activations */
     const int ng = 2 * n_go, nd = (n_do + 1) >> 1, nslot = hs + K;
     int n_task = 0;
-    const int nR = a.NE > b ? (a.NE - 1 - b) / G + 1 : 0;
+    const int nR = a.idx_in ? 0 : (a.NE > b ? (a.NE - 1 - b) / G + 1 : 0);
     const int words = (int)(sizeof(G53hExpert) / 4);
 #ifdef G53_DT_NOSTAGE
     const bool dstage = false;
@@ -332,18 +334,23 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
 
     /* the routing: top-k, weights, the chosen descriptors (reference :945-976) */
     if (w == G53_DT_NW - 1) {
-        for (int e = lane; e < a.NE; e += 64) biasl[e] = a.bias[e];
+        if (!a.idx_in)
+            for (int e = lane; e < a.NE; e += 64) biasl[e] = a.bias[e];
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_wave_barrier();
         g53_u64 t_seen = 0, t_tau = 0, t_rank = 0;
         int n_polls = 0;
-        bool ok;
-        if (a.NE <= 64 * 5)
+        bool ok = true;
+        if (a.idx_in) {                               /* routed by the caller */
+            if (lane < K) { sidx[lane] = a.idx_in[lane]; sw[lane] = a.w_in[lane]; }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+        } else if (a.NE <= 64 * 5)
             ok = g53_route_wave<5>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx, sw, kbuf, ebuf,
-                                   a.err, lane, t_seen, n_polls, t_tau, t_rank);
+                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin);
         else
             ok = g53_route_wave<G53_DEC_MAXNE / 64>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch,
-                                                    sidx, sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank);
+                                                    sidx, sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin);
         if (!ok) {                                    /* scores missing: no routed slots */
             if (lane == 0) g53_flag_err(a.err, 1);
             if (lane < K) { sidx[lane] = -1; sw[lane] = 0.0f; }
@@ -355,7 +362,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
         G53_CBAR();
         if (lane == 0) g53_lds_add(&routed, 1);
         __builtin_amdgcn_s_setprio(0);
-        if (b == 0 && lane < K) {
+        if (b == 0 && lane < K && !a.idx_in) {
             if (a.idx_out) a.idx_out[lane] = sidx[lane];
             if (a.w_out) a.w_out[lane] = sw[lane];
         }
@@ -470,7 +477,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
 #pragma unroll
                     for (int k = 0; k < G53_DT_NGO / 64; k++) stale |= (unsigned)(tv[k] >> 32) != a.epoch;
                     if (!__ballot(stale)) break;
-                    if (++spins > G53_SPIN_LIMIT / 16) { if (lane == 0) g53_flag_err(a.err, 1); break; }
+                    if (++spins > a.spin / 16 + 1) { if (lane == 0) g53_flag_err(a.err, 1); break; }
                     for (int q = 0; q < nap; q++) __builtin_amdgcn_s_sleep(8);
                     if (nap < 8) nap *= 2;
                 }
@@ -502,7 +509,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
                 }
                 spins = 0;
                 while (__ballot(pend != 0)) {
-                    if (++spins > G53_SPIN_LIMIT) { if (lane == 0) g53_flag_err(a.err, 1); break; }
+                    if (++spins > a.spin) { if (lane == 0) g53_flag_err(a.err, 1); break; }
                     g53_backoff();
 #pragma unroll
                     for (int mm = 0; mm < 32; mm++) {
@@ -565,7 +572,6 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
 /* ------------------------------------------------------------------ host side ---- */
 static int g_dt_grid = -1;
 static unsigned g_dt_epoch = 0;
-static int *g_dt_state = nullptr;       /* [0] error flags                                 */
 static void *g_dt_buf = nullptr;        /* tagged scores | tagged activations              */
 static size_t g_dt_buf_bytes = 0;
 static g53_u64 *g_dt_trace = nullptr;
@@ -576,22 +582,14 @@ extern "C" int g53h_set_tiled_decode_trace(void *dev_buf)
     return 0;
 }
 
-int g53h_decode_tiled_errors(void)
-{
-    if (!g_dt_state) return 0;
-    int e = 0;
-    if (hipStreamSynchronize(g53h_stream()) != hipSuccess) return -1;
-    if (hipMemcpy(&e, g_dt_state, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return -1;
-    if (e) (void)hipMemset(g_dt_state, 0, sizeof(int));
-    return e;
-}
-
 int g53h_decode_tiled_grid(void) { return g_dt_grid; }
 
 /* Launch k_dec_tiled; returns 1 when the layer is not one it takes (the caller falls back). */
-int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out)
+int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out,
+                      const int *idx_in, const float *w_in)
 {
-    if (!L->tiled || L->block_c != 128 || L->hidden != G53_DEC_E || L->inter != G53_DEC_I || L->router_dt != 1 ||
+    if (!L->tiled || L->block_c != 128 || L->hidden != G53_DEC_E || L->inter != G53_DEC_I ||
+        (!idx_in && (L->router_dt != 1 || !L->router)) ||
         L->topk < 1 || L->topk > G53_DEC_MAXK || L->n_experts > G53_DEC_MAXNE)
         return 1;
     if (g_dt_grid < 0) {
@@ -602,11 +600,6 @@ int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *id
             (void)hipGetLastError();
         } else if (per >= 1 && cus >= 128 && cus <= 512) {
             g_dt_grid = cus;
-        }
-        if (g_dt_grid && (hipMalloc((void **)&g_dt_state, 256) != hipSuccess ||
-                          hipMemset(g_dt_state, 0, 256) != hipSuccess)) {
-            (void)hipGetLastError();
-            g_dt_grid = 0;
         }
     }
     if (!g_dt_grid) return 1;
@@ -632,9 +625,9 @@ int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *id
     e.experts = L->experts; e.shared = L->shared;
     e.score = (g53_u64 *)buf;
     e.act = (g53_u64 *)(buf + off_act + (g_dt_epoch % G53_DT_ROT) * act_copy);
-    e.err = g_dt_state; e.idx_out = idx_out; e.w_out = w_out;
+    e.err = g53h_errblock() + 1; e.idx_out = idx_out; e.w_out = w_out; e.idx_in = idx_in; e.w_in = w_in;
     e.NE = L->n_experts; e.K = L->topk; e.norm_topk = L->norm_topk; e.epoch = g_dt_epoch;
-    e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dt_trace;
+    e.spin = g53h_spin_limit(); e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dt_trace;
     g53h_prof_mark(G53_PROF_START);
     hipLaunchKernelGGL(k_dec_tiled, dim3(g_dt_grid), dim3(G53_DT_NT), 0, g53h_stream(), e);
     G53_LAUNCHED("k_dec_tiled");

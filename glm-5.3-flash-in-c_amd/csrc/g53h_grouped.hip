@@ -744,11 +744,11 @@ int g53h_grouped_use(const G53hMoeLayer *L, int T) { return g_grp_mode && T >= 2
 
 extern "C" int g53h_grouped_errors(void)
 {
-    if (!g_grp_err) return 0;
+    if (g53h_ready()) return 0;
     int v = 0;
     if (g53h_check(hipStreamSynchronize(g53h_stream()), "sync", __FILE__, __LINE__)) return -1;
-    if (g53h_check(hipMemcpy(&v, g_grp_err, 4, hipMemcpyDeviceToHost), "d2h", __FILE__, __LINE__)) return -1;
-    if (v && g53h_check(hipMemset(g_grp_err, 0, 4), "memset", __FILE__, __LINE__)) return -1;
+    if (g53h_check(hipMemcpy(&v, g53h_errblock() + 2, 4, hipMemcpyDeviceToHost), "d2h", __FILE__, __LINE__)) return -1;
+    if (v && g53h_check(hipMemset(g53h_errblock() + 2, 0, 4), "memset", __FILE__, __LINE__)) return -1;
     return v;
 }
 
@@ -838,7 +838,7 @@ static int g53_grp_combine_pass(float *out, const float *wts)
     const int tc = g_pass.tc, E = g_pass.a.E;
     const long nq = (long)tc * E / 4;
     hipLaunchKernelGGL(k_grp_combine, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, out, g_pass.contrib, wts,
-                       g_pass.pos_of, tc, E, g_pass.K, g_pass.hs, g_grp_err, g_pass.meta);
+                       g_pass.pos_of, tc, E, g_pass.K, g_pass.hs, g53h_errblock() + 2, g_pass.meta);
     G53_LAUNCHED("k_grp_combine");
     g53h_prof_mark(G53_PROF_COMBINE);
     g_pass.active = 0;

@@ -560,9 +560,12 @@ __device__ inline void g53_argmax_merge(float &bv, int &bi, float ov, int oi)
 /* route_topn (src/core/glm53f_ops.c:1021-1042): the scan starts from expert 0, so a NaN at
  * index 0 wins every round and NaN elsewhere is skipped. */
 __global__ void __launch_bounds__(64) k_route_topn(int *__restrict__ idx, int n,
-                                                   const float *__restrict__ choice, int NE)
+                                                   const float *__restrict__ choice, int NE,
+                                                   const float *__restrict__ score, float *__restrict__ score_out)
 {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x, t = blockIdx.x;
+    choice += (size_t)t * NE;
+    idx += (size_t)t * n;
     float c[G53_SEL_PER_LANE];
     for (int k = 0; k < G53_SEL_PER_LANE; k++) {
         const int e = lane + 64 * k;
@@ -589,8 +592,46 @@ __global__ void __launch_bounds__(64) k_route_topn(int *__restrict__ idx, int n,
         }
         for (int k = 0; k < G53_SEL_PER_LANE; k++)
             if (lane + 64 * k == best) c[k] = -INFINITY;
-        if (lane == 0) idx[j] = best;
+        if (lane == 0) {
+            idx[j] = best;
+            if (score_out) score_out[(size_t)t * n + j] = score[(size_t)t * NE + best];
+        }
     }
+}
+
+/* The prefill prediction's vote (src/core/glm53f_ops.c:1206-1225): the experts named in ids
+ * [T][n] ordered by how many tokens named them, most first, ties in the order of their first
+ * appearance (t, then j). out[0] = the number of distinct experts, out[1 + r] = the expert of
+ * rank r. One workgroup: counts and first positions in LDS, then each expert's rank counted
+ * against every other. */
+__global__ void __launch_bounds__(1024) k_vote(int *__restrict__ out, const int *__restrict__ ids, int T, int n,
+                                               int NE)
+{
+    __shared__ int votes[1024], first[1024];
+    for (int e = threadIdx.x; e < NE; e += 1024) { votes[e] = 0; first[e] = 0x7fffffff; }
+    __syncthreads();
+    for (int q = threadIdx.x; q < T * n; q += 1024) {
+        const int e = ids[q];
+        if (e < 0 || e >= NE) continue;
+        atomicAdd(&votes[e], 1);
+        atomicMin(&first[e], q);
+    }
+    __syncthreads();
+    int distinct = 0;
+    for (int e = threadIdx.x; e < NE; e += 1024) {                   /* NE <= 1024 */
+        const int v = votes[e];
+        if (!v) continue;
+        const int f = first[e];
+        int r = 0;
+        for (int o = 0; o < NE; o++) {
+            const int vo = votes[o];
+            r += vo > v || (vo == v && vo && first[o] < f);
+        }
+        out[1 + r] = e;
+    }
+    if (threadIdx.x < NE) distinct = votes[threadIdx.x] != 0;        /* NE <= 1024: one each */
+    const int total = __syncthreads_count(distinct);
+    if (threadIdx.x == 0) out[0] = total;
 }
 
 extern "C" int g53h_route_topn(int *idx, int n, const float *x, const void *gate, int gate_dt,
@@ -604,7 +645,35 @@ extern "C" int g53h_route_topn(int *idx, int n, const float *x, const void *gate
     hipLaunchKernelGGL(k_router_scores, dim3(NE, 1), dim3(64), 0, g53h_stream(), ws + NE, ws, x, 1, gate,
                        gate_dt, bias, NE, E);
     G53_LAUNCHED("k_router_scores");
-    hipLaunchKernelGGL(k_route_topn, dim3(1), dim3(64), 0, g53h_stream(), idx, n, ws, NE);
+    hipLaunchKernelGGL(k_route_topn, dim3(1), dim3(64), 0, g53h_stream(), idx, n, ws, NE, ws + NE, nullptr);
     G53_LAUNCHED("k_route_topn");
+    return 0;
+}
+
+extern "C" int g53h_route_topn_batch(int *idx, float *score_out, int n, const float *x, int T, const void *gate,
+                                     int gate_dt, const float *bias, int NE, int E)
+{
+    if (g53h_ready()) return -1;
+    if (n <= 0 || T <= 0) return 0;
+    if (NE < 1 || NE > 64 * G53_SEL_PER_LANE) return g53h_fail("g53h_route_topn_batch: %d experts", NE);
+    if (n > NE) return g53h_fail("g53h_route_topn_batch: %d of %d experts", n, NE);
+    float *ws = (float *)g53h_workspace((size_t)2 * T * NE * sizeof(float));
+    if (!ws) return -1;
+    float *choice = ws, *score = ws + (size_t)T * NE;
+    hipLaunchKernelGGL(k_router_scores, dim3(NE, T), dim3(64), 0, g53h_stream(), score, choice, x, T, gate,
+                       gate_dt, bias, NE, E);
+    G53_LAUNCHED("k_router_scores");
+    hipLaunchKernelGGL(k_route_topn, dim3(T), dim3(64), 0, g53h_stream(), idx, n, choice, NE, score, score_out);
+    G53_LAUNCHED("k_route_topn");
+    return 0;
+}
+
+extern "C" int g53h_vote(int *out, const int *ids, int T, int n, int NE)
+{
+    if (g53h_ready()) return -1;
+    if (NE < 1 || NE > 1024) return g53h_fail("g53h_vote: %d experts", NE);
+    if (T < 0 || n < 0) return g53h_fail("g53h_vote: %d x %d ids", T, n);
+    hipLaunchKernelGGL(k_vote, dim3(1), dim3(1024), 0, g53h_stream(), out, ids, T, n, NE);
+    G53_LAUNCHED("k_vote");
     return 0;
 }

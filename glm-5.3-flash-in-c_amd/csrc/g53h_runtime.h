@@ -29,6 +29,11 @@ void       *g53h_workspace(size_t bytes);
 /* A zero-initialised region of 4096 ints that kernels use as arrival counters and flags and
  * always restore to zero before they exit. */
 int        *g53h_counters(void);
+/* The layer kernels' error flags, one int each ([0] k_dec_layer, [1] k_dec_tiled, [2] the
+ * grouped path), zero at init; g53h_errors_async copies and clears them. */
+int        *g53h_errblock(void);
+/* Polls before a wait on another workgroup gives up (g53h_set_spin_limit). */
+int         g53h_spin_limit(void);
 
 /* Kernel timing marks (no-ops unless g53h_prof_enable(1)): tag 0 opens an interval, the
  * tags below close the interval since the previous mark. */

@@ -19,6 +19,7 @@ static int         g_ev_next = 0;
 static void       *g_ws = nullptr;
 static size_t      g_ws_bytes = 0;
 static int        *g_counters = nullptr;
+static int        *g_errs = nullptr;   /* [0] k_dec_layer, [1] k_dec_tiled, [2] grouped path   */
 
 extern "C" int g53h_fail(const char *fmt, ...)
 {
@@ -65,6 +66,8 @@ extern "C" int g53h_init(int device)
     G53_TRY(hipEventCreate(&g_ev[1]));
     G53_TRY(hipMalloc((void **)&g_counters, 4096 * sizeof(int)));
     G53_TRY(hipMemset(g_counters, 0, 4096 * sizeof(int)));
+    G53_TRY(hipMalloc((void **)&g_errs, 64 * sizeof(int)));
+    G53_TRY(hipMemset(g_errs, 0, 64 * sizeof(int)));
     G53_TRY(hipDeviceSynchronize());
     g_device = device;
     g_ready = 1;
@@ -76,6 +79,30 @@ extern "C" int g53h_num_cus(void) { return g_cus; }
 hipStream_t g53h_stream(void) { return g_stream; }
 hipStream_t g53h_copy_stream(void) { return g_copy; }
 int *g53h_counters(void) { return g_counters; }
+int *g53h_errblock(void) { return g_errs; }
+
+static int g_spin = 0;
+extern "C" int g53h_set_spin_limit(int polls)
+{
+    const int old = g_spin;
+    g_spin = polls > 0 ? polls : 0;
+    return old;
+}
+int g53h_spin_limit(void) { return g_spin > 0 ? g_spin : (1 << 20); }
+
+__global__ void k_errs_clear(int *e)
+{
+    if (threadIdx.x < G53H_NERR) e[threadIdx.x] = 0;
+}
+
+extern "C" int g53h_errors_async(int *host)
+{
+    if (g53h_ready()) return -1;
+    G53_TRY(hipMemcpyAsync(host, g_errs, G53H_NERR * sizeof(int), hipMemcpyDeviceToHost, g_stream));
+    hipLaunchKernelGGL(k_errs_clear, dim3(1), dim3(64), 0, g_stream, g_errs);
+    G53_LAUNCHED("k_errs_clear");
+    return 0;
+}
 
 extern "C" int g53h_sync(void)
 {

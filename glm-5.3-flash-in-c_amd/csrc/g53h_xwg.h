@@ -127,7 +127,7 @@ template <int NV>
 __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float *bias, int NE, int K, int norm_topk,
                                                float routed_scale, unsigned epoch, int *sidx, float *sw,
                                                uint32_t *kbuf, int *ebuf, int *err, int lane, g53_u64 &t_seen,
-                                               int &n_polls, g53_u64 &t_tau, g53_u64 &t_rank)
+                                               int &n_polls, g53_u64 &t_tau, g53_u64 &t_rank, int limit)
 {
     const __amdgpu_buffer_rsrc_t rs = g53_rsrc(score);
     float scv[NV];
@@ -141,7 +141,7 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
     }
     int spins = 0;
     while (__ballot(pend != 0)) {
-        if (++spins > G53_SPIN_LIMIT) return false;
+        if (++spins > limit) return false;
         n_polls++;
         __builtin_amdgcn_s_sleep(2);
         g53_u64 t[NV];                                    /* every load in flight at once */
@@ -242,7 +242,7 @@ template <int NV>
 __device__ __forceinline__ bool g53_route_bisect(const g53_u64 *score, const float *bias, int NE, int K, int norm_topk,
                                                  float routed_scale, unsigned epoch, int *sidx, float *sw,
                                                  uint32_t *kbuf, int *ebuf, float *fbuf, int *err, int lane,
-                                                 g53_u64 &t_seen, g53_u64 *tr = nullptr)
+                                                 g53_u64 &t_seen, int limit, g53_u64 *tr = nullptr)
 {
     const __amdgpu_buffer_rsrc_t rs = g53_rsrc(score);
     float scv[NV];
@@ -256,7 +256,7 @@ __device__ __forceinline__ bool g53_route_bisect(const g53_u64 *score, const flo
     }
     int spins = 0;
     while (__ballot(pend != 0)) {
-        if (++spins > G53_SPIN_LIMIT) return false;
+        if (++spins > limit) return false;
         __builtin_amdgcn_s_sleep(2);
         g53_u64 t[NV];
 #pragma unroll

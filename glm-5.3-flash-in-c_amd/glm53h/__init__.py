@@ -166,6 +166,11 @@ _SIGS = {
     "g53h_decode_errors": (C.c_int, []),
     "g53h_decode_grid": (C.c_int, []),
     "g53h_set_decode_trace": (C.c_int, [C.c_void_p]),
+    "g53h_errors_async": (C.c_int, [C.c_void_p]),
+    "g53h_route_topn_batch": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                                        C.c_void_p, C.c_int, C.c_int]),
+    "g53h_vote": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "g53h_set_spin_limit": (C.c_int, [C.c_int]),
     "g53h_set_tiled_decode_trace": (C.c_int, [C.c_void_p]),
     "g53h_tile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "g53h_untile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),

@@ -35,7 +35,23 @@ static void g53_die(const char *what)
 }
 
 /* ------------------------------------------------------------ resident weights ---- */
-typedef struct { const void *h; size_t n; void *d; int dt; } G53Res;
+/* An entry is found by host address and checked against the size and a signature of 64 words
+ * sampled across the bytes: a caller that frees its weights and reuses the address for others
+ * gets them uploaded again instead of the stale copy. */
+typedef struct { const void *h; size_t n; void *d; int dt; uint64_t sig; } G53Res;
+
+static uint64_t res_sig(const void *h, size_t n)
+{
+    const unsigned char *b = (const unsigned char *)h;
+    uint64_t v = 0x9e3779b97f4a7c15ull ^ n;
+    for (int k = 0; k < 64 && n >= 8; k++) {
+        uint64_t word;
+        memcpy(&word, b + (size_t)k * ((n - 8) / 63), 8);
+        v = (v ^ word) * 0x100000001b3ull;
+        v ^= v >> 29;
+    }
+    return v;
+}
 static G53Res *g_res = NULL;
 static size_t g_res_cap = 0, g_res_n = 0;
 
@@ -84,12 +100,13 @@ static const void *resident(const void *h, size_t n)
     if (!h) return NULL;
     if (g53h_is_device_ptr(h)) return h;
     G53Res *r = res_find(h);
-    if (r && r->n >= n) return r->d;
+    const uint64_t sig = res_sig(h, n);
+    if (r && r->n == n && r->dt < 0 && r->sig == sig) return r->d;
     void *d = g53h_alloc(n);
     if (!d || g53h_h2d(d, h, n)) g53_die("uploading a weight to HBM");
     if (!r) r = res_insert(h);
-    else g53h_free(r->d);
-    r->n = n; r->d = d; r->dt = -1;
+    else if (g53h_sync() || g53h_free(r->d)) g53_die("replacing a resident weight");
+    r->n = n; r->d = d; r->dt = -1; r->sig = sig;
     return d;
 }
 
@@ -100,7 +117,8 @@ static const void *resident_router(const float *h, size_t n, int *dt)
 {
     if (g53h_is_device_ptr(h)) { *dt = 0; return h; }
     G53Res *r = res_find(h);
-    if (r && r->dt >= 0 && r->n >= n * (r->dt ? 2 : 4)) { *dt = r->dt; return r->d; }
+    const uint64_t sig = res_sig(h, n * sizeof(float));
+    if (r && r->dt >= 0 && r->n == n * (r->dt ? 2 : 4) && r->sig == sig) { *dt = r->dt; return r->d; }
     int bf = 1;
     for (size_t i = 0; i < n && bf; i++) if (g53_fbits(h[i]) & 0xffffu) bf = 0;
     void *d;
@@ -119,8 +137,8 @@ static const void *resident_router(const float *h, size_t n, int *dt)
         if (!d || g53h_h2d(d, h, bytes)) g53_die("uploading the router");
     }
     if (!r) r = res_insert(h);
-    else g53h_free(r->d);
-    r->n = bytes; r->d = d; r->dt = bf;
+    else if (g53h_sync() || g53h_free(r->d)) g53_die("replacing a resident router");
+    r->n = bytes; r->d = d; r->dt = bf; r->sig = sig;
     *dt = bf;
     return d;
 }
@@ -142,7 +160,7 @@ static size_t mat_scale_bytes(const Glm53fMat *m)
 static void check_f8(const Glm53fMat *m, const char *what)
 {
     if (!m->w) { fprintf(stderr, "glm53f: FATAL, multiply through an unbound matrix (%s)\n", what); abort(); }
-    if (m->dt != GLM53F_WF8) {
+    if (m->dt != GLM53F_WF8 && m->dt != GLM53F_WF8T) {
         fprintf(stderr, "glm53f: FATAL, %s has storage type %d; the MI355X expert path multiplies "
                         "FP8 E4M3 matrices only\n", what, m->dt);
         abort();
@@ -171,6 +189,7 @@ static G53hMat view_mat_f8(const Glm53fMat *m)
     memset(&d, 0, sizeof d);
     d.w = (const uint8_t *)m->w; d.s = m->s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    d.flags = m->dt == GLM53F_WF8T ? G53H_MAT_TILED : 0;
     return d;
 }
 
@@ -188,6 +207,36 @@ static void *buf_get(G53Buf *b, size_t n)
 }
 
 static G53Buf g_xin, g_out, g_idx, g_w, g_flag, g_table, g_pred, g_tmp, g_contrib;
+
+/* The same in the octet-tiled layout (for the tiled decode kernel), resident as well: uploaded
+ * row-major once, converted on the device, kept under the host address with its own tag. */
+static G53Buf g_tile_stage;
+static G53hMat dev_mat_resident_tiled(const Glm53fMat *m, const char *what)
+{
+    check_f8(m, what);
+    G53hMat d;
+    memset(&d, 0, sizeof d);
+    d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    d.flags = G53H_MAT_TILED;
+    d.s = (const float *)resident(m->s, mat_scale_bytes(m));
+    if (g53h_is_device_ptr(m->w)) {
+        fprintf(stderr, "glm53f: FATAL, %s: an HBM matrix is used as it is, not converted\n", what);
+        abort();
+    }
+    const size_t n = mat_code_bytes(m);
+    G53Res *r = res_find((const char *)m->w + 1);        /* the tiled copy's own key */
+    const uint64_t sig = res_sig(m->w, n);
+    if (r && r->n == n && r->dt == -2 && r->sig == sig) { d.w = (const uint8_t *)r->d; return d; }
+    uint8_t *stage = (uint8_t *)buf_get(&g_tile_stage, n);
+    uint8_t *t = (uint8_t *)g53h_alloc(n);
+    if (!t || g53h_h2d(stage, m->w, n) || g53h_tile_f8(t, stage, m->rows, m->cols) || g53h_sync())
+        g53_die("tiling a resident weight");
+    if (!r) r = res_insert((const char *)m->w + 1);
+    else if (g53h_sync() || g53h_free(r->d)) g53_die("replacing a resident weight");
+    r->n = n; r->d = t; r->dt = -2; r->sig = sig;
+    d.w = t;
+    return d;
+}
 
 /* Host operand -> HBM (or the operand itself when it is HBM already). */
 static const float *stage_in(G53Buf *b, const float *h, size_t n)
@@ -319,7 +368,269 @@ size_t glm53f_moe_scratch(const Glm53fCfg *c, int T)
            n * (2 * E + 3 * (size_t)c->moe_inter);
 }
 
-/* Host expert views are copied into these per-call staging slots (one per unique expert). */
+static void check_expert_shape(const Glm53fExpertQ *q, const Glm53fCfg *c, int layer, int e)
+{
+    const Glm53fMat *ms[3] = {&q->gate, &q->up, &q->down};
+    const int rows[3] = {c->moe_inter, c->moe_inter, c->hidden}, cols[3] = {c->hidden, c->hidden, c->moe_inter};
+    for (int i = 0; i < 3; i++) {
+        check_f8(ms[i], "a routed expert matrix");
+        if (ms[i]->rows != rows[i] || ms[i]->cols != cols[i]) {
+            fprintf(stderr, "glm53f: FATAL, layer %d expert %d matrix %d is %dx%d, expected %dx%d\n",
+                    layer, e, i, ms[i]->rows, ms[i]->cols, rows[i], cols[i]);
+            abort();
+        }
+    }
+}
+
+static void *g_pin_x, *g_pin_tab, *g_pin_back, *g_pin_err;
+static size_t g_pin_x_n, g_pin_tab_n, g_pin_back_n, g_pin_err_n;
+
+static void *pinned(void **p, size_t *have, size_t n)
+{
+    if (n <= *have) return *p;
+    if (*p && (g53h_sync() || g53h_host_free(*p))) g53_die("freeing pinned staging");
+    *p = g53h_host_alloc(n);
+    if (!*p) g53_die("allocating pinned staging");
+    *have = n;
+    return *p;
+}
+
+/* ------------------------------------------------------------- error flags ---- */
+/* The layer kernels' flags come back with the layer's last copy (g53h_errors_async before it):
+ * a wait that gave up or an unusable descriptor aborts, as the reference aborts on its own
+ * errors (src/core/glm53f_ops.c:28-39); a token without K selectable experts is the reference's
+ * NaN routing abort (:961-965). */
+static int *errors_enqueue(void)
+{
+    int *e = (int *)pinned(&g_pin_err, &g_pin_err_n, G53H_NERR * sizeof(int));
+    if (g53h_errors_async(e)) g53_die("reading the kernel error flags");
+    return e;
+}
+
+static void errors_check(const int *e, int layer, int K)
+{
+    const int dec = e[0] | e[1], grp = e[2];
+    if (dec & 2) {
+        fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) is below %d, above the limit of %d.\n", K, K);
+        abort();
+    }
+    if (dec || grp) {
+        fprintf(stderr, "glm53f: FATAL, the MoE kernels of layer %d reported error flags (decode 0x%x, grouped 0x%x):"
+                        "%s%s%s; aborting rather than returning a corrupt output.\n",
+                layer, dec, grp, ((dec | grp) & 1) ? " a bound or wait was exceeded" : "",
+                (grp & 2) ? " a wait between waves timed out" : "",
+                ((dec | grp) & 8) ? " an expert descriptor the kernels cannot read" : "");
+        abort();
+    }
+}
+
+/* --------------------------------------------------------- switches (env) ---- */
+/* GLM53F_NO_PREFILL_PREFETCH and GLM53F_PREFILL_PRED, read once (src/core/glm53f_ops.c:1186-1194). */
+static int g_prefill_off = -1, g_prefill_pred = -1;
+static void read_switches(void)
+{
+    if (g_prefill_off >= 0) return;
+    g_prefill_off = getenv("GLM53F_NO_PREFILL_PREFETCH") ? 1 : 0;
+    const char *pp = getenv("GLM53F_PREFILL_PRED");
+    g_prefill_pred = pp ? atoi(pp) : -1;
+}
+
+/* GLM53F_ROUTE_TOP16=path: one line per decode MoE layer, the 16 best candidates in selection
+ * order as id:score (the sigmoid before normalisation), the format of the reference's
+ * route_top16_trace (src/core/glm53f_ops.c:1044-1080), from the device router. */
+static FILE *g_top16 = NULL;
+static int g_top16_on = -1;
+static void route_top16(int layer, const float *xd, const Glm53fMoeW *w, const Glm53fCfg *c)
+{
+    if (g_top16_on < 0) {
+        const char *p = getenv("GLM53F_ROUTE_TOP16");
+        g_top16 = p ? fopen(p, "a") : NULL;
+        g_top16_on = g_top16 != NULL;
+    }
+    if (!g_top16_on) return;
+    const int NE = c->n_experts, n = NE < 16 ? NE : 16;
+    int dt = 0;
+    const void *gate = resident_router(w->gate, (size_t)NE * c->hidden, &dt);
+    const float *bias = (const float *)resident(w->bias, (size_t)NE * sizeof(float));
+    int *id_d = (int *)buf_get(&g_tmp, 32 * sizeof(int));
+    float *sc_d = (float *)(id_d + 16);
+    int ids[16];
+    float sc[16];
+    if (g53h_route_topn_batch(id_d, sc_d, n, xd, 1, gate, dt, bias, NE, c->hidden) ||
+        g53h_d2h(ids, id_d, (size_t)n * sizeof(int)) || g53h_d2h(sc, sc_d, (size_t)n * sizeof(float)))
+        g53_die("the routing trace");
+    fprintf(g_top16, "%d", layer);
+    for (int j = 0; j < n; j++) fprintf(g_top16, " %d:%.6g", ids[j], sc[j]);
+    fputc('\n', g_top16);
+    fflush(g_top16);
+}
+
+/* ------------------------------------------------------- next-layer prediction ---- */
+/* The experts layer + 1 will probably want, for the hint protocol (src/core/glm53f_ops.c:
+ * 1021-1042, 1196-1226): at T = 1 the next router's top `per` on this input; for a chunk of
+ * tokens every token's top `per`, merged by the device vote (most voted first, ties in order of
+ * first appearance). All tokens in one launch, one copy back. Returns the count written. */
+static int predict_next(int *pred, const float *xd, const Glm53fMoeW *w, const Glm53fCfg *c, int T, int per)
+{
+    const int NE = c->n_experts, E = c->hidden;
+    int dt = 0;
+    const void *gate = resident_router(w->next_gate, (size_t)NE * E, &dt);
+    const float *bias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
+    int *ids_d = (int *)buf_get(&g_pred, ((size_t)T * per + 1 + NE) * sizeof(int));
+    if (g53h_route_topn_batch(ids_d, NULL, per, xd, T, gate, dt, bias, NE, E)) g53_die("next-layer prediction");
+    if (T == 1) {
+        if (g53h_d2h(pred, ids_d, (size_t)per * sizeof(int))) g53_die("next-layer prediction");
+        return per;
+    }
+    int *vote_d = ids_d + (size_t)T * per;
+    if (g53h_vote(vote_d, ids_d, T, per, NE)) g53_die("next-layer prediction");
+    int *back = (int *)pinned(&g_pin_back, &g_pin_back_n, (size_t)(1 + NE) * sizeof(int));
+    if (g53h_d2h(back, vote_d, (size_t)(1 + NE) * sizeof(int))) g53_die("next-layer prediction");
+    const int no = back[0] < 64 * 2 * GLM53F_MAX_TOPK ? back[0] : 64 * 2 * GLM53F_MAX_TOPK;
+    memcpy(pred, back + 1, (size_t)no * sizeof(int));
+    return no;
+}
+
+/* --------------------------------------------------- decode through the HBM cache ---- */
+/* One token with the experts served by this library's HBM cache, in one fused launch: the
+ * reference's protocol (route, hint the own then the next layer's experts, get, multiply,
+ * release; src/core/glm53f_ops.c:1169-1342) with two host round trips. The routing, the
+ * prediction and the NaN flag come back in one copy; an expert that fails to load is the
+ * reference's drop (counted, reported, its contribution zero). With octet-tiled slots the layer
+ * kernel takes the routing as given (it is not computed twice) and a compact table of the K
+ * chosen descriptors and the shared one (K + 1 descriptors uploaded); with row-major slots it
+ * routes again with the same bit-exact router, over a table that holds only the chosen ones. */
+static G53Buf g_ident;
+
+static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int with_shared)
+{
+    const int E = c->hidden, K = c->topk, NE = c->n_experts;
+    Glm53fExpertSrc *src = w->src;
+    float *xd = (float *)x;
+    if (!g53h_is_device_ptr(x)) {                   /* x up without a wait */
+        float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, (size_t)E * sizeof(float));
+        memcpy(xp, x, (size_t)E * sizeof(float));
+        xd = (float *)buf_get(&g_xin, (size_t)E * sizeof(float));
+        if (g53h_h2d_async(xd, xp, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
+    }
+    const int per_max = 2 * GLM53F_MAX_TOPK;
+    int *rd = (int *)buf_get(&g_idx, (size_t)(K + 1 + per_max) * sizeof(int));
+    int *idx_d = rd, *flag_d = rd + K, *pred_d = rd + K + 1;
+    float *w_d = (float *)buf_get(&g_w, (size_t)K * sizeof(float));
+    int dt = 0;
+    const void *gate = resident_router(w->gate, (size_t)NE * E, &dt);
+    const float *bias = (const float *)resident(w->bias, (size_t)NE * sizeof(float));
+    if (g53h_memset(flag_d, 0, sizeof(int)) ||
+        g53h_router(idx_d, w_d, xd, 1, gate, dt, bias, NE, E, K, c->norm_topk, c->routed_scale, flag_d))
+        g53_die("glm53f_router");
+    const int prefetch = w->prefetch_n > 0 && src->hint != NULL;
+    int per = 0;
+    if (prefetch && w->next_gate) {
+        per = w->prefetch_n < per_max ? w->prefetch_n : per_max;
+        int ndt = 0;
+        const void *ngate = resident_router(w->next_gate, (size_t)NE * E, &ndt);
+        const float *nbias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
+        if (g53h_route_topn_batch(pred_d, NULL, per, xd, 1, ngate, ndt, nbias, NE, E)) g53_die("next-layer prediction");
+    }
+    int *back = (int *)pinned(&g_pin_back, &g_pin_back_n, (size_t)(K + 1 + per_max) * sizeof(int));
+    if (g53h_d2h(back, rd, (size_t)(K + 1 + per) * sizeof(int))) g53_die("glm53f_moe routing");
+    if (back[K]) {
+        fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) is below %d, above the limit of %d.\n", K, K);
+        abort();
+    }
+    int ids[GLM53F_MAX_TOPK];
+    memcpy(ids, back, (size_t)K * sizeof(int));
+    route_top16(w->layer, xd, w, c);
+    if (prefetch) {
+        src->hint(src, w->layer, ids, K);
+        if (per > 0) src->hint(src, w->layer + 1, back + K + 1, per);
+    }
+    /* the chosen experts' views (slot order), the shared expert after them */
+    G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
+    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1;
+    memset(tab, 0, (size_t)(K + 1) * sizeof(G53hExpert));
+    for (int j = 0; j < K; j++) {
+        Glm53fExpertQ q;
+        memset(&q, 0, sizeof q);
+        if (src->get(src, w->layer, ids[j], &q) != 0) {
+            glm53f_expert_drops++;
+            fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this output is CORRUPT\n", w->layer,
+                    ids[j]);
+            continue;                               /* absent: its contribution is zero */
+        }
+        held[nh++] = ids[j];
+        check_expert_shape(&q, c, w->layer, ids[j]);
+        tab[j].gate = view_mat_f8(&q.gate);
+        tab[j].up = view_mat_f8(&q.up);
+        tab[j].down = view_mat_f8(&q.down);
+        if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_TILED)) tiled = 0;
+    }
+    if (with_shared) {
+        /* the shared expert resident in the layout of the routed slots */
+        const int tile_ok = tiled && w->sh_gate.rows % 8 == 0 && w->sh_gate.cols % 128 == 0 &&
+                            w->sh_down.rows % 8 == 0 && w->sh_down.cols % 128 == 0;
+        if (tile_ok) {
+            tab[K].gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
+            tab[K].up = dev_mat_resident_tiled(&w->sh_up, "shared up");
+            tab[K].down = dev_mat_resident_tiled(&w->sh_down, "shared down");
+        } else {
+            tab[K].gate = dev_mat_resident(&w->sh_gate, "shared gate");
+            tab[K].up = dev_mat_resident(&w->sh_up, "shared up");
+            tab[K].down = dev_mat_resident(&w->sh_down, "shared down");
+            tiled = 0;
+        }
+    }
+    G53hMoeLayer L;
+    memset(&L, 0, sizeof L);
+    L.hidden = E; L.inter = c->moe_inter; L.topk = K; L.norm_topk = c->norm_topk;
+    L.routed_scale = c->routed_scale; L.swiglu_limit = c->swiglu_limit;
+    L.router = gate; L.router_dt = dt; L.bias = bias; L.block_c = 128;
+    for (int j = 0; j <= K; j++) {
+        const G53hExpert *e = &tab[j];
+        if ((j < K || with_shared) && e->gate.w && (e->gate.bc != 128 || e->up.bc != 128 || e->down.bc != 128))
+            L.block_c = 0;
+    }
+    G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
+    const int odev = g53h_is_device_ptr(out);
+    float *od = odev ? out : (float *)buf_get(&g_out, (size_t)E * sizeof(float));
+    if (tiled) {
+        /* compact table: slot j holds the j-th chosen expert (the kernel is told indices 0 .. K-1),
+         * slot K the shared expert */
+        int *ident = (int *)buf_get(&g_ident, GLM53F_MAX_TOPK * sizeof(int));
+        static int ident_ready = 0;
+        if (!ident_ready) {
+            int h[GLM53F_MAX_TOPK];
+            for (int j = 0; j < GLM53F_MAX_TOPK; j++) h[j] = j;
+            if (g53h_h2d(ident, h, sizeof h)) g53_die("glm53f_moe");
+            ident_ready = 1;
+        }
+        if (g53h_h2d_async(tab_d, tab, (size_t)(K + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
+        L.n_experts = K; L.experts = tab_d; L.shared = with_shared ? tab_d + K : NULL; L.tiled = 1;
+        if (g53h_moe_routed_given(od, xd, 1, &L, ident, w_d)) g53_die("glm53f_moe");
+    } else {
+        /* the table indexed by expert: the chosen entries filled, the others zero */
+        G53hExpert chosen[GLM53F_MAX_TOPK + 1];
+        memcpy(chosen, tab, (size_t)(K + 1) * sizeof(G53hExpert));
+        memset(tab, 0, (size_t)(NE + 1) * sizeof(G53hExpert));
+        for (int j = 0; j < K; j++) if (chosen[j].gate.w) tab[ids[j]] = chosen[j];
+        tab[NE] = chosen[K];
+        if (g53h_h2d_async(tab_d, tab, (size_t)(NE + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
+        L.n_experts = NE; L.experts = tab_d; L.shared = with_shared ? tab_d + NE : NULL;
+        if (g53h_moe(od, xd, 1, &L, NULL, NULL)) g53_die("glm53f_moe");
+    }
+    /* the HBM cache orders each slot's reuse after the kernels launched so far */
+    for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
+    int *errs = errors_enqueue();
+    if (!odev) {
+        if (g53h_d2h(out, od, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
+    } else if (g53h_sync()) {
+        g53_die("glm53f_moe");
+    }
+    errors_check(errs, w->layer, K);
+}
+
+/* ------------------------------------------------------------- MoE chunk ---- */
+/* Host expert views are copied into these per-call staging slots (one per expert in a batch). */
 typedef struct { G53Buf b; } G53Slot;
 static G53Slot *g_hslots = NULL;
 static int g_nhslots = 0;
@@ -336,223 +647,72 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off)
     if (g53h_h2d(w, m->w, cb) || g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
     d.w = w; d.s = (const float *)s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    d.flags = m->dt == GLM53F_WF8T ? G53H_MAT_TILED : 0;
     return d;
 }
 
-static void check_expert_shape(const Glm53fExpertQ *q, const Glm53fCfg *c, int layer, int e)
-{
-    const Glm53fMat *ms[3] = {&q->gate, &q->up, &q->down};
-    const int rows[3] = {c->moe_inter, c->moe_inter, c->hidden}, cols[3] = {c->hidden, c->hidden, c->moe_inter};
-    for (int i = 0; i < 3; i++) {
-        check_f8(ms[i], "a routed expert matrix");
-        if (ms[i]->rows != rows[i] || ms[i]->cols != cols[i]) {
-            fprintf(stderr, "glm53f: FATAL, layer %d expert %d matrix %d is %dx%d, expected %dx%d\n",
-                    layer, e, i, ms[i]->rows, ms[i]->cols, rows[i], cols[i]);
-            abort();
-        }
-    }
-}
+#define G53_MOE_BATCH 16                /* reference's getmany batch (src/core/glm53f_ops.c:989) */
 
-/* Next-layer prediction for the hint protocol (src/core/glm53f_ops.c:1190-1228). */
-static int predict_next(int *pred, const float *x_host, const float *xd, const Glm53fMoeW *w,
-                        const Glm53fCfg *c, int T)
-{
-    (void)x_host;
-    const int NE = c->n_experts, E = c->hidden;
-    int per = w->prefetch_n;
-    if (per > 2 * GLM53F_MAX_TOPK) per = 2 * GLM53F_MAX_TOPK;
-    if (per <= 0) return 0;
-    int dt = 0;
-    const void *gate = resident_router(w->next_gate, (size_t)NE * E, &dt);
-    const float *bias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
-    int *pd = (int *)buf_get(&g_pred, (size_t)2 * GLM53F_MAX_TOPK * sizeof(int));
-    if (T == 1) {
-        if (g53h_route_topn(pd, per, xd, gate, dt, bias, NE, E) || g53h_d2h(pred, pd, (size_t)per * sizeof(int)))
-            g53_die("next-layer prediction");
-        return per;
-    }
-    if (!w->prefill_next) return 0;
-    /* prefill: per-token votes, most-voted first, ties in first-seen order */
-    int *votes = (int *)calloc((size_t)NE, sizeof(int)), *order = (int *)malloc((size_t)NE * sizeof(int));
-    int tmp[2 * GLM53F_MAX_TOPK], no = 0;
-    if (!votes || !order) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
-    for (int t = 0; t < T; t++) {
-        if (g53h_route_topn(pd, per, xd + (size_t)t * E, gate, dt, bias, NE, E) ||
-            g53h_d2h(tmp, pd, (size_t)per * sizeof(int)))
-            g53_die("next-layer prediction");
-        for (int j = 0; j < per; j++) {
-            if (!votes[tmp[j]]) order[no++] = tmp[j];
-            votes[tmp[j]]++;
-        }
-    }
-    for (int i = 1; i < no; i++) {
-        const int v = order[i];
-        int j = i - 1;
-        while (j >= 0 && votes[order[j]] < votes[v]) { order[j + 1] = order[j]; j--; }
-        order[j + 1] = v;
-    }
-    memcpy(pred, order, (size_t)no * sizeof(int));
-    free(votes);
-    free(order);
-    return no;
-}
-
-/* Single-token decode with experts served from the HBM cache: the reference's protocol
- * (route, hint own then next-layer experts, get, multiply, release; src/core/glm53f_ops.c:
- * 1169-1342) with two host round trips. x goes up through pinned memory without a wait; the
- * routing, the next-layer prediction and the NaN flag come back in one copy; the routed
- * experts' cache views go into a pinned descriptor table copied up on the stream; the layer
- * then runs as g53h_moe at T = 1 (the fused decode kernels at the released shapes), whose own
- * routing is the same bit-exact routing and reads only the table entries filled here (the
- * others are zero, so a different choice would contribute nothing and raise the decode error
- * flag, never read a stale slot); release() orders each slot's reuse after these kernels.
- * Returns 0 when done, 1 when the general path must take the call (an expert failed to load). */
-static void *g_pin_x, *g_pin_tab;
-static size_t g_pin_x_n, g_pin_tab_n;
-
-static void *pinned(void **p, size_t *have, size_t n)
-{
-    if (n <= *have) return *p;
-    if (*p && (g53h_sync() || g53h_host_free(*p))) g53_die("freeing pinned staging");
-    *p = g53h_host_alloc(n);
-    if (!*p) g53_die("allocating pinned staging");
-    *have = n;
-    return *p;
-}
-
-static int decode_cached(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int with_shared)
+/* One chunk of T <= 64 tokens (reference moe_chunk, src/core/glm53f_ops.c:1144-1342). */
+static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T, int with_shared)
 {
     const int E = c->hidden, K = c->topk, NE = c->n_experts;
     Glm53fExpertSrc *src = w->src;
-    /* x up, no wait (the copy below waits for the stream) */
-    float *xd = (float *)x;
-    if (!g53h_is_device_ptr(x)) {
-        float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, (size_t)E * sizeof(float));
-        memcpy(xp, x, (size_t)E * sizeof(float));
-        xd = (float *)buf_get(&g_xin, (size_t)E * sizeof(float));
-        if (g53h_h2d_async(xd, xp, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
+    if (T == 1 && g53h_cache_is(src)) {
+        decode_cached(out, x, w, c, with_shared);
+        return;
     }
-    /* routing, prediction and flag in one device buffer, read back with one copy */
-    const int per_max = 2 * GLM53F_MAX_TOPK;
-    int *rd = (int *)buf_get(&g_pred, (size_t)(2 * K + per_max + 1) * sizeof(int));
-    int *idx_d = rd, *flag_d = rd + K, *pred_d = rd + K + 1;
-    float *w_d = (float *)buf_get(&g_w, (size_t)K * sizeof(float));
-    int dt = 0;
-    const void *gate = resident_router(w->gate, (size_t)NE * E, &dt);
-    const float *bias = (const float *)resident(w->bias, (size_t)NE * sizeof(float));
-    if (g53h_memset(flag_d, 0, sizeof(int)) ||
-        g53h_router(idx_d, w_d, xd, 1, gate, dt, bias, NE, E, K, c->norm_topk, c->routed_scale, flag_d))
-        g53_die("glm53f_router");
-    const int prefetch = w->prefetch_n > 0 && src->hint != NULL;
-    int per = 0;
-    if (prefetch && w->next_gate) {
-        per = w->prefetch_n < per_max ? w->prefetch_n : per_max;
-        int ndt = 0;
-        const void *ngate = resident_router(w->next_gate, (size_t)NE * E, &ndt);
-        const float *nbias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
-        if (g53h_route_topn(pred_d, per, xd, ngate, ndt, nbias, NE, E)) g53_die("next-layer prediction");
-    }
-    int back[2 * GLM53F_MAX_TOPK + GLM53F_MAX_TOPK + 1];
-    if (g53h_d2h(back, rd, (size_t)(K + 1 + per) * sizeof(int))) g53_die("glm53f_moe routing");
-    if (back[K]) {
-        fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) found no candidate\n");
-        abort();
-    }
-    const int *ids = back;
-    if (prefetch) {
-        src->hint(src, w->layer, ids, K);
-        if (per > 0) src->hint(src, w->layer + 1, back + K + 1, per);
-    }
-    /* the routed experts' views into a zeroed pinned table; the shared expert at [NE] */
-    G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
-    memset(tab, 0, (size_t)(NE + 1) * sizeof(G53hExpert));
-    int held[GLM53F_MAX_TOPK], nh = 0;
-    for (int j = 0; j < K; j++) {
-        Glm53fExpertQ q;
-        memset(&q, 0, sizeof q);
-        if (src->get(src, w->layer, ids[j], &q) != 0) {          /* a drop: the general path */
-            for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
-            return 1;
-        }
-        held[nh++] = ids[j];
-        check_expert_shape(&q, c, w->layer, ids[j]);
-        tab[ids[j]].gate = view_mat_f8(&q.gate);
-        tab[ids[j]].up = view_mat_f8(&q.up);
-        tab[ids[j]].down = view_mat_f8(&q.down);
-    }
-    int block_c = 128;
-    for (int j = 0; j < K; j++) {
-        const G53hExpert *e = &tab[ids[j]];
-        if (e->gate.bc != 128 || e->up.bc != 128 || e->down.bc != 128) block_c = 0;
-    }
-    if (with_shared) {
-        tab[NE].gate = dev_mat_resident(&w->sh_gate, "shared gate");
-        tab[NE].up = dev_mat_resident(&w->sh_up, "shared up");
-        tab[NE].down = dev_mat_resident(&w->sh_down, "shared down");
-        if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128) block_c = 0;
-    }
-    G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
-    if (g53h_h2d_async(tab_d, tab, (size_t)(NE + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
-    G53hMoeLayer L;
-    memset(&L, 0, sizeof L);
-    L.hidden = E; L.inter = c->moe_inter; L.n_experts = NE; L.topk = K; L.norm_topk = c->norm_topk;
-    L.routed_scale = c->routed_scale; L.swiglu_limit = c->swiglu_limit;
-    L.router = gate; L.router_dt = dt; L.bias = bias;
-    L.experts = tab_d; L.shared = with_shared ? tab_d + NE : NULL; L.block_c = block_c;
-    const int odev = g53h_is_device_ptr(out);
-    float *od = odev ? out : (float *)buf_get(&g_out, (size_t)E * sizeof(float));
-    if (g53h_moe(od, xd, 1, &L, NULL, NULL)) g53_die("glm53f_moe");
-    for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
-    if (!odev) {
-        if (g53h_d2h(out, od, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
-    } else if (g53h_sync()) {
-        g53_die("glm53f_moe");
-    }
-    return 0;
-}
-
-static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T,
-                     int with_shared)
-{
-    if (T < 1) return;
-    ensure_device();
-    const int E = c->hidden, K = c->topk, NE = c->n_experts;
-    if (NE > 1024) {
-        fprintf(stderr, "glm53f: FATAL, routed experts is %d, above the limit of 1024.\n", NE);
-        abort();
-    }
-    if (T == 1 && g53h_cache_is(w->src) && decode_cached(out, x, w, c, with_shared) == 0) return;
     const float *xd = stage_in(&g_xin, x, (size_t)T * E);
-    int *idx_d = (int *)buf_get(&g_idx, (size_t)T * K * sizeof(int));
+    int *idx_d = (int *)buf_get(&g_idx, ((size_t)T * K + 1) * sizeof(int));
     float *w_d = (float *)buf_get(&g_w, (size_t)T * K * sizeof(float));
-    route_dev(idx_d, w_d, xd, T, w, c);
-    int *ids = (int *)malloc((size_t)T * K * sizeof(int));
-    int *uniq = (int *)malloc((size_t)T * K * sizeof(int));
-    unsigned char *seen = (unsigned char *)calloc((size_t)NE, 1);
-    G53hExpert *table = (G53hExpert *)calloc((size_t)NE, sizeof(G53hExpert));
-    unsigned char *got = (unsigned char *)calloc((size_t)NE, 1);
-    if (!ids || !uniq || !seen || !table || !got) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
-    if (g53h_d2h(ids, idx_d, (size_t)T * K * sizeof(int))) g53_die("glm53f_moe routing");
-    int nu = 0;
+    /* routing of every token, read back with the NaN flag in one copy */
+    {
+        int dt = 0;
+        const void *gate = resident_router(w->gate, (size_t)NE * E, &dt);
+        const float *bias = (const float *)resident(w->bias, (size_t)NE * sizeof(float));
+        int *flag_d = idx_d + (size_t)T * K;
+        if (g53h_memset(flag_d, 0, sizeof(int)) ||
+            g53h_router(idx_d, w_d, xd, T, gate, dt, bias, NE, E, K, c->norm_topk, c->routed_scale, flag_d))
+            g53_die("glm53f_router");
+    }
+    int *ids = (int *)pinned(&g_pin_back, &g_pin_back_n, ((size_t)64 * GLM53F_MAX_TOPK + 1 + 1024) * sizeof(int));
+    if (g53h_d2h(ids, idx_d, ((size_t)T * K + 1) * sizeof(int))) g53_die("glm53f_moe routing");
+    if (ids[(size_t)T * K]) {
+        fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) is below %d, above the limit of %d.\n", K, K);
+        abort();
+    }
+    int uniq[64 * GLM53F_MAX_TOPK], nu = 0;
+    unsigned char seen[1024];
+    memset(seen, 0, (size_t)NE);
     for (int i = 0; i < T * K; i++)
         if (!seen[ids[i]]) { seen[ids[i]] = 1; uniq[nu++] = ids[i]; }
+    if (T == 1) route_top16(w->layer, xd, w, c);
 
-    Glm53fExpertSrc *src = w->src;
-    const int prefetch = w->prefetch_n > 0 && src->hint != NULL;
+    read_switches();
+    const int prefetch = w->prefetch_n > 0 && src->hint != NULL && (T == 1 || !g_prefill_off);
     if (prefetch) {
         src->hint(src, w->layer, uniq, nu);
         if (w->next_gate) {
-            int pred[64 * 2 * GLM53F_MAX_TOPK];
-            const int np = predict_next(pred, x, xd, w, c, T);
-            if (np > 0) src->hint(src, w->layer + 1, pred, np);
+            int per = (T > 1 && g_prefill_pred >= 0) ? g_prefill_pred : w->prefetch_n;
+            if (per > 2 * GLM53F_MAX_TOPK) per = 2 * GLM53F_MAX_TOPK;
+            if (per > NE) per = NE;
+            static int pred[64 * 2 * GLM53F_MAX_TOPK];
+            if (T == 1) {
+                const int np = per > 0 ? predict_next(pred, xd, w, c, 1, per) : 0;
+                src->hint(src, w->layer + 1, pred, np);
+            } else if (per > 0 && (w->prefill_next || g_prefill_pred >= 0)) {
+                const int np = predict_next(pred, xd, w, c, T, per);
+                src->hint(src, w->layer + 1, pred, np);
+            }
         }
     }
 
-    /* Fetch the unique experts in first-seen order, in batches of at most topk so that a
-     * cache of topk+1 slots (the reference's minimum) never has more pinned at once; each
-     * batch is multiplied and then released. Contributions are kept per (token, slot) and
-     * combined in top-k order at the end, so the batching does not change the result. */
-    const int B = K < 16 ? K : 16;
+    /* the unique experts in first-seen order, in the reference's getmany batches of 16; within a
+     * batch at most topk of them are held at once (a cache of topk + 1 slots, the reference's
+     * minimum, must always find a victim), multiplied together and then released.
+     * Contributions are kept per (token, slot) and combined in top-k order at the end, so the
+     * batching does not change the result. */
+    const int B = K < G53_MOE_BATCH ? K : G53_MOE_BATCH;
     if (g_nhslots < B) {
         G53Slot *ns = (G53Slot *)realloc(g_hslots, (size_t)B * sizeof *ns);
         if (!ns) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
@@ -562,7 +722,7 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
     }
     const int nslots = K + (with_shared ? 1 : 0);
     G53hExpert *table_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
-    float *contrib = (float *)buf_get(&g_contrib, (size_t)T * nslots * E * sizeof(float));
+    G53hExpert *table = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
     G53hMoeLayer L;
     memset(&L, 0, sizeof L);
     L.hidden = E; L.inter = c->moe_inter; L.n_experts = NE; L.topk = K; L.norm_topk = c->norm_topk;
@@ -571,85 +731,92 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
     L.block_c = 128;
     /* a chunk of tokens takes the grouped matrix-core kernels when the layer qualifies: every
      * batch of fetched experts is multiplied for all its tokens at once */
-    const int grouped = T >= 2 && T <= g53h_grouped_max_tokens(&L) && (!with_shared || (w->sh_gate.bc == 128 &&
-                        w->sh_up.bc == 128 && w->sh_down.bc == 128));
+    const int grouped = T >= 2 && T <= g53h_grouped_max_tokens(&L) &&
+                        (!with_shared || (w->sh_gate.bc == 128 && w->sh_up.bc == 128 && w->sh_down.bc == 128));
+    float *contrib = grouped ? NULL : (float *)buf_get(&g_contrib, (size_t)T * nslots * E * sizeof(float));
     if (grouped) {                               /* the plan reserves the shared expert's rows */
         L.shared = with_shared ? table_d + NE : NULL;
         if (g53h_grouped_begin(xd, T, &L, idx_d)) g53_die("glm53f_moe");
     }
-    int *held = (int *)malloc((size_t)B * sizeof(int));
-    if (!held) { fprintf(stderr, "glm53f: FATAL, out of host memory\n"); abort(); }
-    for (int b0 = 0; b0 < nu || (b0 == 0 && with_shared); b0 += B) {
-        const int bn = (nu - b0) < B ? (nu - b0) : B;
-        int nh = 0, block_c = 128;
-        memset(table, 0, (size_t)NE * sizeof(G53hExpert));
-        if (bn > 0 && !prefetch && src->getmany) src->getmany(src, w->layer, uniq + b0, bn);
-        for (int u = b0; u < b0 + bn; u++) {
-            const int e = uniq[u];
-            Glm53fExpertQ q;
-            memset(&q, 0, sizeof q);
-            if (src->get(src, w->layer, e, &q) != 0) {
-                glm53f_expert_drops++;
-                fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this output is CORRUPT\n",
-                        w->layer, e);
-                table[e].gate.flags = G53H_MAT_DROPPED;           /* dropped: its contributions are zero */
-                continue;
+    int held[GLM53F_MAX_TOPK];
+    int first = 1;
+    for (int g0 = 0; g0 < nu || (g0 == 0 && with_shared); g0 += G53_MOE_BATCH) {
+        const int gn = (nu - g0) < G53_MOE_BATCH ? (nu - g0) : G53_MOE_BATCH;
+        if (gn > 0 && !prefetch && src->getmany) src->getmany(src, w->layer, uniq + g0, gn);
+        for (int b0 = g0; b0 < g0 + gn || (first && with_shared); b0 += B) {
+            const int bn = (g0 + gn - b0) < B ? (g0 + gn - b0) : B;
+            int nh = 0, block_c = 128;
+            memset(table, 0, (size_t)NE * sizeof(G53hExpert));
+            for (int u = b0; u < b0 + bn; u++) {
+                const int e = uniq[u];
+                Glm53fExpertQ q;
+                memset(&q, 0, sizeof q);
+                if (src->get(src, w->layer, e, &q) != 0) {
+                    glm53f_expert_drops++;
+                    fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this output is CORRUPT\n",
+                            w->layer, e);
+                    table[e].gate.flags = G53H_MAT_DROPPED;   /* its contributions are zero */
+                    continue;
+                }
+                held[nh++] = e;
+                check_expert_shape(&q, c, w->layer, e);
+                if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128) block_c = 0;
+                if (g53h_is_device_ptr(q.gate.w)) {
+                    table[e].gate = view_mat_f8(&q.gate);
+                    table[e].up = view_mat_f8(&q.up);
+                    table[e].down = view_mat_f8(&q.down);
+                } else {
+                    const size_t need = 3 * ((size_t)E * c->moe_inter + 256) + 3 * (mat_scale_bytes(&q.down) + 512);
+                    uint8_t *dst = (uint8_t *)buf_get(&g_hslots[u - b0].b, need);
+                    size_t off = 0;
+                    table[e].gate = stage_mat(&q.gate, dst, &off);
+                    table[e].up = stage_mat(&q.up, dst, &off);
+                    table[e].down = stage_mat(&q.down, dst, &off);
+                }
+                if (table[e].gate.flags & G53H_MAT_TILED) L.tiled = 1;
             }
-            held[nh++] = e;
-            check_expert_shape(&q, c, w->layer, e);
-            if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128) block_c = 0;
-            if (g53h_is_device_ptr(q.gate.w)) {
-                table[e].gate = view_mat_f8(&q.gate);
-                table[e].up = view_mat_f8(&q.up);
-                table[e].down = view_mat_f8(&q.down);
-            } else {
-                const size_t need = 3 * ((size_t)E * c->moe_inter + 256) + 3 * (mat_scale_bytes(&q.down) + 512);
-                uint8_t *dst = (uint8_t *)buf_get(&g_hslots[u - b0].b, need);
-                size_t off = 0;
-                table[e].gate = stage_mat(&q.gate, dst, &off);
-                table[e].up = stage_mat(&q.up, dst, &off);
-                table[e].down = stage_mat(&q.down, dst, &off);
-            }
-        }
-        L.shared = NULL;
-        if (with_shared && b0 == 0) {             /* the shared expert rides with the first batch */
-            G53hExpert sh;
-            sh.gate = dev_mat_resident(&w->sh_gate, "shared gate");
-            sh.up = dev_mat_resident(&w->sh_up, "shared up");
-            sh.down = dev_mat_resident(&w->sh_down, "shared down");
-            if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128) block_c = 0;
-            if (g53h_h2d(table_d + NE, &sh, sizeof sh)) g53_die("glm53f_moe");
-            L.shared = table_d + NE;
-        }
-        if (g53h_h2d(table_d, table, (size_t)NE * sizeof(G53hExpert))) g53_die("glm53f_moe");
-        L.block_c = block_c;
-        if (grouped) {
-            if (block_c != 128) {
-                fprintf(stderr, "glm53f: FATAL, a routed expert of layer %d has no 128-column blocks\n", w->layer);
-                abort();
-            }
-            if (g53h_grouped_batch(&L)) g53_die("glm53f_moe");
-        } else if (L.shared) {
-            if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
-        } else {
-            /* a layout with the shared slot still has K+1 slots per token */
-            G53hExpert none;
-            memset(&none, 0, sizeof none);
-            if (with_shared) {
-                if (g53h_h2d(table_d + NE, &none, sizeof none)) g53_die("glm53f_moe");
+            L.shared = NULL;
+            if (with_shared && first) {              /* the shared expert rides with the first batch */
+                G53hExpert sh;
+                sh.gate = dev_mat_resident(&w->sh_gate, "shared gate");
+                sh.up = dev_mat_resident(&w->sh_up, "shared up");
+                sh.down = dev_mat_resident(&w->sh_down, "shared down");
+                if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128) block_c = 0;
+                table[NE] = sh;
+                if (g53h_h2d_async(table_d + NE, table + NE, sizeof sh)) g53_die("glm53f_moe");
                 L.shared = table_d + NE;
             }
-            if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
+            if (g53h_h2d_async(table_d, table, (size_t)NE * sizeof(G53hExpert))) g53_die("glm53f_moe");
+            L.block_c = block_c;
+            if (grouped) {
+                if (block_c != 128) {
+                    fprintf(stderr, "glm53f: FATAL, a routed expert of layer %d has no 128-column blocks\n", w->layer);
+                    abort();
+                }
+                if (g53h_grouped_batch(&L)) g53_die("glm53f_moe");
+            } else if (L.shared) {
+                if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
+            } else {
+                /* a layout with the shared slot still has K+1 slots per token */
+                if (with_shared) {
+                    G53hExpert none;
+                    memset(&none, 0, sizeof none);
+                    table[NE] = none;
+                    if (g53h_h2d_async(table_d + NE, table + NE, sizeof none)) g53_die("glm53f_moe");
+                    L.shared = table_d + NE;
+                }
+                if (g53h_moe_partial(contrib, xd, T, &L, idx_d)) g53_die("glm53f_moe");
+            }
+            first = 0;
+            /* release the batch once the kernels that read it are done: the HBM cache orders that
+             * on the device (release records an event its next copy into the slot waits for); any
+             * other source, and the pinned table rewritten for the next batch, wait for the stream */
+            if (g53h_sync()) g53_die("glm53f_moe");
+            if (src->release)
+                for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
+            if (bn <= 0) break;
         }
-        /* release the batch once the kernels that read it are done: the HBM cache orders that
-         * on the device (release records an event its next copy into the slot waits for); any
-         * other source, or a next batch that rewrites the descriptor table, waits for the
-         * stream to drain */
-        if ((!g53h_cache_is(src) || b0 + B < nu) && g53h_sync()) g53_die("glm53f_moe");
-        if (src->release)
-            for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
     }
-    free(held);
     L.shared = with_shared ? table_d + NE : NULL;
     const int odev = g53h_is_device_ptr(out);
     float *od = odev ? out : (float *)buf_get(&g_out, (size_t)T * E * sizeof(float));
@@ -658,24 +825,40 @@ static void moe_impl(float *out, const float *x, const Glm53fMoeW *w, const Glm5
     } else if (g53h_moe_combine(od, contrib, w_d, T, &L)) {
         g53_die("glm53f_moe");
     }
+    int *errs = errors_enqueue();
     if (!odev) {
         if (g53h_d2h(out, od, (size_t)T * E * sizeof(float))) g53_die("glm53f_moe");
     } else if (g53h_sync()) {
         g53_die("glm53f_moe");
     }
-    free(ids); free(uniq); free(seen); free(table); free(got);
+    errors_check(errs, w->layer, K);
+}
+
+static void moe_layer(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T, int with_shared)
+{
+    if (T < 1) return;
+    ensure_device();
+    if (c->n_experts > 1024) {
+        fprintf(stderr, "glm53f: FATAL, routed experts is %d, above the limit of 1024.\n", c->n_experts);
+        abort();
+    }
+    /* chunks of 64 tokens, as src/core/glm53f_ops.c:1344-1362 */
+    for (int t0 = 0; t0 < T; t0 += G53_MOE_CHUNK) {
+        const int n = (T - t0) < G53_MOE_CHUNK ? (T - t0) : G53_MOE_CHUNK;
+        moe_chunk(out + (size_t)t0 * c->hidden, x + (size_t)t0 * c->hidden, w, c, n, with_shared);
+    }
 }
 
 void glm53f_moe(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T,
                 float *scratch)
 {
     (void)scratch;
-    moe_impl(out, x, w, c, T, 1);
+    moe_layer(out, x, w, c, T, 1);
 }
 
 void glm53f_moe_routed(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int T,
                        float *scratch)
 {
     (void)scratch;
-    moe_impl(out, x, w, c, T, 0);
+    moe_layer(out, x, w, c, T, 0);
 }

@@ -103,6 +103,15 @@ int g53h_router(int *idx_d, float *w_d, const float *x_d, int T, const void *gat
 int g53h_route_topn(int *idx_d, int n, const float *x_d, const void *gate_d, int gate_dt,
                     const float *bias_d, int n_experts, int hidden);
 
+/* route_topn for T tokens at once: idx [T][n]; score_out [T][n] (optional) receives the chosen
+ * experts' sigmoid scores (for the GLM53F_ROUTE_TOP16 trace, src/core/glm53f_ops.c:1044-1080). */
+int g53h_route_topn_batch(int *idx_d, float *score_out_d, int n, const float *x_d, int T, const void *gate_d,
+                          int gate_dt, const float *bias_d, int n_experts, int hidden);
+/* The prefill prediction's vote over ids_d [T][n] (replaces src/core/glm53f_ops.c:1206-1225):
+ * out_d[0] = the number of distinct experts, out_d[1 ..] = those experts, most voted first, ties
+ * in order of first appearance. out_d holds 1 + n_experts ints; n_experts <= 1024. */
+int g53h_vote(int *out_d, const int *ids_d, int T, int n, int n_experts);
+
 /* ---------------------------------------------------------------- MoE layer ---- */
 typedef struct {
     int   hidden, inter, n_experts, topk, norm_topk;
@@ -151,7 +160,8 @@ int g53h_moe_combine(float *out_d, const float *contrib_d, const float *w_d, int
  * g53h_moe takes this path for T >= 2 when g53h_set_grouped is on (the default; it returns the
  * previous setting) and the layer qualifies; otherwise the exact per-token kernels.
  * g53h_grouped_errors waits for the stream and returns, then clears, the grouped kernels' flags
- * (1: a routed index out of range, 8: an expert descriptor without the 128x128 layout). */
+ * (1: a routed index out of range, 2: a wait between waves timed out, 8: an expert descriptor
+ * without the 128x128 layout). */
 int g53h_moe_grouped(float *out_d, const float *x_d, int T, const G53hMoeLayer *L, int *idx_d,
                      float *w_d);
 /* The grouped layer in phases, for a host driver that fetches experts in batches (the C
@@ -184,6 +194,17 @@ int g53h_set_grouped_trace(void *dev_buf);
 int g53h_set_fused_decode(int on);
 int g53h_decode_errors(void);
 int g53h_decode_grid(void);
+/* Error flags of the layer kernels, for a caller that reads them with its own synchronisation
+ * (the C drop-in): enqueues on the compute stream a copy of the G53H_NERR flag words into
+ * host (pinned memory keeps the copy asynchronous), then clears them; host holds them once the
+ * stream has passed that point. [0] k_dec_layer and [1] k_dec_tiled (the bits of
+ * g53h_decode_errors), [2] the grouped path (the bits of g53h_grouped_errors). */
+#define G53H_NERR 3
+int g53h_errors_async(int *host);
+/* Test hook: the number of polls after which a wait on another workgroup of the one-launch
+ * decode kernels gives up (and sets bit 1 of their error flags); 0 restores the default.
+ * Returns the previous setting. Waits between the waves of one workgroup are not affected. */
+int g53h_set_spin_limit(int polls);
 /* Diagnostics: with dev_buf != NULL (device, grid x 32 uint64), the fused kernel's workgroups
  * record 100 MHz timestamps at their phase boundaries; NULL turns it off. */
 int g53h_set_decode_trace(void *dev_buf);

@@ -93,8 +93,11 @@ typedef struct {
 } Glm53fCfg;
 
 /* Storage formats of a matrix. Only GLM53F_WF8 is multiplied on the GPU by this library;
- * the router is fp32 (GLM53F_WF32) or bf16 (GLM53F_WBF16) bit patterns. */
-enum { GLM53F_WF32 = 0, GLM53F_WBF16 = 1, GLM53F_WF8 = 2, GLM53F_WI4 = 3 };
+ * the router is fp32 (GLM53F_WF32) or bf16 (GLM53F_WBF16) bit patterns. GLM53F_WF8T is this
+ * library's own: the expert views of its HBM cache (glm53f_cache.h) hold the same E4M3 codes in
+ * the octet-tiled layout of g53h.h (G53H_MAT_TILED), for its kernels; the reference never makes
+ * one. */
+enum { GLM53F_WF32 = 0, GLM53F_WBF16 = 1, GLM53F_WF8 = 2, GLM53F_WI4 = 3, GLM53F_WF8T = 0x102 };
 
 /* A self-describing matrix. For GLM53F_WF8, w holds rows*cols E4M3 codes row-major and s
  * the fp32 block scales [ceil(rows/br)][scols]; element (i,j) = E4M3(w[i*cols+j]) *

@@ -103,3 +103,81 @@ void ref_mm(float *y, const float *x, int T, const uint8_t *W, const float *S, i
 void ref_swiglu(float *y, const float *gu, int n, float limit) { glm53f_swiglu_clamp(y, gu, n, limit); }
 
 float ref_e4m3f(uint8_t b) { return glm53f_e4m3f(b); }
+
+/* The reference's expert-source protocol, recorded: the same in-memory experts behind a source
+ * whose get / release / getmany / hint append to a log ([1, layer, e] get, [2, layer, e]
+ * release, [3, layer, n, ids...] getmany, [4, layer, n, ids...] hint), with the next layer's
+ * router for the prediction. Returns the log length (ints), or -1 when it would overflow. */
+typedef struct {
+    MemSrc m;
+    int *log, cap, n, bad;
+} LogSrc;
+
+static void logv(LogSrc *s, int v)
+{
+    if (s->n < s->cap) s->log[s->n++] = v;
+    else s->bad = 1;
+}
+
+static int log_get(Glm53fExpertSrc *self, int layer, int e, Glm53fExpertQ *q)
+{
+    LogSrc *s = (LogSrc *)self;
+    logv(s, 1); logv(s, layer); logv(s, e);
+    return mem_get(self, layer, e, q);
+}
+
+static void log_release(Glm53fExpertSrc *self, int layer, int e)
+{
+    LogSrc *s = (LogSrc *)self;
+    logv(s, 2); logv(s, layer); logv(s, e);
+}
+
+static int log_getmany(Glm53fExpertSrc *self, int layer, const int *ids, int n)
+{
+    LogSrc *s = (LogSrc *)self;
+    logv(s, 3); logv(s, layer); logv(s, n);
+    for (int i = 0; i < n; i++) logv(s, ids[i]);
+    return 0;
+}
+
+static void log_hint(Glm53fExpertSrc *self, int layer, const int *ids, int n)
+{
+    LogSrc *s = (LogSrc *)self;
+    logv(s, 4); logv(s, layer); logv(s, n);
+    for (int i = 0; i < n; i++) logv(s, ids[i]);
+}
+
+int ref_moe_proto(float *out, const float *x, int T, int E, int I, int NE, int K, int br, int bc,
+                  int norm_topk, float routed_scale, float limit, const float *gate, const float *bias,
+                  const RefExpert *experts, const RefExpert *shared, int layer, const float *next_gate,
+                  const float *next_bias, int prefetch_n, int prefill_next, int with_hint, int with_getmany,
+                  int *log, int cap)
+{
+    Glm53fCfg c;
+    cfg_of(&c, E, I, NE, K, br, bc, norm_topk, routed_scale, limit);
+    c.n_layers = layer + 2;
+    LogSrc src;
+    memset(&src, 0, sizeof src);
+    src.m.src.get = log_get;
+    src.m.src.release = log_release;
+    src.m.src.getmany = with_getmany ? log_getmany : NULL;
+    src.m.src.hint = with_hint ? log_hint : NULL;
+    src.m.src.ctx = &src;
+    src.m.ex = experts; src.m.E = E; src.m.I = I; src.m.br = br; src.m.bc = bc;
+    src.log = log; src.cap = cap;
+    Glm53fMoeW w;
+    memset(&w, 0, sizeof w);
+    w.gate = gate; w.bias = bias; w.src = &src.m.src; w.layer = layer;
+    w.next_gate = next_gate; w.next_bias = next_bias;
+    w.prefetch_n = prefetch_n; w.prefill_next = prefill_next;
+    if (shared) {
+        fill(&w.sh_gate, shared->gw, shared->gs, I, E, br, bc);
+        fill(&w.sh_up, shared->uw, shared->us, I, E, br, bc);
+        fill(&w.sh_down, shared->dw, shared->ds, E, I, br, bc);
+    }
+    float *scratch = (float *)malloc(glm53f_moe_scratch(&c, T) * sizeof(float));
+    if (!scratch) return -1;
+    glm53f_moe(out, x, &w, &c, T, scratch);
+    free(scratch);
+    return src.bad ? -1 : src.n;
+}

@@ -65,6 +65,12 @@ def ref():
                                           C.c_void_p, C.c_void_p, C.c_void_p]
         L.ref_e4m3f.restype = C.c_float
         L.ref_e4m3f.argtypes = [C.c_uint8]
+        if hasattr(L, "ref_moe_proto"):
+            L.ref_moe_proto.restype = C.c_int
+            L.ref_moe_proto.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                        C.c_int, C.c_void_p, C.c_int]
         _ref = L
     return _ref
 
@@ -173,3 +179,26 @@ def fp8_kat_cases():
         cases.append(dict(rows=rows, cols=cols, br=br, bc=bc, with_nan=with_nan, w=w, s=s.astype(np.float32),
                           x=x.astype(np.float32)))
     return cases
+
+
+def ref_proto(sp, x, router, bias, mats_by_e, shared_mats, layer, next_router, next_bias, prefetch_n, prefill_next,
+              with_hint=True, with_getmany=True):
+    """The reference glm53f_moe's output and its recorded expert-source calls (ref_shim.c
+    ref_moe_proto): [1, L, e] get, [2, L, e] release, [3, L, n, ids] getmany, [4, L, n, ids] hint."""
+    R = ref()
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, sp.E)
+    T = x.shape[0]
+    out = np.zeros((T, sp.E), np.float32)
+    tab, keep = expert_table(mats_by_e, sp.NE)
+    sht, keep2 = expert_table({0: shared_mats}, 1)
+    router = np.ascontiguousarray(router, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    nr = np.ascontiguousarray(next_router, np.float32)
+    nb = np.ascontiguousarray(next_bias, np.float32)
+    log = np.zeros(1 << 20, np.int32)
+    n = R.ref_moe_proto(out.ctypes.data, x.ctypes.data, T, sp.E, sp.I, sp.NE, sp.K, sp.br, sp.bc, sp.norm_topk,
+                        sp.routed_scale, sp.limit, router.ctypes.data, bias.ctypes.data, C.addressof(tab),
+                        C.byref(sht[0]), layer, nr.ctypes.data, nb.ctypes.data, prefetch_n, prefill_next,
+                        int(with_hint), int(with_getmany), log.ctypes.data, len(log))
+    assert n >= 0
+    return out, log[:n].copy()
