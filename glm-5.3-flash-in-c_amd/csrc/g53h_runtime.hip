@@ -95,6 +95,20 @@ __global__ void k_errs_clear(int *e)
     if (threadIdx.x < G53H_NERR) e[threadIdx.x] = 0;
 }
 
+__global__ void k_errs_or(int *e, int word, int bits)
+{
+    if (threadIdx.x == 0) e[word] |= bits;
+}
+
+extern "C" int g53h_inject_errors(int word, int bits)
+{
+    if (g53h_ready()) return -1;
+    if (word < 0 || word >= G53H_NERR) return g53h_fail("g53h_inject_errors: word %d of %d", word, G53H_NERR);
+    hipLaunchKernelGGL(k_errs_or, dim3(1), dim3(64), 0, g_stream, g_errs, word, bits);
+    G53_LAUNCHED("k_errs_or");
+    return 0;
+}
+
 extern "C" int g53h_errors_async(int *host)
 {
     if (g53h_ready()) return -1;

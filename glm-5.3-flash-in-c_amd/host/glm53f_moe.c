@@ -170,11 +170,25 @@ static void check_f8(const Glm53fMat *m, const char *what)
                 what, m->br, m->bc, m->scols, m->cols);
         abort();
     }
+    if (m->dt == GLM53F_WF8T && (m->rows % 8 || m->cols % 128)) {
+        fprintf(stderr, "glm53f: FATAL, %s is octet-tiled with %d rows and %d columns (rows a multiple of 8, "
+                        "columns of 128)\n", what, m->rows, m->cols);
+        abort();
+    }
+}
+
+static void check_rowmajor(const Glm53fMat *m, const char *what)
+{
+    check_f8(m, what);
+    if (m->dt != GLM53F_WF8) {
+        fprintf(stderr, "glm53f: FATAL, %s is octet-tiled; layer weights are bound row-major (GLM53F_WF8)\n", what);
+        abort();
+    }
 }
 
 static G53hMat dev_mat_resident(const Glm53fMat *m, const char *what)
 {
-    check_f8(m, what);
+    check_rowmajor(m, what);
     G53hMat d;
     memset(&d, 0, sizeof d);
     d.w = (const uint8_t *)resident(m->w, mat_code_bytes(m));
@@ -213,7 +227,7 @@ static G53Buf g_xin, g_out, g_idx, g_w, g_flag, g_table, g_pred, g_tmp, g_contri
 static G53Buf g_tile_stage;
 static G53hMat dev_mat_resident_tiled(const Glm53fMat *m, const char *what)
 {
-    check_f8(m, what);
+    check_rowmajor(m, what);
     G53hMat d;
     memset(&d, 0, sizeof d);
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
@@ -644,10 +658,29 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off)
     *off += (cb + 255) & ~(size_t)255;
     uint8_t *s = dst + *off;
     *off += (sb + 255) & ~(size_t)255;
-    if (g53h_h2d(w, m->w, cb) || g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
+    if (m->dt == GLM53F_WF8T) {                 /* the chunk kernels read row-major codes */
+        uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
+        if (g53h_h2d(t, m->w, cb) || g53h_untile_f8(w, t, m->rows, m->cols)) g53_die("copying a host expert to HBM");
+    } else if (g53h_h2d(w, m->w, cb)) {
+        g53_die("copying a host expert to HBM");
+    }
+    if (g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
     d.w = w; d.s = (const float *)s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
-    d.flags = m->dt == GLM53F_WF8T ? G53H_MAT_TILED : 0;
+    return d;
+}
+
+/* An HBM view as the chunk kernels read it: row-major views as they are, octet-tiled ones
+ * converted into the staging slot (ordered on the stream before the kernels that read it). */
+static G53hMat rowmajor_view(const Glm53fMat *m, uint8_t *dst, size_t *off)
+{
+    G53hMat d = view_mat_f8(m);
+    if (m->dt != GLM53F_WF8T) return d;
+    uint8_t *w = dst + *off;
+    *off += (mat_code_bytes(m) + 255) & ~(size_t)255;
+    if (g53h_untile_f8(w, (const uint8_t *)m->w, m->rows, m->cols)) g53_die("converting a tiled expert view");
+    d.w = w;
+    d.flags = 0;
     return d;
 }
 
@@ -758,22 +791,25 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                     table[e].gate.flags = G53H_MAT_DROPPED;   /* its contributions are zero */
                     continue;
                 }
-                held[nh++] = e;
                 check_expert_shape(&q, c, w->layer, e);
                 if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128) block_c = 0;
-                if (g53h_is_device_ptr(q.gate.w)) {
-                    table[e].gate = view_mat_f8(&q.gate);
-                    table[e].up = view_mat_f8(&q.up);
-                    table[e].down = view_mat_f8(&q.down);
+                const size_t need = 3 * ((size_t)E * c->moe_inter + 256) + 3 * (mat_scale_bytes(&q.down) + 512);
+                const int dev = g53h_is_device_ptr(q.gate.w);
+                uint8_t *dst = (!dev || q.gate.dt == GLM53F_WF8T || q.up.dt == GLM53F_WF8T || q.down.dt == GLM53F_WF8T) ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
+                size_t off = 0;
+                if (dev) {
+                    held[nh++] = e;                      /* released once its kernels are queued */
+                    table[e].gate = rowmajor_view(&q.gate, dst, &off);
+                    table[e].up = rowmajor_view(&q.up, dst, &off);
+                    table[e].down = rowmajor_view(&q.down, dst, &off);
                 } else {
-                    const size_t need = 3 * ((size_t)E * c->moe_inter + 256) + 3 * (mat_scale_bytes(&q.down) + 512);
-                    uint8_t *dst = (uint8_t *)buf_get(&g_hslots[u - b0].b, need);
-                    size_t off = 0;
                     table[e].gate = stage_mat(&q.gate, dst, &off);
                     table[e].up = stage_mat(&q.up, dst, &off);
                     table[e].down = stage_mat(&q.down, dst, &off);
+                    /* the copies have completed: hand the views back at once, in the reference's
+                     * get / release order (src/core/glm53f_ops.c:1256-1328) */
+                    if (src->release) src->release(src, w->layer, e);
                 }
-                if (table[e].gate.flags & G53H_MAT_TILED) L.tiled = 1;
             }
             L.shared = NULL;
             if (with_shared && first) {              /* the shared expert rides with the first batch */

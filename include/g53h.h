@@ -205,6 +205,9 @@ int g53h_errors_async(int *host);
  * decode kernels gives up (and sets bit 1 of their error flags); 0 restores the default.
  * Returns the previous setting. Waits between the waves of one workgroup are not affected. */
 int g53h_set_spin_limit(int polls);
+/* Test hook: ORs bits into error word `word` (0 .. G53H_NERR-1) on the compute stream, as a
+ * kernel that hit that condition would; the caller's next read of the flags sees them. */
+int g53h_inject_errors(int word, int bits);
 /* Diagnostics: with dev_buf != NULL (device, grid x 32 uint64), the fused kernel's workgroups
  * record 100 MHz timestamps at their phase boundaries; NULL turns it off. */
 int g53h_set_decode_trace(void *dev_buf);
