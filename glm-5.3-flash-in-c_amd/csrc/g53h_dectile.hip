@@ -584,14 +584,15 @@ extern "C" int g53h_set_tiled_decode_trace(void *dev_buf)
 
 int g53h_decode_tiled_grid(void) { return g_dt_grid; }
 
-/* Launch k_dec_tiled; returns 1 when the layer is not one it takes (the caller falls back). */
-int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out,
-                      const int *idx_in, const float *w_in)
+static int dt_takes(const G53hMoeLayer *L, const int *idx_in)
 {
-    if (!L->tiled || L->block_c != 128 || L->hidden != G53_DEC_E || L->inter != G53_DEC_I ||
-        (!idx_in && (L->router_dt != 1 || !L->router)) ||
-        L->topk < 1 || L->topk > G53_DEC_MAXK || L->n_experts > G53_DEC_MAXNE)
-        return 1;
+    return L->tiled && L->block_c == 128 && L->hidden == G53_DEC_E && L->inter == G53_DEC_I &&
+           (idx_in || (L->router_dt == 1 && L->router)) && L->topk >= 1 && L->topk <= G53_DEC_MAXK &&
+           L->n_experts >= 1 && L->n_experts <= G53_DEC_MAXNE;
+}
+
+static int dt_size_grid(void)
+{
     if (g_dt_grid < 0) {
         const int cus = g53h_num_cus();
         int per = 0;
@@ -602,9 +603,38 @@ int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *id
             g_dt_grid = cus;
         }
     }
-    if (!g_dt_grid) return 1;
-    const size_t off_act = (size_t)G53_DEC_MAXNE * 8;
-    const size_t act_copy = (size_t)(G53_DEC_MAXK + 1) * G53_DEC_I * 8;
+    return g_dt_grid;
+}
+
+/* Scratch of one launch: tagged scores [G53_DEC_MAXNE], then G53_DT_ROT copies of the tagged
+ * activations [(G53_DEC_MAXK + 1) * G53_DEC_I], one per epoch in rotation. Tags are the epoch,
+ * so the memory needs clearing only when a fresh buffer starts and when the epoch wraps. */
+#define G53_DT_OFF_ACT ((size_t)G53_DEC_MAXNE * 8)
+#define G53_DT_ACT_COPY ((size_t)(G53_DEC_MAXK + 1) * G53_DEC_I * 8)
+#define G53_DT_SCRATCH (G53_DT_OFF_ACT + G53_DT_ROT * G53_DT_ACT_COPY)
+
+static void dt_launch(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out,
+                      const int *idx_in, const float *w_in, char *buf, unsigned epoch)
+{
+    G53TiledArgs e;
+    e.out = out; e.x = x; e.router = (const uint16_t *)L->router; e.bias = L->bias;
+    e.experts = L->experts; e.shared = L->shared;
+    e.score = (g53_u64 *)buf;
+    e.act = (g53_u64 *)(buf + G53_DT_OFF_ACT + (epoch % G53_DT_ROT) * G53_DT_ACT_COPY);
+    e.err = g53h_errblock() + 1; e.idx_out = idx_out; e.w_out = w_out; e.idx_in = idx_in; e.w_in = w_in;
+    e.NE = L->n_experts; e.K = L->topk; e.norm_topk = L->norm_topk; e.epoch = epoch;
+    e.spin = g53h_spin_limit(); e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dt_trace;
+    g53h_prof_mark(G53_PROF_START);
+    hipLaunchKernelGGL(k_dec_tiled, dim3(g_dt_grid), dim3(G53_DT_NT), 0, g53h_stream(), e);
+    g53h_prof_mark(G53_PROF_FUSED);
+}
+
+/* Launch k_dec_tiled; returns 1 when the layer is not one it takes (the caller falls back). */
+int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out,
+                      const int *idx_in, const float *w_in)
+{
+    if (!dt_takes(L, idx_in) || !dt_size_grid()) return 1;
+    const size_t off_act = G53_DT_OFF_ACT, act_copy = G53_DT_ACT_COPY;
     if (!g_dt_buf) {
         const size_t bytes = off_act + G53_DT_ROT * act_copy;
         G53_TRY(hipMalloc(&g_dt_buf, bytes));
@@ -619,18 +649,64 @@ int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *id
         G53_TRY(hipDeviceSynchronize());
         g_dt_epoch = 1;
     }
-    char *buf = (char *)g_dt_buf;
-    G53TiledArgs e;
-    e.out = out; e.x = x; e.router = (const uint16_t *)L->router; e.bias = L->bias;
-    e.experts = L->experts; e.shared = L->shared;
-    e.score = (g53_u64 *)buf;
-    e.act = (g53_u64 *)(buf + off_act + (g_dt_epoch % G53_DT_ROT) * act_copy);
-    e.err = g53h_errblock() + 1; e.idx_out = idx_out; e.w_out = w_out; e.idx_in = idx_in; e.w_in = w_in;
-    e.NE = L->n_experts; e.K = L->topk; e.norm_topk = L->norm_topk; e.epoch = g_dt_epoch;
-    e.spin = g53h_spin_limit(); e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dt_trace;
-    g53h_prof_mark(G53_PROF_START);
-    hipLaunchKernelGGL(k_dec_tiled, dim3(g_dt_grid), dim3(G53_DT_NT), 0, g53h_stream(), e);
+    (void)off_act; (void)act_copy;
+    dt_launch(out, x, L, idx_out, w_out, idx_in, w_in, (char *)g_dt_buf, g_dt_epoch);
     G53_LAUNCHED("k_dec_tiled");
-    g53h_prof_mark(G53_PROF_FUSED);
+    return 0;
+}
+
+/* ------------------------------------------------ the variant that allocates nothing ---- */
+/* The same launch with its scratch in this file-scope array (zero at load; each device holds
+ * its own copy until the process ends). Host code uses the per-device address from
+ * hipGetSymbolAddress, never the array's name. Calls that overlap on one device race. */
+static __device__ __align__(256) unsigned char scratch[G53_DT_SCRATCH];
+#define G53_NA_MAXDEV 64
+static void *g_na_ptr[G53_NA_MAXDEV];
+static unsigned g_na_epoch[G53_NA_MAXDEV];
+
+__global__ void k_na_clear(uint4 *p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0, 0, 0, 0);
+}
+
+/* Set-up, once per device with that device current (called by g53h_init). */
+int g53_noalloc_setup(int device)
+{
+    if (device < 0 || device >= G53_NA_MAXDEV) return g53h_fail("g53h_moe_decode_noalloc: device %d", device);
+    if (g_na_ptr[device]) return 0;
+    void *p = nullptr;
+    G53_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return g53h_fail("g53h_moe_decode_noalloc: no device address for the scratch array");
+    g_na_ptr[device] = p;
+    g_na_epoch[device] = 0;
+    return 0;
+}
+
+extern "C" int g53h_moe_decode_noalloc(float *out_d, const float *x_d, const G53hMoeLayer *L, int *idx_d,
+                                       float *w_d)
+{
+    const int dev = g53h_current_device();
+    if (dev < 0 || dev >= G53_NA_MAXDEV || !g_na_ptr[dev])
+        return g53h_fail("g53h_moe_decode_noalloc: call g53h_init on this device first");
+    if (!L || !out_d || !x_d || !L->experts) return g53h_fail("g53h_moe_decode_noalloc: missing argument");
+    if (L->n_experts < 1 || L->n_experts > G53_DEC_MAXNE)
+        return g53h_fail("g53h_moe_decode_noalloc: %d routed experts, above the limit of %d", L->n_experts,
+                         G53_DEC_MAXNE);
+    if (L->topk < 1 || L->topk > G53_DEC_MAXK)
+        return g53h_fail("g53h_moe_decode_noalloc: top-k %d, above the limit of %d", L->topk, G53_DEC_MAXK);
+    if (!dt_takes(L, nullptr))
+        return g53h_fail("g53h_moe_decode_noalloc: the layer must be octet-tiled with hidden %d, inter %d, "
+                         "128-column blocks and a bf16 router", G53_DEC_E, G53_DEC_I);
+    if (!dt_size_grid()) return g53h_fail("g53h_moe_decode_noalloc: the decode kernel does not fit this device");
+    char *buf = (char *)g_na_ptr[dev];
+    if (++g_na_epoch[dev] == 0) {                        /* wrapped: clear the tags, start over */
+        const size_t n = G53_DT_SCRATCH / 16;
+        hipLaunchKernelGGL(k_na_clear, dim3(1024), dim3(256), 0, g53h_stream(), (uint4 *)buf, n);
+        G53_LAUNCHED("k_na_clear");
+        g_na_epoch[dev] = 1;
+    }
+    dt_launch(out_d, x_d, L, idx_d, w_d, nullptr, nullptr, buf, g_na_epoch[dev]);
+    G53_LAUNCHED("k_dec_tiled");
     return 0;
 }

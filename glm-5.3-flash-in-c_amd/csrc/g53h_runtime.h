@@ -19,6 +19,8 @@ int  g53h_num_cus(void);
 /* Check the last kernel launch. */
 #define G53_LAUNCHED(name) do { if (g53h_check(hipGetLastError(), name, __FILE__, __LINE__)) return -1; } while (0)
 
+int g53h_current_device(void);        /* the device g53h_init bound, -1 before it      */
+int g53_noalloc_setup(int device);    /* scratch address of the no-alloc decode (init)  */
 hipStream_t g53h_stream(void);        /* compute stream (initialises on first use)      */
 hipStream_t g53h_copy_stream(void);   /* side stream for host-to-HBM expert copies     */
 

@@ -69,10 +69,13 @@ extern "C" int g53h_init(int device)
     G53_TRY(hipMalloc((void **)&g_errs, 64 * sizeof(int)));
     G53_TRY(hipMemset(g_errs, 0, 64 * sizeof(int)));
     G53_TRY(hipDeviceSynchronize());
+    if (g53_noalloc_setup(device)) return -1;
     g_device = device;
     g_ready = 1;
     return 0;
 }
+
+int g53h_current_device(void) { return g_ready ? g_device : -1; }
 
 extern "C" int g53h_ready(void) { return g_ready ? 0 : g53h_init(0); }
 extern "C" int g53h_num_cus(void) { return g_cus; }

@@ -172,6 +172,7 @@ _SIGS = {
     "g53h_vote": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "g53h_set_spin_limit": (C.c_int, [C.c_int]),
     "g53h_inject_errors": (C.c_int, [C.c_int, C.c_int]),
+    "g53h_moe_decode_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(G53hMoeLayer), C.c_void_p, C.c_void_p]),
     "g53h_set_tiled_decode_trace": (C.c_int, [C.c_void_p]),
     "g53h_tile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "g53h_untile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),

@@ -192,6 +192,16 @@ int g53h_set_grouped_trace(void *dev_buf);
  * then contributes zero), 0 if none. g53h_decode_grid returns the
  * fused kernel's workgroup count (0: unavailable, -1: not yet sized). */
 int g53h_set_fused_decode(int on);
+
+/* No counterpart in the reference: single-token decode that allocates nothing, for callers
+ * that cannot call hipMalloc (code under HIP graph capture, serving loops, harnesses that
+ * forbid it). Same result as g53h_moe at T = 1 through k_dec_tiled, bit for bit; the layer must
+ * be one that kernel takes (octet-tiled experts, hidden 4096, inter 2048, 128-column blocks,
+ * bf16 router), with n_experts <= 1024 and topk <= 15, else it fails with an error. Its scratch
+ * (tagged scores and activations, 4.2 MB) is a fixed device array each device holds until the
+ * process ends, set up by g53h_init; calls that overlap on one device race. out, x: device
+ * [hidden]; idx_d / w_d (device [topk]) receive the routing when non-NULL. */
+int g53h_moe_decode_noalloc(float *out_d, const float *x_d, const G53hMoeLayer *L, int *idx_d, float *w_d);
 int g53h_decode_errors(void);
 int g53h_decode_grid(void);
 /* Error flags of the layer kernels, for a caller that reads them with its own synchronisation
