@@ -306,11 +306,11 @@ def bench_stack(a):
     cf.routed_scale, cf.norm_topk, cf.swiglu_limit = base.routed_scale, base.norm_topk, base.limit
     cf.fp8_block_r, cf.fp8_block_c = 128, 128
     print(f"[bench] config 5: building the pinned host store ({NE} experts)", file=sys.stderr, flush=True)
-    st = glm53h.Glm53fSt()
+    st = glm53h.G53hStore()
     check(L.g53h_store_synth_init(C.byref(st), E, I, NL + 1, NE, NE, base.seed, C.c_float(base.expert_sigma)), "store")
     cache = glm53h.Glm53fCache()
     budget = 200 * 10 ** 9
-    if L.glm53f_cache_init(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io, 0) != 0:
+    if L.g53h_cache_init_store(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io) != 0:
         sys.exit("glm53f_cache_init failed")
     specs = [S.spec(3, layer=l) for l in range(NL)]
     W = [S.router_host(s_) for s_ in specs]

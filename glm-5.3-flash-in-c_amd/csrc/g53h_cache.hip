@@ -30,6 +30,7 @@
 #include "glm53f.h"
 #include "glm53f_cache.h"
 extern "C" {
+#include "../host/g53h_ckpt.h"
 #include "../host/g53h_lru.h"
 }
 
@@ -48,6 +49,8 @@ struct Copy {
 
 struct Impl {
     G53hLru lru;
+    const G53hStore *store = nullptr;       /* host experts from a caller's store, or       */
+    G53hCkpt *ckpt = nullptr;               /* ... read from the checkpoint into staging    */
     uint8_t *arena = nullptr;
     Geom geo;
     std::vector<hipEvent_t> landed;
@@ -62,6 +65,7 @@ struct Impl {
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
     std::mutex mu;
+    ~Impl() { g53h_ckpt_free(ckpt); }
 };
 
 double now_s()
@@ -75,7 +79,20 @@ size_t al(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 size_t scale_bytes(const Glm53fMat &m) { return (size_t)((m.rows + m.br - 1) / m.br) * m.scols * sizeof(float); }
 
-Impl *impl_of(const Glm53fCache *c) { return (Impl *)c->impl; }
+/* The library's state rides in the reference struct's int4-staging pointer, unused here. */
+Impl *impl_of(const Glm53fCache *c) { return (Impl *)(void *)c->stage; }
+
+int store_view(Impl *m, int layer, int expert, Glm53fExpertQ *h)
+{
+    if (m->ckpt) return g53h_ckpt_view(m->ckpt, layer, expert, h);
+    return m->store->view(m->store, layer, expert, h);
+}
+
+void store_done(Impl *m, int layer, int expert)
+{
+    if (m->ckpt) g53h_ckpt_done(m->ckpt, layer, expert);
+    else if (m->store->done) m->store->done(m->store, layer, expert);
+}
 
 void sync_stats(Glm53fCache *c, const Impl *m)
 {
@@ -85,6 +102,10 @@ void sync_stats(Glm53fCache *c, const Impl *m)
     c->prefetch_reads = m->lru.prefetch_reads;
     c->bg_reads = m->lru.bg_reads;
     c->bg_used = m->lru.bg_used;
+    c->clock = m->lru.clock;
+    c->qlen = m->lru.qlen;
+    c->hint_floor = m->lru.hint_floor;
+    c->last_hint = m->lru.last_hint;
 }
 
 /* Drop a slot's reference to its release event. */
@@ -104,7 +125,7 @@ void poll(Glm53fCache *c, Impl *m)
     for (size_t i = 0; i < m->inflight.size(); i++) {
         Copy &cp = m->inflight[i];
         if (hipEventQuery(cp.ev) == hipSuccess) {
-            if (c->st->done) c->st->done(c->st, cp.layer, cp.expert);
+            store_done(m, cp.layer, cp.expert);
             if (m->gen[cp.slot] == cp.gen) m->landed_ok[cp.slot] = 0;
             m->pool.push_back(cp.ev);
         } else {
@@ -126,12 +147,18 @@ int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t 
     *nread = 0;
     Glm53fExpertQ h;
     memset(&h, 0, sizeof h);
-    if (c->st->view(c->st, layer, expert, &h) != 0) return 0;
+    int rc = store_view(m, layer, expert, &h);
+    while (rc == G53H_CKPT_BUSY && !m->inflight.empty()) {     /* staging full: wait for a copy */
+        if (hipEventSynchronize(m->inflight.front().ev) != hipSuccess) return 0;
+        poll(c, m);
+        rc = store_view(m, layer, expert, &h);
+    }
+    if (rc != 0) return 0;
     const Glm53fMat *mats[3] = {&h.gate, &h.up, &h.down};
     for (int i = 0; i < 3; i++)
         if (!same_mat(*mats[i], m->geo, i)) {
             fprintf(stderr, "glm53f_cache: L%d expert %d does not have the slot's shape\n", layer, expert);
-            if (c->st->done) c->st->done(c->st, layer, expert);
+            store_done(m, layer, expert);
             return 0;
         }
     uint8_t *base = m->arena + (size_t)slot * (size_t)c->slot_bytes;
@@ -325,35 +352,25 @@ void cache_hint(Glm53fExpertSrc *self, int layer, const int *ids, int n)
 
 extern "C" int g53h_cache_is(const Glm53fExpertSrc *src) { return src && src->get == cache_get; }
 
-extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
-                                 int n_io, int i4)
+/* Common set-up once the store is known (m->store or m->ckpt). */
+static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t budget_bytes, int n_io)
 {
-    memset(c, 0, sizeof *c);
-    if (i4) {
-        fprintf(stderr, "glm53f_cache: int4 slots are not supported by the MI355X cache\n");
-        return -1;
-    }
-    if (!st || !st->view || !cfg) return -1;
-    if (g53h_ready()) {
-        fprintf(stderr, "glm53f_cache: %s\n", g53h_error());
-        return -1;
-    }
-    c->st = st;
     c->cfg = cfg;
     c->n_layers = cfg->n_layers + 1;       /* the MTP layer streams experts the same way */
     c->n_experts = cfg->n_experts;
+    c->hint_floor = c->last_hint = -1;
     int probe = -1;
     for (int L = 0; L < cfg->n_layers && L < GLM53F_MAX_LAYERS; L++)
         if (!cfg->is_dense[L]) { probe = L; break; }
-    if (probe < 0) return 0;               /* no MoE layers: nothing to cache */
+    if (probe < 0) { delete m; return 0; }  /* no MoE layers: nothing to cache */
     Glm53fExpertQ h;
     memset(&h, 0, sizeof h);
-    if (st->view(st, probe, 0, &h) != 0) {
+    if (store_view(m, probe, 0, &h) != 0) {
         fprintf(stderr, "glm53f_cache: cannot resolve expert 0 of layer %d\n", probe);
+        delete m;
         return -1;
     }
-    if (st->done) st->done(st, probe, 0);
-    Impl *m = new Impl();
+    store_done(m, probe, 0);
     const Glm53fMat *mats[3] = {&h.gate, &h.up, &h.down};
     size_t off = 0;
     for (int i = 0; i < 3; i++) {
@@ -402,19 +419,69 @@ extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53
         ok = hipEventCreateWithFlags(&m->landed[i], hipEventDisableTiming) == hipSuccess;
     m->demand = g53h_copy_stream();
     ok = ok && hipStreamCreateWithFlags(&m->prefetch, hipStreamNonBlocking) == hipSuccess;
-    c->impl = m;
+    c->stage = (unsigned char **)(void *)m;
     if (!ok) {
         fprintf(stderr, "glm53f_cache: cannot create the copy events and streams\n");
         glm53f_cache_free(c);
         return -1;
     }
+    c->arena = m->arena;
+    c->slot_of = m->lru.slot_of;
+    c->inflight_of = m->lru.inflight_of;
+    c->key_of = m->lru.key_of;
+    c->pins = m->lru.pins;
+    c->prefetched = m->lru.prefetched;
+    c->used_at = m->lru.used_at;
+    c->queued = m->lru.queued;
+    c->qcap = m->lru.qcap;
     c->n_io = n_io > 0 ? n_io : 0;
     c->src.get = cache_get;
     c->src.release = cache_release;
     c->src.getmany = cache_getmany;
     c->src.hint = cache_hint;
     c->src.ctx = c;
+    sync_stats(c, m);
     return 0;
+}
+
+extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
+                                 int n_io, int i4)
+{
+    memset(c, 0, sizeof *c);
+    if (i4) {
+        fprintf(stderr, "glm53f_cache: int4 slots are not supported by the MI355X cache\n");
+        return -1;
+    }
+    if (!st || !cfg) return -1;
+    if (g53h_ready()) {
+        fprintf(stderr, "glm53f_cache: %s\n", g53h_error());
+        return -1;
+    }
+    Impl *m = new Impl();
+    /* staging: one buffer per prefetch read in flight, plus room for demand reads */
+    m->ckpt = g53h_ckpt_new(st, cfg, cfg->n_layers + 1, (n_io > 0 ? n_io : 0) + 4);
+    if (!m->ckpt) {
+        fprintf(stderr, "glm53f_cache: cannot index the checkpoint or allocate pinned staging\n");
+        delete m;
+        return -1;
+    }
+    c->st = st;
+    const int rc = cache_setup(c, m, cfg, budget_bytes, n_io);
+    return rc;
+}
+
+extern "C" int g53h_cache_init_store(Glm53fCache *c, const G53hStore *store, const Glm53fCfg *cfg,
+                                     int64_t budget_bytes, int n_io)
+{
+    memset(c, 0, sizeof *c);
+    if (!store || !store->view || !cfg) return -1;
+    if (g53h_ready()) {
+        fprintf(stderr, "glm53f_cache: %s\n", g53h_error());
+        return -1;
+    }
+    Impl *m = new Impl();
+    m->store = store;
+    return cache_setup(c, m, cfg, budget_bytes, n_io);
 }
 
 extern "C" int glm53f_cache_sync(Glm53fCache *c)
@@ -486,7 +553,7 @@ struct SynthStore {
     size_t per, off[6];
 };
 
-int synth_view(const Glm53fSt *st, int layer, int expert, Glm53fExpertQ *h)
+int synth_view(const G53hStore *st, int layer, int expert, Glm53fExpertQ *h)
 {
     const SynthStore *s = (const SynthStore *)st->ctx;
     if (layer < 0 || layer >= s->n_layers || expert < 0 || expert >= s->n_experts) return -1;
@@ -508,7 +575,7 @@ int synth_view(const Glm53fSt *st, int layer, int expert, Glm53fExpertQ *h)
 
 } /* namespace */
 
-extern "C" int g53h_store_synth_init(Glm53fSt *st, int hidden, int inter, int n_layers, int n_experts, int n_pool,
+extern "C" int g53h_store_synth_init(G53hStore *st, int hidden, int inter, int n_layers, int n_experts, int n_pool,
                                      uint64_t seed, float sigma)
 {
     memset(st, 0, sizeof *st);
@@ -554,7 +621,7 @@ fail:
     return -1;
 }
 
-extern "C" void g53h_store_synth_free(Glm53fSt *st)
+extern "C" void g53h_store_synth_free(G53hStore *st)
 {
     SynthStore *s = (SynthStore *)st->ctx;
     if (s) {

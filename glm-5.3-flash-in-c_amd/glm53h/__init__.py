@@ -100,16 +100,40 @@ VIEW_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(Glm53fExp
 DONE_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_int)
 
 
-class Glm53fSt(C.Structure):
-    """include/glm53f_cache.h: the store the HBM expert cache reads experts from."""
+class G53hStore(C.Structure):
+    """include/glm53f_cache.h: a source of host-resident experts for g53h_cache_init_store."""
     _fields_ = [("view", VIEW_FN), ("done", DONE_FN), ("ctx", C.c_void_p)]
 
 
+class Glm53fTensor(C.Structure):
+    """include/glm53f_st.h (the reference reader's Glm53fTensor)."""
+    _fields_ = [("name", C.c_char_p), ("shard", C.c_int), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("shape", C.c_int64 * 8), ("off", C.c_int64), ("nbytes", C.c_int64)]
+
+
+class Glm53fSt(C.Structure):
+    """include/glm53f_st.h (the reference reader's Glm53fSt): the checkpoint index."""
+    _fields_ = [("fd", C.POINTER(C.c_int)), ("dfd", C.POINTER(C.c_int)), ("path", C.POINTER(C.c_char_p)),
+                ("nshard", C.c_int), ("t", C.POINTER(Glm53fTensor)), ("nt", C.c_int),
+                ("bucket", C.POINTER(C.c_int32)), ("nbucket", C.c_int), ("strpool", C.c_void_p),
+                ("strcap", C.c_size_t), ("strlen_", C.c_size_t)]
+
+
+_COND, _MUTEX = C.c_int64 * 6, C.c_int64 * 5        # glibc x86-64 pthread_cond_t, pthread_mutex_t (8-aligned)
+
+
 class Glm53fCache(C.Structure):
-    """include/glm53f_cache.h (src must stay first)."""
+    """include/glm53f_cache.h: the reference's Glm53fCache layout (src must stay first)."""
     _fields_ = [("src", Glm53fExpertSrc), ("st", C.c_void_p), ("cfg", C.c_void_p),
-                ("n_layers", C.c_int), ("n_experts", C.c_int), ("slot_bytes", C.c_int64),
-                ("nslot", C.c_int), ("n_io", C.c_int), ("impl", C.c_void_p),
+                ("n_layers", C.c_int), ("n_experts", C.c_int), ("arena", C.c_void_p), ("slot_bytes", C.c_int64),
+                ("nslot", C.c_int), ("i4", C.c_int), ("raw_bytes", C.c_int64), ("stage", C.c_void_p),
+                ("stage_busy", C.c_void_p), ("nstage", C.c_int), ("stage_free", _COND), ("i4_fd", C.c_void_p),
+                ("i4_layers", C.c_int), ("slot_of", C.POINTER(C.c_int32)), ("inflight_of", C.POINTER(C.c_int32)),
+                ("key_of", C.POINTER(C.c_int32)), ("pins", C.POINTER(C.c_int32)), ("prefetched", C.c_void_p),
+                ("used_at", C.POINTER(C.c_uint64)), ("ref", C.c_void_p), ("pad", C.c_void_p),
+                ("clock", C.c_uint64), ("mu", _MUTEX), ("landed", _COND), ("work", _COND), ("n_io", C.c_int),
+                ("io", C.c_void_p), ("stop", C.c_int), ("queue", C.c_void_p), ("qcap", C.c_int), ("qlen", C.c_int),
+                ("hint_floor", C.c_int), ("last_hint", C.c_int), ("queued", C.c_void_p),
                 ("hits", C.c_uint64), ("misses", C.c_uint64), ("evictions", C.c_uint64),
                 ("bytes_read", C.c_uint64), ("prefetch_reads", C.c_uint64), ("load_seconds", C.c_double),
                 ("bg_reads", C.c_uint64), ("bg_bytes", C.c_uint64), ("bg_used", C.c_uint64)]
@@ -213,9 +237,17 @@ _SIGS = {
     "glm53f_cache_report": (None, [C.POINTER(Glm53fCache), C.c_char_p]),
     "glm53f_cache_sync": (C.c_int, [C.POINTER(Glm53fCache)]),
     "g53h_cache_is": (C.c_int, [C.POINTER(Glm53fExpertSrc)]),
-    "g53h_store_synth_init": (C.c_int, [C.POINTER(Glm53fSt), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+    "g53h_cache_init_store": (C.c_int, [C.POINTER(Glm53fCache), C.POINTER(G53hStore), C.POINTER(Glm53fCfg),
+                                        C.c_int64, C.c_int]),
+    "g53h_st_open": (C.c_int, [C.POINTER(Glm53fSt), C.c_char_p, C.c_int]),
+    "g53h_st_close": (None, [C.POINTER(Glm53fSt)]),
+    "g53h_st_index": (C.c_int, [C.POINTER(Glm53fSt), C.c_char_p]),
+    "g53h_st_expert_bytes": (C.c_size_t, [C.POINTER(Glm53fCfg)]),
+    "g53h_st_read_expert": (C.c_int, [C.POINTER(Glm53fSt), C.POINTER(Glm53fCfg), C.c_int, C.c_int, C.c_void_p,
+                                      C.c_size_t, C.POINTER(Glm53fExpertQ)]),
+    "g53h_store_synth_init": (C.c_int, [C.POINTER(G53hStore), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                         C.c_uint64, C.c_float]),
-    "g53h_store_synth_free": (None, [C.POINTER(Glm53fSt)]),
+    "g53h_store_synth_free": (None, [C.POINTER(G53hStore)]),
     "g53h_lru_trace": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                                  C.c_void_p]),
 }

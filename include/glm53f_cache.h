@@ -18,56 +18,120 @@
  *     for it on the copy stream, so a slot is never overwritten while a kernel still reads it;
  *   - n_io is the number of prefetch copies kept in flight (0 disables prefetch), instead of a
  *     number of I/O threads;
- *   - the store is any Glm53fSt below, e.g. experts kept in pinned host memory, or a reader of
- *     the checkpoint (the reference's glm53f_expert_ref/glm53f_expert_load into a pinned
- *     staging buffer);
+ *   - glm53f_cache_init reads experts from the checkpoint index (Glm53fSt, the reference's
+ *     reader type): each missing expert is read from its shard into a pinned staging buffer
+ *     (two reads when its three weights and its three scale grids each lie in one run, as
+ *     the released checkpoint stores them, else six), then copied to the slot;
+ *   - g53h_cache_init_store takes any other source of host-resident experts (G53hStore
+ *     below), e.g. experts already in pinned host memory;
  *   - int4 slots (i4 != 0) are not supported: init returns -1.
  */
 #ifndef GLM53F_CACHE_H
 #define GLM53F_CACHE_H
 
+#include <pthread.h>
 #include <stdint.h>
 
 #include "glm53f.h"
+#include "glm53f_st.h"
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-/* Where the cache reads experts from. view() fills host views of the expert's three FP8
- * matrices (codes and fp32 scales, GLM53F_WF8) and returns 0, or -1 when the expert cannot be
- * read (get() then fails: a dropped expert). The bytes must stay valid until done() is called
- * for that expert (when the copy to HBM has completed); done may be NULL for a store whose
- * bytes never move. Calls come from the thread that calls the cache. */
-typedef struct Glm53fSt {
-    int  (*view)(const struct Glm53fSt *st, int layer, int expert, Glm53fExpertQ *host);
-    void (*done)(const struct Glm53fSt *st, int layer, int expert);
-    void *ctx;
-} Glm53fSt;
+#define GLM53F_SLOT_EMPTY     (-1)
+#define GLM53F_SLOT_INFLIGHT  (-2)
 
+/* The reference's cache struct (src/cache/glm53f_cache.h:44-96), field for field, so that its
+ * callers (the model code reads nslot, slot_bytes, i4_layers and the statistics, and passes
+ * &cache.src to the MoE layers) compile and read the right values unchanged. What each field
+ * holds here:
+ *   src                the expert source (get/getmany/release/hint) over the HBM slots
+ *   st, cfg            as given to glm53f_cache_init (st is NULL for g53h_cache_init_store)
+ *   arena              the HBM slot arena (a device pointer), nslot slots of slot_bytes
+ *   slot_of ... used_at, clock, qcap, qlen, hint_floor, last_hint, queued
+ *                      the LRU bookkeeping, with the reference's meaning (read-only for
+ *                      callers; clock is refreshed at each call)
+ *   n_io               prefetch copies kept in flight (0: prefetch off)
+ *   stage              this library's state (an opaque pointer; the int4 staging it names in
+ *                      the reference does not exist here, i4 is always 0)
+ *   statistics         as the reference's, reset by glm53f_cache_reset_stats
+ * Unused here, left zero: raw_bytes, stage_busy, nstage, stage_free, i4_fd, i4_layers, ref,
+ * pad, mu, landed, work, io, stop, queue. */
 typedef struct {
-    Glm53fExpertSrc  src;         /* MUST be first: pass &cache->src to Glm53fMoeW          */
+    Glm53fExpertSrc  src;             /* MUST be first: pass &cache->src to Glm53fMoeW */
+
     const Glm53fSt  *st;
     const Glm53fCfg *cfg;
     int              n_layers, n_experts;
+
+    unsigned char   *arena;
     int64_t          slot_bytes;
     int              nslot;
-    int              n_io;        /* prefetch copies in flight, 0 = prefetch disabled        */
-    void            *impl;        /* library state (slots in HBM, events, LRU bookkeeping)   */
-    /* statistics (reset by glm53f_cache_reset_stats), as the reference's */
+
+    int              i4;
+    int64_t          raw_bytes;
+    unsigned char  **stage;
+    unsigned char   *stage_busy;
+    int              nstage;
+    pthread_cond_t   stage_free;
+    int             *i4_fd;
+    int              i4_layers;
+
+    int32_t         *slot_of;         /* [n_layers*n_experts] -> resident slot, or -1  */
+    int32_t         *inflight_of;     /* [n_layers*n_experts] -> slot being read, or -1 */
+    int32_t         *key_of;          /* [nslot] -> key, EMPTY or INFLIGHT             */
+    int32_t         *pins;            /* [nslot] experts in use                        */
+    unsigned char   *prefetched;      /* [nslot] loaded by prefetch and not yet used    */
+    uint64_t        *used_at;         /* [nslot] LRU stamp                             */
+    void            *ref;             /* Glm53fExpertRef * in the reference; unused     */
+    int64_t         *pad;
+    uint64_t         clock;
+
+    pthread_mutex_t  mu;
+    pthread_cond_t   landed;
+    pthread_cond_t   work;
+
+    int              n_io;
+    pthread_t       *io;
+    int              stop;
+    int32_t         *queue;
+    int              qcap, qlen;
+    int              hint_floor, last_hint;
+    unsigned char   *queued;          /* [n_layers*n_experts] */
+
     uint64_t         hits, misses, evictions, bytes_read, prefetch_reads;
     double           load_seconds;    /* host time spent in get()/getmany()              */
     uint64_t         bg_reads, bg_bytes, bg_used;
 } Glm53fCache;
 
-/* budget_bytes is the HBM arena, rounded down to whole experts. The slot geometry comes from
- * expert 0 of the first MoE layer (cfg->is_dense), as the reference probes it. Fails (-1) if
- * fewer than topk+1 slots fit, if HBM cannot hold the arena, or for i4 != 0. */
+/* budget_bytes is the HBM arena, rounded down to whole experts. Experts are read from the
+ * checkpoint index st (tensor names "model.language_model.layers.L.mlp.experts.E.{gate,up,
+ * down}_proj.{weight,weight_scale_inv}", FP8 E4M3 codes with F32 scale grids); the slot geometry
+ * comes from expert 0 of the first MoE layer (cfg->is_dense), as the reference probes it.
+ * Fails (-1) if fewer than topk+1 slots fit, if HBM cannot hold the arena, if the probe expert
+ * is missing or not FP8, or for i4 != 0. */
 int  glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
                        int n_io, int i4);
 void glm53f_cache_free(Glm53fCache *c);
 void glm53f_cache_reset_stats(Glm53fCache *c);
 void glm53f_cache_report(const Glm53fCache *c, const char *label);
+
+/* Another source of host-resident experts. view() fills host views of the expert's three FP8
+ * matrices (codes and fp32 scales, GLM53F_WF8) and returns 0, or -1 when the expert cannot be
+ * read (get() then fails: a dropped expert). The bytes must stay valid until done() is called
+ * for that expert (when the copy to HBM has completed); done may be NULL for a store whose
+ * bytes never move. Calls come from the thread that calls the cache. */
+typedef struct G53hStore {
+    int  (*view)(const struct G53hStore *st, int layer, int expert, Glm53fExpertQ *host);
+    void (*done)(const struct G53hStore *st, int layer, int expert);
+    void *ctx;
+} G53hStore;
+
+/* glm53f_cache_init over a G53hStore instead of a checkpoint (no counterpart in the
+ * reference, whose cache always reads the checkpoint). */
+int  g53h_cache_init_store(Glm53fCache *c, const G53hStore *store, const Glm53fCfg *cfg, int64_t budget_bytes,
+                           int n_io);
 
 /* Wait until every copy the cache issued has landed (tests and benchmarks). */
 int  glm53f_cache_sync(Glm53fCache *c);
@@ -80,9 +144,9 @@ int  g53h_cache_is(const Glm53fExpertSrc *src);
  * per 128 x 128 block) of the given shapes; expert (layer, e) is pool entry
  * (layer * n_experts + e) % n_pool. For benchmarks and tests that need more experts than host
  * memory holds distinct copies of. */
-int  g53h_store_synth_init(Glm53fSt *st, int hidden, int inter, int n_layers, int n_experts, int n_pool,
+int  g53h_store_synth_init(G53hStore *st, int hidden, int inter, int n_layers, int n_experts, int n_pool,
                            uint64_t seed, float sigma);
-void g53h_store_synth_free(Glm53fSt *st);
+void g53h_store_synth_free(G53hStore *st);
 
 /* The LRU policy alone on a scripted trace (CPU, no device): ops are
  *   1 L E        get          -> out: rc, was resident (1/0), slot

@@ -74,13 +74,12 @@ class Layers:
 def new_cache(cf, st, slots, n_io):
     c = glm53h.Glm53fCache()
     L = glm53h.lib()
-    assert L.glm53f_cache_init(C.byref(c), C.byref(st), C.byref(cf), 0, 0, 0) == -1   # no slot fits
-    budget = 0
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), 0, 0) == -1   # no slot fits
     probe = glm53h.Glm53fCache()
-    assert L.glm53f_cache_init(C.byref(probe), C.byref(st), C.byref(cf), 1 << 30, 0, 0) == 0
+    assert L.g53h_cache_init_store(C.byref(probe), C.byref(st), C.byref(cf), 1 << 30, 0) == 0
     budget = probe.slot_bytes * slots
     L.glm53f_cache_free(C.byref(probe))
-    assert L.glm53f_cache_init(C.byref(c), C.byref(st), C.byref(cf), budget, n_io, 0) == 0
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), budget, n_io) == 0
     assert c.nslot == slots and L.g53h_cache_is(C.byref(c.src)) == 1
     return c
 
@@ -92,7 +91,7 @@ def test_cache_outputs_bit_identical(L):
     x = S.x_host(sp, 6, batch=2)
     say("cache: host-memory source (reference outputs)")
     want = ly.run(HostSrc(cf, ly.ex).src, cf, x)
-    st = glm53h.Glm53fSt()
+    st = glm53h.G53hStore()
     check(L.g53h_store_synth_init(C.byref(st), sp.E, sp.I, N_MOE_LAYERS + 1, sp.NE, sp.NE, sp.seed,
                                   C.c_float(sp.expert_sigma)), "store")
     try:
@@ -122,13 +121,13 @@ def test_cache_outputs_bit_identical(L):
 
 
 class PyStore:
-    """A Glm53fSt over host numpy arrays (pageable memory), failing for the dropped experts and
+    """A G53hStore over host numpy arrays (pageable memory), failing for the dropped experts and
     counting view/done calls."""
 
     def __init__(self, sp, ex, drop=()):
         self.sp, self.ex, self.drop = sp, ex, set(drop)
         self.views, self.dones = 0, 0
-        self.st = glm53h.Glm53fSt()
+        self.st = glm53h.G53hStore()
         self._v = glm53h.VIEW_FN(self.view)
         self._d = glm53h.DONE_FN(self.done)
         self.st.view, self.st.done = self._v, self._d
@@ -177,12 +176,13 @@ def test_cache_rejects_int4_and_tiny_budgets(L):
     ly = Layers(sp)
     store = PyStore(sp, ly.ex)
     c = glm53h.Glm53fCache()
-    assert L.glm53f_cache_init(C.byref(c), C.byref(store.st), C.byref(cf), 1 << 30, 0, 1) == -1
+    ckpt = glm53h.Glm53fSt()
+    assert L.glm53f_cache_init(C.byref(c), C.byref(ckpt), C.byref(cf), 1 << 30, 0, 1) == -1   # int4 slots
     probe = glm53h.Glm53fCache()
-    assert L.glm53f_cache_init(C.byref(probe), C.byref(store.st), C.byref(cf), 1 << 30, 0, 0) == 0
+    assert L.g53h_cache_init_store(C.byref(probe), C.byref(store.st), C.byref(cf), 1 << 30, 0) == 0
     sb = probe.slot_bytes
     L.glm53f_cache_free(C.byref(probe))
-    assert L.glm53f_cache_init(C.byref(c), C.byref(store.st), C.byref(cf), sb * sp.K, 0, 0) == -1   # < topk+1
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(store.st), C.byref(cf), sb * sp.K, 0) == -1   # < topk+1
 
 
 class PoolSrc:
@@ -242,7 +242,7 @@ def test_cache_config2_decode_through_fused_kernels(L):
     say("config 2 through host memory (general path)")
     host = PoolSrc(sp, pool)
     want = run(host.src, 0)
-    st = glm53h.Glm53fSt()
+    st = glm53h.G53hStore()
     check(L.g53h_store_synth_init(C.byref(st), sp.E, sp.I, 3, sp.NE, NP, sp.seed, C.c_float(sp.expert_sigma)), "store")
     try:
         for slots, n_io, pf in [(sp.K + 1, 0, 0), (12, 2, 6)]:

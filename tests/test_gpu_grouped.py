@@ -237,7 +237,7 @@ def test_dropin_grouped_batches_vs_exact_and_oracle(L):
 
     say("drop-in grouped through the HBM cache")
     cf.n_layers = 2
-    st = glm53h.Glm53fSt()
+    st = glm53h.G53hStore()
     check(L.g53h_store_synth_init(C.byref(st), sp.E, sp.I, 2, sp.NE, sp.NE, sp.seed, C.c_float(sp.expert_sigma)),
           "store")
     w = glm53h.Glm53fMoeW()
