@@ -287,20 +287,77 @@ def cpu_stack_layer(sp, W, b, x, sh, seconds):
                       f"reads), OpenMP threads {threads}, median of {len(times)} calls"}
 
 
+def route_dev(L, x, W, b, K):
+    """Top-K indices [T][K] of the device router (bf16 router weights) for host x [T][E]."""
+    T, E = x.shape
+    NE = W.shape[0]
+    gate = DevBuf.from_array((np.ascontiguousarray(W, np.float32).view(np.uint32) >> 16).astype(np.uint16))
+    xd, bd = DevBuf.from_array(np.ascontiguousarray(x, np.float32)), DevBuf.from_array(np.ascontiguousarray(b))
+    idx, wd, flag = DevBuf(T * K * 4), DevBuf(T * K * 4), DevBuf(4)
+    flag.zero()
+    check(L.g53h_router(idx.ptr, wd.ptr, xd.ptr, T, gate.ptr, 1, bd.ptr, NE, E, K, 1, C.c_float(2.5), flag.ptr),
+          "router")
+    return idx.download(np.int32).reshape(T, K)
+
+
+def routing_stats(ids, ranks, NE, K):
+    """(popularity exponent over ranks 2-200, token-to-token reuse) of routing ids [T][K] whose
+    experts have popularity ranks ranks[e] (0-based)."""
+    from glm53h import zipf
+    freq = np.bincount(ranks[ids.ravel()], minlength=NE) / ids.shape[0]
+    m = np.zeros((ids.shape[0], NE), bool)
+    np.put_along_axis(m, ids, True, 1)
+    return zipf.slope(freq), float((m[1:] & m[:-1]).sum() / (K * (ids.shape[0] - 1)))
+
+
+def stack_routing(L, W, B, X, specs, rho):
+    """The routing the run saw, measured on the device router: per-layer popularity ranks are
+    the bias order. Reported for the run's own tokens (all layers pooled by rank) and for a
+    2048-token continuation of layer 0's input chain (a sample long enough for the exponent)."""
+    NE, K = specs[0].NE, specs[0].K
+    NL = len(W)
+    ranks = [np.argsort(np.argsort(-B[l], kind="stable"), kind="stable") for l in range(NL)]
+    ids = [route_dev(L, np.ascontiguousarray(X[:, l]), W[l], B[l], K) for l in range(NL)]
+    freq = np.zeros(NE)
+    reuse_n = 0
+    for l in range(NL):
+        freq += np.bincount(ranks[l][ids[l].ravel()], minlength=NE)
+        m = np.zeros((ids[l].shape[0], NE), bool)
+        np.put_along_axis(m, ids[l], True, 1)
+        reuse_n += (m[1:] & m[:-1]).sum()
+    from glm53h import zipf
+    run_slope = zipf.slope(freq / (NL * X.shape[0]))
+    run_reuse = reuse_n / (NL * K * (X.shape[0] - 1))
+    rng = np.random.default_rng(55)
+    cur = X[-1, 0].astype(np.float64)
+    long_x = np.empty((2048, X.shape[2]), np.float32)
+    for t in range(2048):
+        cur = rho * cur + np.sqrt(1 - rho * rho) * rng.standard_normal(X.shape[2])
+        cur = (cur.astype(np.float32).view(np.uint32) + 0x8000 & 0xFFFF0000).view(np.float32).astype(np.float64)
+        long_x[t] = cur
+    s_long, r_long = routing_stats(route_dev(L, long_x, W[0], B[0], K), ranks[0], NE, K)
+    return {"target": {"zipf_s": specs[0].zipf_s, "reuse": 0.70, "rho": rho},
+            "run_tokens": {"tokens": int(NL * X.shape[0]), "zipf_slope": round(-run_slope, 3),
+                           "reuse": round(float(run_reuse), 3)},
+            "layer0_2048_tokens": {"zipf_slope": round(-s_long, 3), "reuse": round(r_long, 3)}}
+
+
 def bench_stack(a):
     """a 42-layer stack of routed-expert layers (config-2 shapes) in single-
     token decode, 32 steps, each layer one glm53f_moe call (the drop-in, with the reference's
     hint protocol: own experts, then the next layer's router on this input, prefetch_n 6). The
     experts come through the HBM cache (200 GB of slots) from pinned host memory. Per-layer
-    routers are seeded bf16 with a Zipf(1.1) selection bias over a per-layer permutation; each
-    layer's input follows x <- 0.9 x + sqrt(1 - 0.81) z (bf16), which reuses about 70% of a
-    layer's experts from one token to the next. The cache starts holding the 189 most popular
-    experts of every layer (7,938 experts, what 200 GB holds), the steady state of a long run."""
+    routers are seeded bf16; the selection bias is glm53h.zipf's calibrated curve (top-8
+    popularity min(1, c r^-1.1)) over a per-layer permutation, and each layer's input follows
+    x <- rho x + sqrt(1 - rho^2) z (bf16) with rho calibrated for 70% token-to-token reuse. Both
+    are measured back on the device router and reported. The cache starts holding the most
+    popular experts of every layer (what 200 GB holds), then warms up under the workload."""
     L = glm53h.init(0)
-    NL, steps, warm = 42, (a.steps if a.steps != 400 else 32), (a.warmup if a.warmup != 50 else 2)
+    NL, steps, warm = 42, (a.steps if a.steps != 400 else 32), (a.warmup if a.warmup != 50 else 8)
     base = S.spec(3)
     E, I, NE, K = base.E, base.I, base.NE, base.K
-    rho, pf, n_io = 0.9, 6, 4
+    from glm53h import zipf
+    rho, pf, n_io = zipf.table(NE, K, base.zipf_s)["rho"], 6, 4
     cf = glm53h.Glm53fCfg()
     cf.hidden, cf.n_layers, cf.n_experts, cf.topk, cf.n_shared, cf.moe_inter = E, NL, NE, K, 1, I
     cf.routed_scale, cf.norm_topk, cf.swiglu_limit = base.routed_scale, base.norm_topk, base.limit
@@ -329,7 +386,7 @@ def bench_stack(a):
     def bf16(v):
         return (np.asarray(v, np.float32).view(np.uint32) + 0x8000 & 0xFFFF0000).view(np.float32)
 
-    # every input of the run, made before the timed region: x <- 0.9 x + sqrt(1 - 0.81) z per layer
+    # every input of the run, made before the timed region: x <- rho x + sqrt(1 - rho^2) z per layer
     X = np.empty((warm + steps, NL, E), np.float32)
     cur = [bf16(rng.standard_normal(E)) for _ in range(NL)]
     for s_ in range(warm + steps):
@@ -386,6 +443,7 @@ def bench_stack(a):
             check(L.g53h_h2d(dbuf.ptr, m.w, m.rows * m.cols), "h2d")
     link = 16 * sum(m.rows * m.cols for m in mats) / (time.perf_counter() - t1) / 1e9
     L.glm53f_cache_report(C.byref(cache), b"config 5")
+    routing = stack_routing(L, W, B, X, specs, rho)
     nslot = cache.nslot
     L.glm53f_cache_free(C.byref(cache))
     L.g53h_store_synth_free(C.byref(st))
@@ -402,7 +460,10 @@ def bench_stack(a):
                    "layers": NL, "slots": nslot,
                    "prefetch_n": pf, "prefetch_reads_in_flight": n_io, "input_correlation": rho,
                    "parallelism": "single GPU"},
+        "routing": routing,
         "hit_rate": round(hits / max(hits + misses, 1), 4),
+        "miss_rate": round(misses / max(hits + misses, 1), 4),
+        "misses_per_token": round(misses / steps, 2),
         "requests": int(hits + misses), "misses": int(misses),
         "prefetch_reads": int(bg_reads), "prefetch_used": int(bg_used),
         "h2d_GB": round(h2d / 1e9, 3), "h2d_GBps_avg": round(h2d / dt / 1e9, 2), "h2d_link_GBps": round(link, 2),

@@ -73,16 +73,19 @@ def router_host(sp: LayerSpec):
 
 
 def bias_host(sp: LayerSpec):
-    """Selection bias [NE]: U(-a, a), or for a Zipf(s) popularity -0.1*(s/1.1)*ln(rank) over a
-    seeded permutation of ranks (calibrated so that top-8 selection frequency falls as rank^-s)."""
+    """Selection bias [NE]: U(-a, a), or for a Zipf(s) popularity the calibrated bias-by-rank
+    curve of glm53h.zipf (top-k selection probability min(1, c rank^-s)) over a seeded
+    permutation of ranks, one permutation per layer."""
     if sp.zipf_s is None:
         out = np.empty(sp.NE, np.float32)
         lib().g53h_synth_uniform_host(out.ctypes.data, sp.NE, sp.seed, stream(K_BIAS, sp.layer),
                                       C.c_float(sp.bias_a))
         return out
+    from . import zipf
+    curve = np.asarray(zipf.table(sp.NE, sp.K, sp.zipf_s)["bias_by_rank"], np.float64)
     rng = np.random.default_rng(sp.seed * 1000003 + sp.layer)
-    rank = rng.permutation(sp.NE) + 1
-    return (-0.1 * (sp.zipf_s / 1.1) * np.log(rank)).astype(np.float32)
+    rank = rng.permutation(sp.NE)                  # expert e has popularity rank rank[e] + 1
+    return curve[rank].astype(np.float32)
 
 
 def x_host(sp: LayerSpec, T, batch=0):

@@ -1,0 +1,108 @@
+"""Config 5 as a test: a stack of 8 routed-expert layers at the released shapes (hidden 4096,
+inter 2048, 288 experts, top-8, shared expert) in single-token decode through the drop-in and
+the HBM cache (src/cache/glm53f_cache.c:128-306 is the reference's), with the calibrated
+Zipf(1.1) routing and correlated inputs of the bench and a budget of 40 slots for 2,304
+experts, so reads, evictions and prefetch reads all happen. Sampled outputs equal the oracle's
+bit for bit; every output equals the one from a cache large enough to never evict, without
+prefetch (the cache decides what is resident when, never what a layer returns)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import glm53h
+import glm53h.synth as S
+import oracle_lib as O
+from glm53h import check, zipf
+from test_gpu_parity import cfg_struct, fmat, same, say
+
+pytestmark = pytest.mark.gpu
+NL, STEPS, NP = 8, 4, 24
+
+
+@pytest.fixture(scope="module")
+def L():
+    return glm53h.init(0)
+
+
+def test_stack_through_cache_with_misses(L):
+    sps = [S.spec(3, layer=l) for l in range(NL)]
+    sp = sps[0]
+    c = dict(E=sp.E, I=sp.I, NE=sp.NE, K=sp.K, routed_scale=sp.routed_scale, norm_topk=sp.norm_topk,
+             limit=sp.limit, br=sp.br, bc=sp.bc)
+    cf = cfg_struct(c)
+    cf.n_layers = NL
+    W = [S.router_host(s_) for s_ in sps]
+    B = [S.bias_host(s_) for s_ in sps]
+    sh = S.expert_host(S.spec(2), "shared")
+    rho = zipf.table(sp.NE, sp.K, sp.zipf_s)["rho"]
+    rng = np.random.default_rng(3)
+    bf = lambda v: (np.asarray(v, np.float32).view(np.uint32) + 0x8000 & 0xFFFF0000).view(np.float32)
+    X = np.empty((STEPS, NL, sp.E), np.float32)
+    cur = [bf(rng.standard_normal(sp.E)) for _ in range(NL)]
+    for t in range(STEPS):
+        for l in range(NL):
+            cur[l] = bf(rho * cur[l] + np.sqrt(1 - rho * rho) * rng.standard_normal(sp.E))
+            X[t, l] = cur[l]
+    store = glm53h.G53hStore()
+    say("building the pinned store of", NP, "experts")
+    check(L.g53h_store_synth_init(C.byref(store), sp.E, sp.I, NL + 1, sp.NE, NP, sp.seed, C.c_float(sp.expert_sigma)),
+          "store")
+
+    def run(slots, n_io, pf):
+        cache = glm53h.Glm53fCache()
+        probe = glm53h.Glm53fCache()
+        assert L.g53h_cache_init_store(C.byref(probe), C.byref(store), C.byref(cf), 1 << 30, 0) == 0
+        sb = probe.slot_bytes
+        L.glm53f_cache_free(C.byref(probe))
+        assert L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), sb * slots, n_io) == 0
+        outs = np.zeros((STEPS, NL, sp.E), np.float32)
+        try:
+            for t in range(STEPS):
+                for l in range(NL):
+                    w = glm53h.Glm53fMoeW()
+                    w.gate, w.bias = W[l].ctypes.data, B[l].ctypes.data
+                    (gw, gs), (uw, us), (dw, ds) = sh
+                    w.sh_gate = fmat(gw, gs, sp.I, sp.E, sp.br, sp.bc)
+                    w.sh_up = fmat(uw, us, sp.I, sp.E, sp.br, sp.bc)
+                    w.sh_down = fmat(dw, ds, sp.E, sp.I, sp.br, sp.bc)
+                    w.src = C.pointer(cache.src)
+                    w.layer, w.prefetch_n = l, pf
+                    if l + 1 < NL:
+                        w.next_gate, w.next_bias = W[l + 1].ctypes.data, B[l + 1].ctypes.data
+                    o = np.zeros((1, sp.E), np.float32)
+                    xt = np.ascontiguousarray(X[t, l:l + 1])
+                    L.glm53f_moe(o.ctypes.data, xt.ctypes.data, C.byref(w), C.byref(cf), 1, None)
+                    outs[t, l] = o[0]
+            check(L.glm53f_cache_sync(C.byref(cache)), "sync")
+            stats = dict(hits=cache.hits, misses=cache.misses, evictions=cache.evictions, bg_reads=cache.bg_reads,
+                         bg_used=cache.bg_used, bytes=cache.bytes_read + cache.bg_bytes)
+        finally:
+            L.glm53f_cache_free(C.byref(cache))
+        return outs, stats
+
+    try:
+        say("stack: 40 slots, prefetch 4 in flight, prefetch_n 6")
+        got, st = run(40, 4, 6)
+        say("stack stats", st)
+        assert st["misses"] > 0 and st["evictions"] > 0 and st["bg_reads"] > 0
+        assert st["hits"] + st["misses"] == STEPS * NL * sp.K
+        say("stack: 300 slots, no prefetch")
+        want, st2 = run(300, 0, 0)
+        assert st2["evictions"] == 0
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        pool = {}
+        for t, l in ((0, 0), (STEPS - 1, NL - 1), (2, 3)):
+            say("oracle check: token", t, "layer", l)
+            idx, _ = O.router(O.oracle(), X[t, l:l + 1], sps[l], W[l], B[l])
+            mats = {}
+            for e in idx[0]:
+                p = (l * sp.NE + int(e)) % NP
+                if p not in pool:
+                    pool[p] = S.expert_host(S.spec(2), p)
+                mats[int(e)] = pool[p]
+            o, oi, _ = O.moe(O.oracle(), X[t, l:l + 1], sps[l], W[l], B[l], mats, sh)
+            assert np.array_equal(oi, idx) and same(got[t, l], o[0])
+    finally:
+        L.g53h_store_synth_free(C.byref(store))
+        L.glm53f_forget_host_weights()
