@@ -21,6 +21,7 @@
 
 #include <mutex>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <time.h>
 #include <vector>
@@ -62,6 +63,10 @@ struct Impl {
     std::vector<int> used_free;
     int cur_used = -1;                      /* event recorded since the last get(), or -1   */
     hipStream_t demand = nullptr, prefetch = nullptr;
+    /* octet-tiled slots (G53H_MAT_TILED): a matrix's codes land in the stream's staging buffer and
+     * are tiled into the slot by a kernel on the same stream, so one buffer per stream suffices */
+    bool tiled = false;
+    uint8_t *stage_demand = nullptr, *stage_prefetch = nullptr;
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
     std::mutex mu;
@@ -167,10 +172,18 @@ int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t 
         unuse(m, slot);
     }
     if (m->landed_ok[slot] && hipStreamWaitEvent(s, m->landed[slot], 0) != hipSuccess) return 0;
+    uint8_t *stage = s == m->prefetch ? m->stage_prefetch : m->stage_demand;
     for (int i = 0; i < 3; i++) {
-        if (hipMemcpyAsync(base + m->geo.off[i], mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
-            hipMemcpyAsync(base + m->geo.off[3 + i], mats[i]->s, m->geo.bytes[3 + i], hipMemcpyHostToDevice, s) !=
-                hipSuccess)
+        if (m->tiled) {
+            if (hipMemcpyAsync(stage, mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
+                g53h_tile_f8_on(base + m->geo.off[i], stage, m->geo.rows[i], m->geo.cols[i], s))
+                return 0;
+        } else if (hipMemcpyAsync(base + m->geo.off[i], mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) !=
+                   hipSuccess) {
+            return 0;
+        }
+        if (hipMemcpyAsync(base + m->geo.off[3 + i], mats[i]->s, m->geo.bytes[3 + i], hipMemcpyHostToDevice, s) !=
+            hipSuccess)
             return 0;
         *nread += (int64_t)(m->geo.bytes[i] + m->geo.bytes[3 + i]);
     }
@@ -210,7 +223,7 @@ void view_of(const Glm53fCache *c, const Impl *m, int slot, Glm53fExpertQ *q)
         Glm53fMat &v = *mats[i];
         v.w = base + m->geo.off[i];
         v.s = (const float *)(base + m->geo.off[3 + i]);
-        v.dt = GLM53F_WF8;
+        v.dt = m->tiled ? GLM53F_WF8T : GLM53F_WF8;
         v.rows = m->geo.rows[i]; v.cols = m->geo.cols[i];
         v.br = m->geo.br[i]; v.bc = m->geo.bc[i]; v.scols = m->geo.scols[i];
     }
@@ -391,6 +404,11 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
         off = al(off + m->geo.bytes[3 + i], 256);
     }
     c->slot_bytes = (int64_t)al(off, 4096);
+    /* slots octet-tiled at the shapes the one-launch tiled decode reads (hidden 4096, inter
+     * 2048, 128 x 128 blocks), row-major otherwise or with GLM53F_CACHE_ROWMAJOR set */
+    m->tiled = !getenv("GLM53F_CACHE_ROWMAJOR") && m->geo.rows[0] == 2048 && m->geo.cols[0] == 4096 &&
+               m->geo.rows[1] == 2048 && m->geo.cols[1] == 4096 && m->geo.rows[2] == 4096 && m->geo.cols[2] == 2048;
+    for (int i = 0; i < 3; i++) m->tiled = m->tiled && m->geo.br[i] == 128 && m->geo.bc[i] == 128;
     c->nslot = (int)(budget_bytes / c->slot_bytes);
     if (c->nslot < cfg->topk + 1) {
         fprintf(stderr, "glm53f_cache: budget %.2f GB gives %d slots of %.2f MB; top-%d needs at least %d\n",
@@ -419,6 +437,12 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
         ok = hipEventCreateWithFlags(&m->landed[i], hipEventDisableTiming) == hipSuccess;
     m->demand = g53h_copy_stream();
     ok = ok && hipStreamCreateWithFlags(&m->prefetch, hipStreamNonBlocking) == hipSuccess;
+    if (ok && m->tiled) {
+        const size_t sb = m->geo.bytes[0] > m->geo.bytes[2] ? m->geo.bytes[0] : m->geo.bytes[2];
+        m->stage_demand = (uint8_t *)g53h_alloc(sb);
+        m->stage_prefetch = (uint8_t *)g53h_alloc(sb);
+        ok = m->stage_demand && m->stage_prefetch;
+    }
     c->stage = (unsigned char **)(void *)m;
     if (!ok) {
         fprintf(stderr, "glm53f_cache: cannot create the copy events and streams\n");
@@ -506,6 +530,8 @@ extern "C" void glm53f_cache_free(Glm53fCache *c)
         for (Copy &cp : m->inflight) (void)hipEventDestroy(cp.ev);
         if (m->prefetch) (void)hipStreamDestroy(m->prefetch);
         if (m->arena) g53h_free(m->arena);
+        g53h_free(m->stage_demand);
+        g53h_free(m->stage_prefetch);
         g53_lru_free(&m->lru);
         delete m;
     }

@@ -870,6 +870,7 @@ extern "C" int g53h_moe_grouped(float *out, const float *x, int T, const G53hMoe
 {
     if (g53h_ready()) return -1;
     if (!g53h_grouped_ok(L)) return g53h_fail("g53h_moe_grouped: layer shapes not supported");
+    if (L->tiled) return g53h_fail("g53h_moe_grouped: the grouped kernels read row-major expert codes, not octet-tiled");
     if (T < 0) return g53h_fail("g53h_moe_grouped: T %d", T);
     if (T == 0) return 0;
     const int K = L->topk, NE = L->n_experts;
@@ -930,6 +931,7 @@ extern "C" int g53h_grouped_begin(const float *x, int T, const G53hMoeLayer *L, 
 extern "C" int g53h_grouped_batch(const G53hMoeLayer *L)
 {
     if (!g_pass.active) return g53h_fail("g53h_grouped_batch: no pass begun");
+    if (L && L->tiled) return g53h_fail("g53h_grouped_batch: the grouped kernels read row-major expert codes, not octet-tiled");
     if (!L || L->n_experts != g_pass.a.NE || L->hidden != g_pass.a.E || L->inter != g_pass.a.I)
         return g53h_fail("g53h_grouped_batch: another layer than the pass's");
     if (L->shared && !g_pass.hs) return g53h_fail("g53h_grouped_batch: the pass was planned without a shared expert");

@@ -322,6 +322,15 @@ static int g53_check_layer(const G53hMoeLayer *L, int T)
     return 0;
 }
 
+/* Octet-tiled experts are read only by the single-token decode kernel k_dec_tiled (released
+ * shapes); every other kernel assumes row-major codes, so any other case is refused. */
+static int g53_tiled_refused(const char *fn, int T)
+{
+    return g53h_fail("%s: octet-tiled experts are read only by the single-token decode kernel (T = 1, hidden %d, "
+                     "inter %d, 128x128 blocks, top-k <= 15, bf16 router or given routing); this call has T = %d",
+                     fn, 4096, 2048, T);
+}
+
 extern "C" int g53h_moe_routed_given(float *out, const float *x, int T, const G53hMoeLayer *L,
                                      const int *idx, const float *wts)
 {
@@ -331,6 +340,7 @@ extern "C" int g53h_moe_routed_given(float *out, const float *x, int T, const G5
         const int r = g53h_decode_tiled(out, x, L, nullptr, nullptr, idx, wts);
         if (r <= 0) return r;
     }
+    if (L->tiled) return g53_tiled_refused("g53h_moe_routed_given", T);
     const size_t ssz = g53_slots_bytes(L, T), csz = g53_contrib_bytes(L, T);
     char *ws = (char *)g53h_workspace(ssz + csz + g53_layer_ws_bytes(L, T));
     if (!ws) return -1;
@@ -344,6 +354,7 @@ extern "C" int g53h_moe_partial(float *contrib, const float *x, int T, const G53
 {
     if (g53h_ready() || g53_check_layer(L, T)) return -1;
     if (T == 0) return 0;
+    if (L->tiled) return g53_tiled_refused("g53h_moe_partial", T);
     const size_t ssz = g53_slots_bytes(L, T);
     char *ws = (char *)g53h_workspace(ssz + g53_layer_ws_bytes(L, T));
     if (!ws) return -1;
@@ -371,6 +382,7 @@ extern "C" int g53h_moe(float *out, const float *x, int T, const G53hMoeLayer *L
                                : g53h_decode_fused(out, x, L, idx_out, w_out);
         if (r <= 0) return r;
     }
+    if (L->tiled) return g53_tiled_refused("g53h_moe", T);
     if (g53h_grouped_use(L, T)) return g53h_moe_grouped(out, x, T, L, idx_out, w_out);
     const int K = L->topk, NE = L->n_experts;
     const size_t rsz = align256((size_t)2 * T * NE * 4), isz = align256((size_t)T * K * 4);

@@ -315,19 +315,15 @@ extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
  * NULL the chosen experts' descriptors (and the shared expert's) are copied to slots[t][*], so
  * the expert kernels find their matrices with one load. NE <= 64 * NV. */
 template <int NV>
-__global__ void __launch_bounds__(256) k_router_select_w(int *__restrict__ idx, float *__restrict__ w,
-                                                         float *__restrict__ score, float *__restrict__ choice,
-                                                         const double *__restrict__ part, int S,
-                                                         const float *__restrict__ bias, int T, int NE, int K,
-                                                         int norm_topk, float routed_scale,
-                                                         int *__restrict__ nan_flag,
-                                                         const G53hExpert *__restrict__ experts,
-                                                         const G53hExpert *__restrict__ shared,
-                                                         G53hExpert *__restrict__ slots)
+__device__ __forceinline__ void g53_select_token(int t, int lane, int *__restrict__ idx, float *__restrict__ w,
+                                                 float *__restrict__ score, float *__restrict__ choice,
+                                                 const double *__restrict__ part, int S,
+                                                 const float *__restrict__ bias, int T, int NE, int K,
+                                                 int norm_topk, float routed_scale, int *__restrict__ nan_flag,
+                                                 int set_flag, const G53hExpert *__restrict__ experts,
+                                                 const G53hExpert *__restrict__ shared,
+                                                 G53hExpert *__restrict__ slots)
 {
-    const int lane = threadIdx.x & 63;
-    const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-    if (t >= T) return;
     uint32_t key[NV];
     int vid[NV];
     float vsc[NV];
@@ -412,7 +408,10 @@ __global__ void __launch_bounds__(256) k_router_select_w(int *__restrict__ idx, 
         key[NV - 1] = me ? 0u : key[NV - 1];
         pos++;
     }
-    if (pos < K && lane == 0 && nan_flag) atomicOr(nan_flag, 1);
+    if (lane == 0 && nan_flag) {
+        if (set_flag) *nan_flag = pos < K;                    /* one token: the flag's only writer */
+        else if (pos < K) atomicOr(nan_flag, 1);
+    }
     float wj = my_s;
     if (norm_topk) {
         double sum = 0.0;
@@ -433,6 +432,24 @@ __global__ void __launch_bounds__(256) k_router_select_w(int *__restrict__ idx, 
             ((int *)&slots[(size_t)t * nslots + j])[k] = ((const int *)src)[k];
         }
     }
+}
+
+template <int NV>
+__global__ void __launch_bounds__(256) k_router_select_w(int *__restrict__ idx, float *__restrict__ w,
+                                                         float *__restrict__ score, float *__restrict__ choice,
+                                                         const double *__restrict__ part, int S,
+                                                         const float *__restrict__ bias, int T, int NE, int K,
+                                                         int norm_topk, float routed_scale,
+                                                         int *__restrict__ nan_flag,
+                                                         const G53hExpert *__restrict__ experts,
+                                                         const G53hExpert *__restrict__ shared,
+                                                         G53hExpert *__restrict__ slots)
+{
+    const int lane = threadIdx.x & 63;
+    const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (t >= T) return;
+    g53_select_token<NV>(t, lane, idx, w, score, choice, part, S, bias, T, NE, K, norm_topk, routed_scale, nan_flag,
+                         0, experts, shared, slots);
 }
 
 /* slots[t][j] = experts[idx[t][j]] (j < K), slots[t][K] = *shared: the descriptor table of
@@ -559,11 +576,10 @@ __device__ inline void g53_argmax_merge(float &bv, int &bi, float ov, int oi)
 
 /* route_topn (src/core/glm53f_ops.c:1021-1042): the scan starts from expert 0, so a NaN at
  * index 0 wins every round and NaN elsewhere is skipped. */
-__global__ void __launch_bounds__(64) k_route_topn(int *__restrict__ idx, int n,
-                                                   const float *__restrict__ choice, int NE,
-                                                   const float *__restrict__ score, float *__restrict__ score_out)
+__device__ __forceinline__ void g53_topn_token(int t, int lane, int *__restrict__ idx, int n,
+                                               const float *__restrict__ choice, int NE,
+                                               const float *__restrict__ score, float *__restrict__ score_out)
 {
-    const int lane = threadIdx.x, t = blockIdx.x;
     choice += (size_t)t * NE;
     idx += (size_t)t * n;
     float c[G53_SEL_PER_LANE];
@@ -597,6 +613,60 @@ __global__ void __launch_bounds__(64) k_route_topn(int *__restrict__ idx, int n,
             if (score_out) score_out[(size_t)t * n + j] = score[(size_t)t * NE + best];
         }
     }
+}
+
+__global__ void __launch_bounds__(64) k_route_topn(int *__restrict__ idx, int n,
+                                                   const float *__restrict__ choice, int NE,
+                                                   const float *__restrict__ score, float *__restrict__ score_out)
+{
+    g53_topn_token((int)blockIdx.x, (int)threadIdx.x, idx, n, choice, NE, score, score_out);
+}
+
+/* One decode token's routing and next-layer prediction in two launches: the scores of both
+ * routers (blockIdx.y 0: this layer's, 1: the next layer's), then workgroup 0 selects the top-k
+ * with weights and writes the NaN flag (0 or 1), workgroup 1 the next layer's top-n. */
+__global__ void __launch_bounds__(64) k_router_scores2(float *__restrict__ sc0, float *__restrict__ ch0,
+                                                       const void *__restrict__ g0, int dt0,
+                                                       const float *__restrict__ b0,
+                                                       float *__restrict__ sc1, float *__restrict__ ch1,
+                                                       const void *__restrict__ g1, int dt1,
+                                                       const float *__restrict__ b1, const float *__restrict__ x,
+                                                       int NE, int E)
+{
+    const int lane = threadIdx.x, e = blockIdx.x, which = blockIdx.y;
+    const float d = g53_router_dot(which ? g1 : g0, which ? dt1 : dt0, e, E, x, lane);
+    if (lane == 0) {
+        const float s = g53_sigmoidf(d);
+        (which ? sc1 : sc0)[e] = s;
+        (which ? ch1 : ch0)[e] = s + (which ? b1 : b0)[e];
+    }
+}
+
+template <int NV>
+__global__ void __launch_bounds__(128) k_route_decode(int *__restrict__ idx, float *__restrict__ w,
+                                                      int *__restrict__ nan_flag, float *__restrict__ score,
+                                                      float *__restrict__ choice, const float *__restrict__ bias,
+                                                      int NE, int K, int norm_topk, float routed_scale,
+                                                      int *__restrict__ pred, int n, const float *__restrict__ nscore,
+                                                      const float *__restrict__ nchoice, unsigned *__restrict__ mb,
+                                                      int mb_slot, int mb_off_w, unsigned seq)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (wave == 0)
+        g53_select_token<NV>(0, lane, idx, w, score, choice, nullptr, 1, bias, 1, NE, K, norm_topk, routed_scale,
+                             nan_flag, 1, nullptr, nullptr, nullptr);
+    else if (n > 0)
+        g53_topn_token(0, lane, pred, n, nchoice, NE, nscore, nullptr);
+    if (!mb) return;
+    /* the host's copy: idx [K], the flag, pred [n], then the sequence word */
+    __threadfence_block();
+    __syncthreads();
+    unsigned *d = mb + mb_off_w;
+    for (int i = threadIdx.x; i < K + 1 + n; i += 128)
+        d[i] = (unsigned)(i < K ? idx[i] : i == K ? nan_flag[0] : pred[i - K - 1]);
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(mb + mb_slot, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 /* The prefill prediction's vote (src/core/glm53f_ops.c:1206-1225): the experts named in ids
@@ -675,5 +745,37 @@ extern "C" int g53h_vote(int *out, const int *ids, int T, int n, int NE)
     if (T < 0 || n < 0) return g53h_fail("g53h_vote: %d x %d ids", T, n);
     hipLaunchKernelGGL(k_vote, dim3(1), dim3(1024), 0, g53h_stream(), out, ids, T, n, NE);
     G53_LAUNCHED("k_vote");
+    return 0;
+}
+
+extern "C" int g53h_route_decode(int *idx, float *w, int *nan_flag, int *pred, int n, const float *x, const void *gate,
+                                 int gate_dt, const float *bias, const void *next_gate, int next_dt,
+                                 const float *next_bias, int NE, int E, int K, int norm_topk, float routed_scale,
+                                 int mb_slot, unsigned seq, size_t mb_off)
+{
+    if (g53h_ready()) return -1;
+    if (NE < 1 || NE > 1024) return g53h_fail("g53h_route_decode: %d experts (max 1024)", NE);
+    if (K < 1 || K > NE || K > GLM53F_MAX_TOPK_DEV) return g53h_fail("g53h_route_decode: topk %d", K);
+    const int pn = next_gate && n > 0;
+    if (pn && n > NE) return g53h_fail("g53h_route_decode: %d of %d experts", n, NE);
+    if (!pn) n = 0;
+    if (mb_slot >= 0 && (mb_slot >= G53H_MBOX_SLOTS || mb_off % 4 || mb_off < G53H_MBOX_SLOTS * 4 ||
+                         mb_off + 4 * (size_t)(K + 1 + n) > G53H_MBOX_BYTES))
+        return g53h_fail("g53h_route_decode: mailbox slot %d offset %zu", mb_slot, mb_off);
+    float *ws = (float *)g53h_workspace((size_t)4 * NE * sizeof(float));
+    if (!ws) return -1;
+    float *sc0 = ws, *ch0 = ws + NE, *sc1 = ws + 2 * NE, *ch1 = ws + 3 * NE;
+    hipLaunchKernelGGL(k_router_scores2, dim3(NE, pn ? 2 : 1), dim3(64), 0, g53h_stream(), sc0, ch0, gate, gate_dt,
+                       bias, sc1, ch1, pn ? next_gate : gate, next_dt, pn ? next_bias : bias, x, NE, E);
+    G53_LAUNCHED("k_router_scores2");
+    unsigned *mb = mb_slot >= 0 ? g53h_mailbox_dev() : nullptr;
+    const int off_w = (int)(mb_off / 4);
+    if (NE <= 320)
+        hipLaunchKernelGGL(k_route_decode<5>, dim3(1), dim3(128), 0, g53h_stream(), idx, w, nan_flag, sc0, ch0, bias,
+                           NE, K, norm_topk, routed_scale, pred, n, sc1, ch1, mb, mb_slot, off_w, seq);
+    else
+        hipLaunchKernelGGL(k_route_decode<16>, dim3(1), dim3(128), 0, g53h_stream(), idx, w, nan_flag, sc0, ch0, bias,
+                           NE, K, norm_topk, routed_scale, pred, n, sc1, ch1, mb, mb_slot, off_w, seq);
+    G53_LAUNCHED("k_route_decode");
     return 0;
 }

@@ -19,10 +19,13 @@ int  g53h_num_cus(void);
 /* Check the last kernel launch. */
 #define G53_LAUNCHED(name) do { if (g53h_check(hipGetLastError(), name, __FILE__, __LINE__)) return -1; } while (0)
 
+unsigned *g53h_mailbox_dev(void);    /* device address of the host mailbox             */
 int g53h_current_device(void);        /* the device g53h_init bound, -1 before it      */
 int g53_noalloc_setup(int device);    /* scratch address of the no-alloc decode (init)  */
 hipStream_t g53h_stream(void);        /* compute stream (initialises on first use)      */
 hipStream_t g53h_copy_stream(void);   /* side stream for host-to-HBM expert copies     */
+/* g53h_tile_f8 on stream s (the expert cache tiles on its copy streams). */
+int g53h_tile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, hipStream_t s);
 
 /* Library workspace in HBM, grown on demand (grow = sync + free + alloc), 256-B aligned.
  * Regions are carved from it per call; nothing in it survives between calls except the

@@ -20,6 +20,8 @@ static void       *g_ws = nullptr;
 static size_t      g_ws_bytes = 0;
 static int        *g_counters = nullptr;
 static int        *g_errs = nullptr;   /* [0] k_dec_layer, [1] k_dec_tiled, [2] grouped path   */
+static unsigned   *g_mbox = nullptr;   /* host mailbox: pinned, mapped, written by kernels      */
+static unsigned   *g_mbox_d = nullptr; /* its device address                                    */
 
 extern "C" int g53h_fail(const char *fmt, ...)
 {
@@ -68,6 +70,9 @@ extern "C" int g53h_init(int device)
     G53_TRY(hipMemset(g_counters, 0, 4096 * sizeof(int)));
     G53_TRY(hipMalloc((void **)&g_errs, 64 * sizeof(int)));
     G53_TRY(hipMemset(g_errs, 0, 64 * sizeof(int)));
+    G53_TRY(hipHostMalloc((void **)&g_mbox, G53H_MBOX_BYTES, hipHostMallocMapped | hipHostMallocCoherent));
+    memset(g_mbox, 0, G53H_MBOX_BYTES);
+    G53_TRY(hipHostGetDevicePointer((void **)&g_mbox_d, g_mbox, 0));
     G53_TRY(hipDeviceSynchronize());
     if (g53_noalloc_setup(device)) return -1;
     g_device = device;
@@ -83,6 +88,48 @@ hipStream_t g53h_stream(void) { return g_stream; }
 hipStream_t g53h_copy_stream(void) { return g_copy; }
 int *g53h_counters(void) { return g_counters; }
 int *g53h_errblock(void) { return g_errs; }
+unsigned *g53h_mailbox_dev(void) { return g_mbox_d; }
+
+extern "C" void *g53h_mailbox(void) { return g53h_ready() ? nullptr : (void *)g_mbox; }
+
+extern "C" int g53h_mailbox_wait(int slot, unsigned seq)
+{
+    if (g53h_ready()) return -1;
+    if (slot < 0 || slot >= G53H_MBOX_SLOTS) return g53h_fail("g53h_mailbox_wait: slot %d", slot);
+    const volatile unsigned *w = g_mbox + slot;
+    /* spin while the stream works; after ~1e6 polls fall back to a blocking wait, which also
+     * reports an error the stream hit (then the word never arrives) */
+    for (long i = 0; i < (1L << 20); i++)
+        if (__atomic_load_n(w, __ATOMIC_ACQUIRE) == seq) return 0;
+    G53_TRY(hipStreamSynchronize(g_stream));
+    if (__atomic_load_n(w, __ATOMIC_ACQUIRE) == seq) return 0;
+    return g53h_fail("g53h_mailbox_wait: slot %d never reached %u", slot, seq);
+}
+
+/* One workgroup: n bytes (a multiple of 4) from src and the G53H_NERR error words into the
+ * mailbox data area at byte offset off, then the sequence word of slot. */
+__global__ void __launch_bounds__(256) k_publish(unsigned *__restrict__ mb, const uint32_t *__restrict__ src, int nw,
+                                                 const int *__restrict__ errs, int off_w, int slot, unsigned seq)
+{
+    uint32_t *d = mb + off_w;
+    for (int i = threadIdx.x; i < G53H_NERR; i += 256) d[i] = (uint32_t)errs[i];
+    for (int i = threadIdx.x; i < nw; i += 256) d[G53H_NERR + i] = src[i];
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(mb + slot, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+extern "C" int g53h_publish(int slot, unsigned seq, size_t off, const void *src_d, size_t bytes)
+{
+    if (g53h_ready()) return -1;
+    if (slot < 0 || slot >= G53H_MBOX_SLOTS || off % 4 || bytes % 4 || off < G53H_MBOX_SLOTS * 4 ||
+        off + (G53H_NERR * 4) + bytes > G53H_MBOX_BYTES)
+        return g53h_fail("g53h_publish: slot %d, %zu bytes at %zu", slot, bytes, off);
+    hipLaunchKernelGGL(k_publish, dim3(1), dim3(256), 0, g_stream, g_mbox_d, (const uint32_t *)src_d, (int)(bytes / 4),
+                       g_errs, (int)(off / 4), slot, seq);
+    G53_LAUNCHED("k_publish");
+    return 0;
+}
 
 static int g_spin = 0;
 extern "C" int g53h_set_spin_limit(int polls)
@@ -109,6 +156,13 @@ extern "C" int g53h_inject_errors(int word, int bits)
     if (word < 0 || word >= G53H_NERR) return g53h_fail("g53h_inject_errors: word %d of %d", word, G53H_NERR);
     hipLaunchKernelGGL(k_errs_or, dim3(1), dim3(64), 0, g_stream, g_errs, word, bits);
     G53_LAUNCHED("k_errs_or");
+    return 0;
+}
+
+extern "C" int g53h_errors_peek_async(int *host)
+{
+    if (g53h_ready()) return -1;
+    G53_TRY(hipMemcpyAsync(host, g_errs, G53H_NERR * sizeof(int), hipMemcpyDeviceToHost, g_stream));
     return 0;
 }
 
@@ -184,6 +238,14 @@ extern "C" int g53h_d2h(void *dst, const void *src, size_t n)
     if (!n) return 0;
     G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_stream));
     G53_TRY(hipStreamSynchronize(g_stream));
+    return 0;
+}
+
+extern "C" int g53h_d2h_async(void *dst, const void *src, size_t n)
+{
+    if (g53h_ready()) return -1;
+    if (!n) return 0;
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_stream));
     return 0;
 }
 

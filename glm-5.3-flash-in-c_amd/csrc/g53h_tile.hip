@@ -62,15 +62,20 @@ int g53_tile_shape(int rows, int cols)
 
 } /* namespace */
 
-extern "C" int g53h_tile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols)
+int g53h_tile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, hipStream_t s)
 {
     if (g53h_ready() || g53_tile_shape(rows, cols)) return -1;
     if (dst_d == src_d) return g53h_fail("g53h_tile_f8: in-place conversion is not supported");
     const long nrun = (long)rows * cols / 16;
-    hipLaunchKernelGGL(k_tile_f8, dim3((unsigned)((nrun + 255) / 256)), dim3(256), 0, g53h_stream(), dst_d, src_d,
-                       cols, nrun);
+    hipLaunchKernelGGL(k_tile_f8, dim3((unsigned)((nrun + 255) / 256)), dim3(256), 0, s, dst_d, src_d, cols, nrun);
     G53_LAUNCHED("k_tile_f8");
     return 0;
+}
+
+extern "C" int g53h_tile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols)
+{
+    if (g53h_ready()) return -1;
+    return g53h_tile_f8_on(dst_d, src_d, rows, cols, g53h_stream());
 }
 
 extern "C" int g53h_untile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols)

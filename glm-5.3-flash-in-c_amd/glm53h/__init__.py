@@ -166,6 +166,9 @@ _SIGS = {
     "g53h_swiglu": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_float]),
     "g53h_router": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                               C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_void_p]),
+    "g53h_route_decode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
+                                    C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                    C.c_int, C.c_float, C.c_int, C.c_uint, C.c_size_t]),
     "g53h_route_topn": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                                   C.c_int, C.c_int]),
     "g53h_moe": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.POINTER(G53hMoeLayer), C.c_void_p,
@@ -196,6 +199,11 @@ _SIGS = {
     "g53h_vote": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "g53h_set_spin_limit": (C.c_int, [C.c_int]),
     "g53h_inject_errors": (C.c_int, [C.c_int, C.c_int]),
+    "g53h_errors_peek_async": (C.c_int, [C.c_void_p]),
+    "g53h_mailbox": (C.c_void_p, []),
+    "g53h_mailbox_wait": (C.c_int, [C.c_int, C.c_uint]),
+    "g53h_publish": (C.c_int, [C.c_int, C.c_uint, C.c_size_t, C.c_void_p, C.c_size_t]),
+    "g53h_d2h_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_moe_decode_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(G53hMoeLayer), C.c_void_p, C.c_void_p]),
     "g53h_set_tiled_decode_trace": (C.c_int, [C.c_void_p]),
     "g53h_tile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),

@@ -35,22 +35,34 @@ static void g53_die(const char *what)
 }
 
 /* ------------------------------------------------------------ resident weights ---- */
-/* An entry is found by host address and checked against the size and a signature of 64 words
- * sampled across the bytes: a caller that frees its weights and reuses the address for others
- * gets them uploaded again instead of the stale copy. */
-typedef struct { const void *h; size_t n; void *d; int dt; uint64_t sig; } G53Res;
+/* An entry is found by host address and checked against the host size and 16 words sampled
+ * across the bytes, recorded at upload: a caller that frees its weights and reuses the address
+ * for others gets them uploaded again instead of the stale copy. Every use compares the first
+ * and the last sampled word and one more in rotation (three loads instead of sixteen, since a
+ * decode step looks up every layer's weights), so all sixteen are compared every 14 uses. */
+#define G53_NSAMP 16
+typedef struct { const void *h; size_t n; void *d; int dt; size_t hn; uint64_t samp[G53_NSAMP]; unsigned use; } G53Res;
 
-static uint64_t res_sig(const void *h, size_t n)
+static uint64_t res_word(const void *h, size_t hn, int k)
 {
-    const unsigned char *b = (const unsigned char *)h;
-    uint64_t v = 0x9e3779b97f4a7c15ull ^ n;
-    for (int k = 0; k < 64 && n >= 8; k++) {
-        uint64_t word;
-        memcpy(&word, b + (size_t)k * ((n - 8) / 63), 8);
-        v = (v ^ word) * 0x100000001b3ull;
-        v ^= v >> 29;
-    }
-    return v;
+    uint64_t w = 0;
+    if (hn >= 8) memcpy(&w, (const unsigned char *)h + (size_t)k * ((hn - 8) / (G53_NSAMP - 1)), 8);
+    return w;
+}
+
+static void res_record(G53Res *r, const void *h, size_t hn)
+{
+    r->hn = hn;
+    r->use = 0;
+    for (int k = 0; k < G53_NSAMP; k++) r->samp[k] = res_word(h, hn, k);
+}
+
+static int res_same(G53Res *r, const void *h, size_t hn)
+{
+    if (r->hn != hn) return 0;
+    const int k = 1 + (int)(r->use++ % (G53_NSAMP - 2));
+    return res_word(h, hn, 0) == r->samp[0] && res_word(h, hn, G53_NSAMP - 1) == r->samp[G53_NSAMP - 1] &&
+           res_word(h, hn, k) == r->samp[k];
 }
 static G53Res *g_res = NULL;
 static size_t g_res_cap = 0, g_res_n = 0;
@@ -98,15 +110,15 @@ static G53Res *res_insert(const void *h)
 static const void *resident(const void *h, size_t n)
 {
     if (!h) return NULL;
+    G53Res *r = res_find(h);                  /* a known host weight: no pointer query */
+    if (r && r->n == n && r->dt < 0 && res_same(r, h, n)) return r->d;
     if (g53h_is_device_ptr(h)) return h;
-    G53Res *r = res_find(h);
-    const uint64_t sig = res_sig(h, n);
-    if (r && r->n == n && r->dt < 0 && r->sig == sig) return r->d;
     void *d = g53h_alloc(n);
     if (!d || g53h_h2d(d, h, n)) g53_die("uploading a weight to HBM");
     if (!r) r = res_insert(h);
     else if (g53h_sync() || g53h_free(r->d)) g53_die("replacing a resident weight");
-    r->n = n; r->d = d; r->dt = -1; r->sig = sig;
+    r->n = n; r->d = d; r->dt = -1;
+    res_record(r, h, n);
     return d;
 }
 
@@ -115,10 +127,12 @@ static const void *resident(const void *h, size_t n)
  * bytes for the same exact values. *dt receives 0 (fp32) or 1 (bf16). */
 static const void *resident_router(const float *h, size_t n, int *dt)
 {
-    if (g53h_is_device_ptr(h)) { *dt = 0; return h; }
     G53Res *r = res_find(h);
-    const uint64_t sig = res_sig(h, n * sizeof(float));
-    if (r && r->dt >= 0 && r->n == n * (r->dt ? 2 : 4) && r->sig == sig) { *dt = r->dt; return r->d; }
+    if (r && r->dt >= 0 && r->n == n * (r->dt ? 2 : 4) && res_same(r, h, n * sizeof(float))) {
+        *dt = r->dt;
+        return r->d;
+    }
+    if (g53h_is_device_ptr(h)) { *dt = 0; return h; }
     int bf = 1;
     for (size_t i = 0; i < n && bf; i++) if (g53_fbits(h[i]) & 0xffffu) bf = 0;
     void *d;
@@ -138,7 +152,8 @@ static const void *resident_router(const float *h, size_t n, int *dt)
     }
     if (!r) r = res_insert(h);
     else if (g53h_sync() || g53h_free(r->d)) g53_die("replacing a resident router");
-    r->n = bytes; r->d = d; r->dt = bf; r->sig = sig;
+    r->n = bytes; r->d = d; r->dt = bf;
+    res_record(r, h, n * sizeof(float));
     *dt = bf;
     return d;
 }
@@ -239,15 +254,15 @@ static G53hMat dev_mat_resident_tiled(const Glm53fMat *m, const char *what)
     }
     const size_t n = mat_code_bytes(m);
     G53Res *r = res_find((const char *)m->w + 1);        /* the tiled copy's own key */
-    const uint64_t sig = res_sig(m->w, n);
-    if (r && r->n == n && r->dt == -2 && r->sig == sig) { d.w = (const uint8_t *)r->d; return d; }
+    if (r && r->n == n && r->dt == -2 && res_same(r, m->w, n)) { d.w = (const uint8_t *)r->d; return d; }
     uint8_t *stage = (uint8_t *)buf_get(&g_tile_stage, n);
     uint8_t *t = (uint8_t *)g53h_alloc(n);
     if (!t || g53h_h2d(stage, m->w, n) || g53h_tile_f8(t, stage, m->rows, m->cols) || g53h_sync())
         g53_die("tiling a resident weight");
     if (!r) r = res_insert((const char *)m->w + 1);
     else if (g53h_sync() || g53h_free(r->d)) g53_die("replacing a resident weight");
-    r->n = n; r->d = t; r->dt = -2; r->sig = sig;
+    r->n = n; r->d = t; r->dt = -2;
+    res_record(r, m->w, n);
     d.w = t;
     return d;
 }
@@ -516,10 +531,38 @@ static int predict_next(int *pred, const float *xd, const Glm53fMoeW *w, const G
  * routes again with the same bit-exact router, over a table that holds only the chosen ones. */
 static G53Buf g_ident;
 
+/* Mailbox use of the cached decode: slot 0 carries the routing read-back (idx, flag, prediction
+ * at byte 1024), slot 1 the error flags and the output (at byte 4096). */
+#define G53_MB_ROUTE 0
+#define G53_MB_ROUTE_OFF 1024
+#define G53_MB_OUT 1
+#define G53_MB_OUT_OFF 4096
+static unsigned g_seq;
+static unsigned next_seq(void)
+{
+    if (++g_seq == 0) g_seq = 1;                     /* 0 is the mailbox's initial value */
+    return g_seq;
+}
+
+#ifdef G53_HOST_PROF
+#include <time.h>
+static double g_hp[16];
+static long g_hp_n;
+static double hp_now(void) { struct timespec t; clock_gettime(CLOCK_MONOTONIC, &t); return t.tv_sec * 1e6 + t.tv_nsec * 1e-3; }
+#define HP(i) do { const double t_ = hp_now(); g_hp[i] += t_ - hp_t; hp_t = t_; } while (0)
+void g53h_host_prof(double *out) { for (int i = 0; i < 16; i++) out[i] = g_hp_n ? g_hp[i] / g_hp_n : 0; memset(g_hp, 0, sizeof g_hp); g_hp_n = 0; }
+#else
+#define HP(i) do { } while (0)
+#endif
+
 static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int with_shared)
 {
     const int E = c->hidden, K = c->topk, NE = c->n_experts;
     Glm53fExpertSrc *src = w->src;
+#ifdef G53_HOST_PROF
+    double hp_t = hp_now();
+    g_hp_n++;
+#endif
     float *xd = (float *)x;
     if (!g53h_is_device_ptr(x)) {                   /* x up without a wait */
         float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, (size_t)E * sizeof(float));
@@ -527,27 +570,39 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         xd = (float *)buf_get(&g_xin, (size_t)E * sizeof(float));
         if (g53h_h2d_async(xd, xp, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
     }
+    HP(8);
     const int per_max = 2 * GLM53F_MAX_TOPK;
     int *rd = (int *)buf_get(&g_idx, (size_t)(K + 1 + per_max) * sizeof(int));
     int *idx_d = rd, *flag_d = rd + K, *pred_d = rd + K + 1;
     float *w_d = (float *)buf_get(&g_w, (size_t)K * sizeof(float));
-    int dt = 0;
+    int dt = 0, ndt = 0;
+    HP(10);
     const void *gate = resident_router(w->gate, (size_t)NE * E, &dt);
+    HP(11);
     const float *bias = (const float *)resident(w->bias, (size_t)NE * sizeof(float));
-    if (g53h_memset(flag_d, 0, sizeof(int)) ||
-        g53h_router(idx_d, w_d, xd, 1, gate, dt, bias, NE, E, K, c->norm_topk, c->routed_scale, flag_d))
-        g53_die("glm53f_router");
+    HP(12);
     const int prefetch = w->prefetch_n > 0 && src->hint != NULL;
     int per = 0;
+    const void *ngate = NULL;
+    const float *nbias = NULL;
     if (prefetch && w->next_gate) {
         per = w->prefetch_n < per_max ? w->prefetch_n : per_max;
-        int ndt = 0;
-        const void *ngate = resident_router(w->next_gate, (size_t)NE * E, &ndt);
-        const float *nbias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
-        if (g53h_route_topn_batch(pred_d, NULL, per, xd, 1, ngate, ndt, nbias, NE, E)) g53_die("next-layer prediction");
+        if (per > NE) per = NE;
+        ngate = resident_router(w->next_gate, (size_t)NE * E, &ndt);
+        HP(13);
+        nbias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
     }
-    int *back = (int *)pinned(&g_pin_back, &g_pin_back_n, (size_t)(K + 1 + per_max) * sizeof(int));
-    if (g53h_d2h(back, rd, (size_t)(K + 1 + per) * sizeof(int))) g53_die("glm53f_moe routing");
+    HP(9);
+    /* routing, NaN flag and the next layer's prediction: two launches, and the kernel writes the
+     * host's copy into the mailbox, which the host polls */
+    const unsigned seq_r = next_seq();
+    if (g53h_route_decode(idx_d, w_d, flag_d, pred_d, per, xd, gate, dt, bias, ngate, ndt, nbias, NE, E, K,
+                          c->norm_topk, c->routed_scale, G53_MB_ROUTE, seq_r, G53_MB_ROUTE_OFF))
+        g53_die("glm53f_router");
+    HP(0);
+    if (g53h_mailbox_wait(G53_MB_ROUTE, seq_r)) g53_die("glm53f_moe routing");
+    const int *back = (const int *)((const char *)g53h_mailbox() + G53_MB_ROUTE_OFF);
+    HP(1);
     if (back[K]) {
         fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) is below %d, above the limit of %d.\n", K, K);
         abort();
@@ -559,6 +614,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         src->hint(src, w->layer, ids, K);
         if (per > 0) src->hint(src, w->layer + 1, back + K + 1, per);
     }
+    HP(2);
     /* the chosen experts' views (slot order), the shared expert after them */
     G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
     int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1;
@@ -579,6 +635,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         tab[j].down = view_mat_f8(&q.down);
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_TILED)) tiled = 0;
     }
+    HP(3);
     if (with_shared) {
         /* the shared expert resident in the layout of the routed slots */
         const int tile_ok = tiled && w->sh_gate.rows % 8 == 0 && w->sh_gate.cols % 128 == 0 &&
@@ -632,15 +689,25 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         L.n_experts = NE; L.experts = tab_d; L.shared = with_shared ? tab_d + NE : NULL;
         if (g53h_moe(od, xd, 1, &L, NULL, NULL)) g53_die("glm53f_moe");
     }
+    HP(4);
     /* the HBM cache orders each slot's reuse after the kernels launched so far */
     for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
-    int *errs = errors_enqueue();
-    if (!odev) {
-        if (g53h_d2h(out, od, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
-    } else if (g53h_sync()) {
-        g53_die("glm53f_moe");
+    /* the error flags and the output come back together through the mailbox, one wait */
+    const size_t ob = odev ? 0 : (size_t)E * sizeof(float);
+    const unsigned seq_o = next_seq();
+    if (G53_MB_OUT_OFF + 4 * G53H_NERR + ob <= G53H_MBOX_BYTES) {
+        if (g53h_publish(G53_MB_OUT, seq_o, G53_MB_OUT_OFF, od, ob)) g53_die("glm53f_moe");
+        HP(5);
+        if (g53h_mailbox_wait(G53_MB_OUT, seq_o)) g53_die("glm53f_moe");
+        HP(6);
+        const int *mo = (const int *)((const char *)g53h_mailbox() + G53_MB_OUT_OFF);
+        errors_check(mo, w->layer, K);
+        if (ob) memcpy(out, mo + G53H_NERR, ob);
+    } else {                                         /* a hidden size beyond the mailbox */
+        int *errs = (int *)pinned(&g_pin_err, &g_pin_err_n, G53H_NERR * sizeof(int));
+        if (g53h_errors_peek_async(errs) || (ob && g53h_d2h_async(out, od, ob)) || g53h_sync()) g53_die("glm53f_moe");
+        errors_check(errs, w->layer, K);
     }
-    errors_check(errs, w->layer, K);
 }
 
 /* ------------------------------------------------------------- MoE chunk ---- */

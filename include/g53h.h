@@ -33,6 +33,9 @@ int         g53h_d2d(void *dst_d, const void *src_d, size_t bytes);   /* stream-
 /* Stream-ordered copy to HBM; src must stay unchanged until the stream has passed the copy
  * (pinned host memory makes it asynchronous). */
 int         g53h_h2d_async(void *dst_d, const void *src_h, size_t bytes);
+/* Stream-ordered copy to the host (asynchronous into pinned memory); dst holds the bytes once
+ * the stream has passed the copy (g53h_sync). */
+int         g53h_d2h_async(void *dst_h, const void *src_d, size_t bytes);
 int         g53h_memset(void *dst_d, int value, size_t bytes);        /* stream-ordered */
 int         g53h_is_device_ptr(const void *p);   /* 1 = HBM of a device, 0 = host      */
 /* Timing on the compute stream: the elapsed time between the two most recent marks. */
@@ -102,6 +105,17 @@ int g53h_router(int *idx_d, float *w_d, const float *x_d, int T, const void *gat
  * experts of sigmoid(W x) + bias for one token, strict order, lowest index on ties. */
 int g53h_route_topn(int *idx_d, int n, const float *x_d, const void *gate_d, int gate_dt,
                     const float *bias_d, int n_experts, int hidden);
+
+/* One decode token (T = 1): g53h_router (with *nan_flag_d written 0 or 1, no clearing needed)
+ * and, when next_gate != NULL and n > 0, g53h_route_topn of the next layer's router into pred
+ * [n], in two launches. Replaces src/core/glm53f_ops.c:1169-1203 (route, then route_topn for the
+ * hint) for the drop-in's cached decode. With mb_slot >= 0 the kernel also writes idx [topk],
+ * the flag and pred [n] as 32-bit words into the host mailbox at byte offset mb_off, then seq
+ * into sequence word mb_slot (see g53h_mailbox below). */
+int g53h_route_decode(int *idx_d, float *w_d, int *nan_flag_d, int *pred_d, int n, const float *x_d,
+                      const void *gate_d, int gate_dt, const float *bias_d, const void *next_gate_d, int next_dt,
+                      const float *next_bias_d, int n_experts, int hidden, int topk, int norm_topk,
+                      float routed_scale, int mb_slot, unsigned seq, size_t mb_off);
 
 /* route_topn for T tokens at once: idx [T][n]; score_out [T][n] (optional) receives the chosen
  * experts' sigmoid scores (for the GLM53F_ROUTE_TOP16 trace, src/core/glm53f_ops.c:1044-1080). */
@@ -211,6 +225,22 @@ int g53h_decode_grid(void);
  * g53h_decode_errors), [2] the grouped path (the bits of g53h_grouped_errors). */
 #define G53H_NERR 3
 int g53h_errors_async(int *host);
+/* The same copy without clearing the flags: for a caller that aborts on any flag (the C drop-in),
+ * so that nothing needs clearing while no flag is set. */
+int g53h_errors_peek_async(int *host);
+/* Host mailbox: G53H_MBOX_BYTES of pinned host memory that kernels write into directly, so a
+ * host waits for a result by polling a word instead of a device-to-host copy and a stream
+ * synchronisation. Words [0, G53H_MBOX_SLOTS) are sequence words; data lives above them.
+ * g53h_mailbox_wait spins until sequence word `slot` equals seq (then the data written before
+ * it is visible), falling back to a blocking stream wait. g53h_publish enqueues on the compute
+ * stream a copy of the G53H_NERR error words and then `bytes` of device memory into the mailbox
+ * at byte offset off, followed by seq in word `slot`. */
+#define G53H_MBOX_BYTES (1 << 16)
+#define G53H_MBOX_SLOTS 16
+void *g53h_mailbox(void);
+int   g53h_mailbox_wait(int slot, unsigned seq);
+int   g53h_publish(int slot, unsigned seq, size_t off, const void *src_d, size_t bytes);
+
 /* Test hook: the number of polls after which a wait on another workgroup of the one-launch
  * decode kernels gives up (and sets bit 1 of their error flags); 0 restores the default.
  * Returns the previous setting. Waits between the waves of one workgroup are not affected. */

@@ -245,7 +245,7 @@ class HostSrc:
         self.pinned -= 1
 
 
-def dropin_moe(cf, W, b, ex, sh, x, drop=(), shared=True, src=None):
+def dropin_moe(cf, W, b, ex, sh, x, drop=(), shared=True, src=None, forget=True):
     L = glm53h.lib()
     src = src or HostSrc(cf, ex, drop)
     w = glm53h.Glm53fMoeW()
@@ -260,7 +260,8 @@ def dropin_moe(cf, W, b, ex, sh, x, drop=(), shared=True, src=None):
     out = np.zeros((T, E), np.float32)
     fn = L.glm53f_moe if shared else L.glm53f_moe_routed
     fn(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cf), T, None)
-    L.glm53f_forget_host_weights()            # the arrays above are freed after this call
+    if forget:
+        L.glm53f_forget_host_weights()        # the arrays above are freed after this call
     assert src.pinned == 0
     return out
 
