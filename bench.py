@@ -353,7 +353,7 @@ def bench_stack(a):
     are measured back on the device router and reported. The cache starts holding the most
     popular experts of every layer (what 200 GB holds), then warms up under the workload."""
     L = glm53h.init(0)
-    NL, steps, warm = 42, (a.steps if a.steps != 400 else 32), (a.warmup if a.warmup != 50 else 8)
+    NL, steps, warm = a.stack_layers, (a.steps if a.steps != 400 else 32), (a.warmup if a.warmup != 50 else 8)
     base = S.spec(3)
     E, I, NE, K = base.E, base.I, base.NE, base.K
     from glm53h import zipf
@@ -455,8 +455,10 @@ def bench_stack(a):
         "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(dt * 1e3 / steps, 3),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded FP8 experts; per-layer bf16 routers with Zipf(1.1) bias; correlated bf16 inputs)",
-        "config": {"workload": "BASELINE config 5: 42-layer decode stack, 32 steps, HBM expert cache of 200 GB, "
-                               "the rest in pinned host memory, next-layer prefetch",
+        "config": {"workload": (f"BASELINE config 5: {NL}-layer decode stack" if NL == 42 else
+                                f"config 5 diagnostic: {NL}-layer decode stack (BASELINE's is 42)") +
+                               f", {steps} steps, HBM expert cache of 200 GB, the rest in pinned host memory, "
+                               "next-layer prefetch",
                    "layers": NL, "slots": nslot,
                    "prefetch_n": pf, "prefetch_reads_in_flight": n_io, "input_correlation": rho,
                    "parallelism": "single GPU"},
@@ -482,6 +484,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--stack-layers", type=int, default=42,
+                    help="config 5: layers in the stack (42 is BASELINE's; fewer, e.g. 24, fit every expert in the "
+                         "200 GB cache, which isolates the per-layer cost from host reads)")
     ap.add_argument("--layout", default="tiled", choices=["tiled", "rowmajor"],
                     help="expert code layout in HBM (config 2): octet-tiled (k_dec_tiled) or row-major (k_dec_layer)")
     a = ap.parse_args()
