@@ -342,6 +342,17 @@ def stack_routing(L, W, B, X, specs, rho):
             "layer0_2048_tokens": {"zipf_slope": round(-s_long, 3), "reuse": round(r_long, 3)}}
 
 
+def policy_eval(path, NE, K):
+    """LRU (this library's cache policy) against the Belady bound on the run's own routing
+    trace, at the reference's two cache sizes (docs/PERFORMANCE.md:301-306), when traced."""
+    if not path:
+        return None
+    from glm53h import route_trace
+    r = route_trace.evaluate(path, slots=(952, 1508), warm=20, topk=K, n_experts=NE)
+    r["trace"] = os.path.basename(path)
+    return r
+
+
 def bench_stack(a):
     """a 42-layer stack of routed-expert layers (config-2 shapes) in single-
     token decode, 32 steps, each layer one glm53f_moe call (the drop-in, with the reference's
@@ -352,6 +363,10 @@ def bench_stack(a):
     x <- rho x + sqrt(1 - rho^2) z (bf16) with rho calibrated for 70% token-to-token reuse. Both
     are measured back on the device router and reported. The cache starts holding the most
     popular experts of every layer (what 200 GB holds), then warms up under the workload."""
+    if a.route_trace:                                   # read by the drop-in at its first call
+        if os.path.exists(a.route_trace):
+            os.remove(a.route_trace)
+        os.environ["GLM53F_ROUTE_TOP16"] = a.route_trace
     L = glm53h.init(0)
     NL, steps, warm = a.stack_layers, (a.steps if a.steps != 400 else 32), (a.warmup if a.warmup != 50 else 8)
     base = S.spec(3)
@@ -463,6 +478,7 @@ def bench_stack(a):
                    "prefetch_n": pf, "prefetch_reads_in_flight": n_io, "input_correlation": rho,
                    "parallelism": "single GPU"},
         "routing": routing,
+        "policy_eval": policy_eval(a.route_trace, NE, K),
         "hit_rate": round(hits / max(hits + misses, 1), 4),
         "miss_rate": round(misses / max(hits + misses, 1), 4),
         "misses_per_token": round(misses / steps, 2),
@@ -484,6 +500,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--route-trace", default=None,
+                    help="config 5: write the decode routing trace (GLM53F_ROUTE_TOP16 format) to this file and "
+                         "report LRU vs Belady misses per token on it (the trace costs time: not for timing)")
     ap.add_argument("--stack-layers", type=int, default=42,
                     help="config 5: layers in the stack (42 is BASELINE's; fewer, e.g. 24, fit every expert in the "
                          "200 GB cache, which isolates the per-layer cost from host reads)")
