@@ -33,6 +33,7 @@ import ctypes as C
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -94,6 +95,25 @@ def run_steps(L, cp, xs, outs, E, n, start=0):
               "g53h_moe")
 
 
+def host_cpu():
+    """The host the CPU baseline ran on: lscpu's model name, nproc (the CPUs this process may
+    use) and the OpenMP threads the reference ran with."""
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.lower().startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        nproc = int(subprocess.run(["nproc"], capture_output=True, text=True, timeout=10).stdout.strip())
+    except (OSError, ValueError, subprocess.SubprocessError):
+        nproc = len(os.sched_getaffinity(0))
+    return {"lscpu_model": model, "nproc": nproc, "omp_threads": int(os.environ.get("OMP_NUM_THREADS", nproc))}
+
+
 def cpu_baseline(layer, x, idx_all, seconds):
     """The reference's glm53f_moe (oracle/_ref, built from the reference's own sources with its
     flags) on this host: config-2 decode of one token per call, experts in host RAM, for about
@@ -116,8 +136,8 @@ def cpu_baseline(layer, x, idx_all, seconds):
         O.moe(R, x[t:t + 1], sp, layer.router_f32, layer.bias_f32, mats, sh)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
-    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "reference",
+    threads = host_cpu()["omp_threads"]
+    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "host": host_cpu(), "kind": "reference",
             "sample": f"reference glm53f_moe (src/core/glm53f_ops.c) compiled -O3 -mavx2 -mfma -fopenmp "
                       f"-ffp-contract=off, OpenMP threads {threads}; config-2 decode of 4 seeded tokens cycled, "
                       f"3 warm-up + median of {len(times)} calls ({sum(times):.1f} s), experts in host RAM",
@@ -163,7 +183,7 @@ def cpu_grouped(layer, x, idx, seconds):
         t0 = time.perf_counter()
         O.moe(R, x, sp, layer.router_f32, layer.bias_f32, mats, sh)
         times.append(time.perf_counter() - t0)
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    threads = host_cpu()["omp_threads"]
     return statistics.median(times), len(times), threads
 
 
@@ -215,7 +235,7 @@ def bench_grouped(a):
         if r:
             med, n, threads = r
             cpu = {"value": round(med * (1e6 if cfg == 3 else 1e3), 1), "unit": "us/layer" if cfg == 3 else "ms/layer",
-                   "cores": threads, "kind": "reference",
+                   "cores": threads, "host": host_cpu(), "kind": "reference",
                    "sample": f"reference glm53f_moe (src/core/glm53f_ops.c, 64-token chunks) compiled -O3 -mavx2 "
                              f"-mfma -fopenmp -ffp-contract=off, OpenMP threads {threads}; the same {T}-token batch "
                              f"(batch 0), median of {n} call(s), experts in host RAM",
@@ -280,9 +300,9 @@ def cpu_stack_layer(sp, W, b, x, sh, seconds):
         t0 = time.perf_counter()
         O.moe(R, xt, sp, W, b, mats, sh)
         times.append(time.perf_counter() - t0)
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    threads = host_cpu()["omp_threads"]
     return {"value": round(statistics.median(times) * 1e6, 1), "unit": "us/layer", "cores": threads,
-            "kind": "reference",
+            "host": host_cpu(), "kind": "reference",
             "sample": f"reference glm53f_moe, one stack layer (layer 0, one token), experts in host RAM (no storage "
                       f"reads), OpenMP threads {threads}, median of {len(times)} calls"}
 
