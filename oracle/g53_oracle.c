@@ -17,6 +17,13 @@
  *   or_route_topn   brute force on small inputs, NaN rules by hand-made cases
  *   or_moe          golden vectors of the compiled reference (configs 1-2 shapes and the
  *                   reference's glm_tiny fixture weights), bit for bit
+ *   or_i4_from_f8   (tests/test_oracle_i4.py) the reference's quantiser known-answer case
+ *                   (tests/unit/test_fp8.c:161) by digest of the compiled reference's output,
+ *                   its half-a-step property, hand-made groups, unaligned scale blocks (golden)
+ *   or_mm_i4        the reference's int4 known-answer cases (tests/unit/test_fp8.c:158-160),
+ *                   golden, bit for bit; a dequantise-then-fp64 bound; a ragged group by hand
+ *   or_moe_i4       golden outputs of the compiled reference with int4 routed experts
+ *                   (configs 1-2), and the weighted sum of separately run int4 experts
  */
 #include <math.h>
 #include <stdint.h>
@@ -169,6 +176,131 @@ int or_moe(float *out, const float *x, int T, int E, int I, int NE, int K, int b
             or_mm_f8(gu + I, xt, 1, ex->uw, ex->us, I, E, br, bc);
             or_swiglu(act, gu, I, limit);
             or_mm_f8(dst, act, 1, ex->dw, ex->ds, E, I, br, bc);
+        }
+        float *ot = out + (size_t)t * E;
+        for (int d = 0; d < E; d++) {
+            double s = 0.0;
+            for (int j = 0; j < K; j++) s += (double)wts[j] * (double)contrib[(size_t)j * E + d];
+            ot[d] = (float)s;
+        }
+        if (shared) {
+            or_mm_f8(gu, xt, 1, shared->gw, shared->gs, I, E, br, bc);
+            or_mm_f8(gu + I, xt, 1, shared->uw, shared->us, I, E, br, bc);
+            or_swiglu(act, gu, I, limit);
+            or_mm_f8(sho, act, 1, shared->dw, shared->ds, E, I, br, bc);
+            for (int d = 0; d < E; d++) ot[d] += sho[d];
+        }
+    }
+    free(ids); free(wts); free(contrib); free(gu); free(act); free(sho);
+    return ret;
+}
+
+/* ------------------------------------------------------------------ int4 ---- */
+/* FP8 -> int4 re-quantisation (reference src/core/glm53f_ops.c:303-371, glm53f_i4_from_f8):
+ * per row and group of 64 columns, vals = the decoded codes (times the block scale when the
+ * group straddles scale blocks), amax = max |vals|, step = (aligned ? amax * blockscale : amax)
+ * / 7 (floored at 1e-30), level = clamp(rint(val * (aligned ? 7 / amax : 1 / step)), -8, 7),
+ * stored as level + 8, two per byte, the even column in the low nibble. q [rows][cols/2],
+ * steps [rows][cols/64]. */
+#define OR_I4_GROUP 64
+void or_i4_from_f8(uint8_t *q, float *steps, const uint8_t *W, const float *S, int rows, int cols, int br,
+                   int bc)
+{
+    const int gs = OR_I4_GROUP, groups = cols / gs, scols = (cols + bc - 1) / bc;
+    for (int o = 0; o < rows; o++) {
+        const uint8_t *row = W + (size_t)o * cols;
+        const float *srow = S + (size_t)(o / br) * scols;
+        for (int g = 0; g < groups; g++) {
+            const int j0 = g * gs, aligned = bc % gs == 0;
+            const float bs = srow[j0 / bc];
+            float vals[OR_I4_GROUP], amax = 0.0f;
+            for (int j = 0; j < gs; j++) {
+                const float w = or_e4m3f(row[j0 + j]) * (aligned ? 1.0f : srow[(j0 + j) / bc]);
+                vals[j] = w;
+                const float a = w < 0.0f ? -w : w;
+                if (a > amax) amax = a;
+            }
+            float step = (aligned ? amax * bs : amax) / 7.0f;
+            if (!(step > 1e-30f)) step = 1e-30f;
+            steps[(size_t)o * groups + g] = step;
+            const float inv = amax > 0.0f ? 7.0f / amax : 0.0f;
+            const float mul = aligned ? inv : (1.0f / step);
+            for (int j = 0; j < gs; j += 2) {
+                int l0 = (int)lrintf(vals[j] * mul), l1 = (int)lrintf(vals[j + 1] * mul);
+                l0 = l0 < -8 ? -8 : (l0 > 7 ? 7 : l0);
+                l1 = l1 < -8 ? -8 : (l1 > 7 ? 7 : l1);
+                q[(size_t)o * (cols / 2) + ((j0 + j) >> 1)] = (uint8_t)((l0 + 8) | ((l1 + 8) << 4));
+            }
+        }
+    }
+}
+
+/* The int4 matrix-vector product (reference src/core/glm53f_ops.c:236-296, matmul_i4): per row
+ * and group of gs columns eight fp32 lanes a[l] = fmaf(level, x, a[l]) stepping by 8, the double
+ * tree, the tail in double, times the group's step in double, added over the row's groups in
+ * order. */
+void or_mm_i4(float *y, const float *x, int T, const uint8_t *Q, const float *steps, int rows, int cols, int gs)
+{
+    const int groups = (cols + gs - 1) / gs;
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * cols;
+        for (int o = 0; o < rows; o++) {
+            const uint8_t *row = Q + (size_t)o * (cols / 2);
+            double acc = 0.0;
+            for (int g = 0; g < groups; g++) {
+                const int j0 = g * gs, j1 = j0 + gs < cols ? j0 + gs : cols;
+                float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                int j = j0;
+                for (; j + 8 <= j1; j += 8)
+                    for (int l = 0; l < 8; l++) {
+                        const uint8_t b = row[(j + l) >> 1];
+                        const int lv = (int)(((j + l) & 1) ? (b >> 4) : (b & 0x0f)) - 8;
+                        a[l] = fmaf((float)lv, xt[j + l], a[l]);
+                    }
+                double bsum = (((double)a[0] + a[4]) + ((double)a[2] + a[6])) + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
+                for (; j < j1; j++) {
+                    const uint8_t b = row[j >> 1];
+                    const int lv = (int)((j & 1) ? (b >> 4) : (b & 0x0f)) - 8;
+                    bsum += (double)lv * (double)xt[j];
+                }
+                acc += bsum * (double)steps[(size_t)o * groups + g];
+            }
+            y[(size_t)t * rows + o] = (float)acc;
+        }
+    }
+}
+
+/* or_moe with int4 routed experts (q, steps per matrix; the shared expert stays FP8, as the
+ * reference's int4 cache holds only routed experts). */
+typedef struct {
+    const uint8_t *gq, *uq, *dq;      /* gq NULL = dropped */
+    const float   *gs, *us, *ds;      /* steps */
+} OrExpertI4;
+
+int or_moe_i4(float *out, const float *x, int T, int E, int I, int NE, int K, int br, int bc, int norm_topk,
+              float routed_scale, float limit, const float *gate, const float *bias, const OrExpertI4 *experts,
+              const OrExpert *shared, int *idx_out, float *w_out)
+{
+    int *ids = (int *)malloc((size_t)K * sizeof(int));
+    float *wts = (float *)malloc((size_t)K * sizeof(float));
+    float *contrib = (float *)malloc((size_t)K * E * sizeof(float));
+    float *gu = (float *)malloc((size_t)2 * I * sizeof(float));
+    float *act = (float *)malloc((size_t)I * sizeof(float));
+    float *sho = (float *)malloc((size_t)E * sizeof(float));
+    int ret = 0;
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * E;
+        if (or_router(ids, wts, xt, gate, bias, NE, E, K, norm_topk, routed_scale)) ret = -1;
+        if (idx_out) memcpy(idx_out + (size_t)t * K, ids, (size_t)K * sizeof(int));
+        if (w_out) memcpy(w_out + (size_t)t * K, wts, (size_t)K * sizeof(float));
+        for (int j = 0; j < K; j++) {
+            const OrExpertI4 *ex = &experts[ids[j]];
+            float *dst = contrib + (size_t)j * E;
+            if (!ex->gq) { memset(dst, 0, (size_t)E * sizeof(float)); continue; }
+            or_mm_i4(gu, xt, 1, ex->gq, ex->gs, I, E, OR_I4_GROUP);
+            or_mm_i4(gu + I, xt, 1, ex->uq, ex->us, I, E, OR_I4_GROUP);
+            or_swiglu(act, gu, I, limit);
+            or_mm_i4(dst, act, 1, ex->dq, ex->ds, E, I, OR_I4_GROUP);
         }
         float *ot = out + (size_t)t * E;
         for (int d = 0; d < E; d++) {

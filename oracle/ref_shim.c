@@ -22,6 +22,7 @@ typedef struct {
     Glm53fExpertSrc src;              /* first member: the MoE passes &src back */
     const RefExpert *ex;
     int E, I, br, bc;
+    int i4;                           /* routed experts are GLM53F_WI4 (q, steps) */
 } MemSrc;
 
 static void fill(Glm53fMat *m, const uint8_t *w, const float *s, int rows, int cols, int br, int bc)
@@ -31,12 +32,25 @@ static void fill(Glm53fMat *m, const uint8_t *w, const float *s, int rows, int c
     m->rows = rows; m->cols = cols; m->br = br; m->bc = bc; m->scols = (cols + bc - 1) / bc;
 }
 
+static void fill_i4(Glm53fMat *m, const uint8_t *q, const float *steps, int rows, int cols)
+{
+    memset(m, 0, sizeof *m);
+    m->w = q; m->s = steps; m->dt = GLM53F_WI4;
+    m->rows = rows; m->cols = cols; m->br = 1; m->bc = GLM53F_I4_GROUP; m->scols = cols / GLM53F_I4_GROUP;
+}
+
 static int mem_get(Glm53fExpertSrc *self, int layer, int e, Glm53fExpertQ *q)
 {
     (void)layer;
     MemSrc *m = (MemSrc *)self;
     const RefExpert *x = &m->ex[e];
     if (!x->gw) return -1;
+    if (m->i4) {
+        fill_i4(&q->gate, x->gw, x->gs, m->I, m->E);
+        fill_i4(&q->up, x->uw, x->us, m->I, m->E);
+        fill_i4(&q->down, x->dw, x->ds, m->E, m->I);
+        return 0;
+    }
     fill(&q->gate, x->gw, x->gs, m->I, m->E, m->br, m->bc);
     fill(&q->up, x->uw, x->us, m->I, m->E, m->br, m->bc);
     fill(&q->down, x->dw, x->ds, m->E, m->I, m->br, m->bc);
@@ -52,9 +66,45 @@ static void cfg_of(Glm53fCfg *c, int E, int I, int NE, int K, int br, int bc, in
     c->fp8_block_r = br; c->fp8_block_c = bc; c->n_layers = 1;
 }
 
+static long moe_any(float *out, const float *x, int T, int E, int I, int NE, int K, int br, int bc,
+                    int norm_topk, float routed_scale, float limit, const float *gate, const float *bias,
+                    const RefExpert *experts, const RefExpert *shared, int i4);
+
 long ref_moe(float *out, const float *x, int T, int E, int I, int NE, int K, int br, int bc,
              int norm_topk, float routed_scale, float limit, const float *gate, const float *bias,
              const RefExpert *experts, const RefExpert *shared)
+{
+    return moe_any(out, x, T, E, I, NE, K, br, bc, norm_topk, routed_scale, limit, gate, bias, experts, shared, 0);
+}
+
+/* The same with GLM53F_WI4 routed experts ({q, steps} per matrix, as glm53f_i4_from_f8 writes
+ * them) and the FP8 shared expert: the reference's --experts int4 mode. */
+long ref_moe_i4(float *out, const float *x, int T, int E, int I, int NE, int K, int br, int bc,
+                int norm_topk, float routed_scale, float limit, const float *gate, const float *bias,
+                const RefExpert *experts, const RefExpert *shared)
+{
+    return moe_any(out, x, T, E, I, NE, K, br, bc, norm_topk, routed_scale, limit, gate, bias, experts, shared, 1);
+}
+
+/* glm53f_i4_from_f8 on an FP8 matrix; glm53f_mm_batch on a GLM53F_WI4 one. */
+void ref_i4_from_f8(uint8_t *q, float *steps, const uint8_t *W, const float *S, int rows, int cols, int br, int bc)
+{
+    Glm53fMat m;
+    fill(&m, W, S, rows, cols, br, bc);
+    glm53f_i4_from_f8(q, steps, &m);
+}
+
+void ref_mm_i4(float *y, const float *x, int T, const uint8_t *q, const float *steps, int rows, int cols)
+{
+    Glm53fMat m;
+    fill_i4(&m, q, steps, rows, cols);
+    if (T == 1) glm53f_mm(y, x, &m);
+    else glm53f_mm_batch(y, x, T, &m);
+}
+
+static long moe_any(float *out, const float *x, int T, int E, int I, int NE, int K, int br, int bc,
+                    int norm_topk, float routed_scale, float limit, const float *gate, const float *bias,
+                    const RefExpert *experts, const RefExpert *shared, int i4)
 {
     Glm53fCfg c;
     cfg_of(&c, E, I, NE, K, br, bc, norm_topk, routed_scale, limit);
@@ -62,7 +112,7 @@ long ref_moe(float *out, const float *x, int T, int E, int I, int NE, int K, int
     memset(&src, 0, sizeof src);
     src.src.get = mem_get;
     src.src.ctx = &src;
-    src.ex = experts; src.E = E; src.I = I; src.br = br; src.bc = bc;
+    src.ex = experts; src.E = E; src.I = I; src.br = br; src.bc = bc; src.i4 = i4;
     Glm53fMoeW w;
     memset(&w, 0, sizeof w);
     w.gate = gate; w.bias = bias; w.src = &src.src; w.layer = 0;
