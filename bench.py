@@ -402,7 +402,7 @@ def bench_stack(a):
     check(L.g53h_store_synth_init(C.byref(st), E, I, NL + 1, NE, NE, base.seed, C.c_float(base.expert_sigma)), "store")
     cache = glm53h.Glm53fCache()
     budget = 200 * 10 ** 9
-    if L.g53h_cache_init_store(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io) != 0:
+    if L.g53h_cache_init_store(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io, 0) != 0:
         sys.exit("glm53f_cache_init failed")
     specs = [S.spec(3, layer=l) for l in range(NL)]
     W = [S.router_host(s_) for s_ in specs]

@@ -16,6 +16,11 @@
  *   - prefetch keeps at most n_io expert reads in flight on the prefetch stream; the queue
  *     (ordered by layer, stale entries cancelled by later hints) feeds it whenever the cache is
  *     called and earlier reads have landed.
+ *   - int4 slots (i4 != 0, the reference's --experts int4): a read copies each FP8 matrix and
+ *     its scales into the stream's staging buffer in HBM, and the quantiser kernel writes the
+ *     slot's GLM53F_WI4 levels and steps from there on the same stream (the reference
+ *     quantises on its I/O threads, src/cache/glm53f_cache.c:114-127); the slot layout is the
+ *     reference's (src/io/glm53f_load.c:141-163), so a budget holds the same number of slots.
  * Every entry point takes one mutex, as the reference's. */
 #include <hip/hip_runtime.h>
 
@@ -38,7 +43,8 @@ extern "C" {
 namespace {
 
 struct Geom {                       /* slot layout, from the probe expert */
-    size_t off[6], bytes[6];        /* gate/up/down codes, then gate/up/down scales */
+    size_t off[6], bytes[6];        /* gate/up/down codes, then gate/up/down scales (in the slot) */
+    size_t fbytes[6];               /* the same parts as read (FP8), for int4 slots            */
     int rows[3], cols[3], br[3], bc[3], scols[3];
 };
 
@@ -66,6 +72,7 @@ struct Impl {
     /* octet-tiled slots (G53H_MAT_TILED): a matrix's codes land in the stream's staging buffer and
      * are tiled into the slot by a kernel on the same stream, so one buffer per stream suffices */
     bool tiled = false;
+    bool i4 = false;                /* int4 slots: FP8 staged, quantised into the slot      */
     uint8_t *stage_demand = nullptr, *stage_prefetch = nullptr;
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
@@ -173,7 +180,22 @@ int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t 
     }
     if (m->landed_ok[slot] && hipStreamWaitEvent(s, m->landed[slot], 0) != hipSuccess) return 0;
     uint8_t *stage = s == m->prefetch ? m->stage_prefetch : m->stage_demand;
-    for (int i = 0; i < 3; i++) {
+    for (int i = 0; m->i4 && i < 3; i++) {
+        /* FP8 codes and scales into staging, then the quantiser into the slot */
+        const size_t sc_off = al(m->geo.fbytes[i], 256);
+        G53hMat f;
+        memset(&f, 0, sizeof f);
+        f.w = stage; f.s = (const float *)(stage + sc_off);
+        f.rows = m->geo.rows[i]; f.cols = m->geo.cols[i]; f.br = m->geo.br[i]; f.bc = m->geo.bc[i];
+        f.scols = m->geo.scols[i];
+        if (hipMemcpyAsync(stage, mats[i]->w, m->geo.fbytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(stage + sc_off, mats[i]->s, m->geo.fbytes[3 + i], hipMemcpyHostToDevice, s) !=
+                hipSuccess ||
+            g53h_i4_from_f8_on(base + m->geo.off[i], (float *)(base + m->geo.off[3 + i]), &f, s))
+            return 0;
+        *nread += (int64_t)(m->geo.fbytes[i] + m->geo.fbytes[3 + i]);
+    }
+    for (int i = 0; !m->i4 && i < 3; i++) {
         if (m->tiled) {
             if (hipMemcpyAsync(stage, mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
                 g53h_tile_f8_on(base + m->geo.off[i], stage, m->geo.rows[i], m->geo.cols[i], s))
@@ -223,9 +245,13 @@ void view_of(const Glm53fCache *c, const Impl *m, int slot, Glm53fExpertQ *q)
         Glm53fMat &v = *mats[i];
         v.w = base + m->geo.off[i];
         v.s = (const float *)(base + m->geo.off[3 + i]);
-        v.dt = m->tiled ? GLM53F_WF8T : GLM53F_WF8;
+        v.dt = m->i4 ? GLM53F_WI4 : (m->tiled ? GLM53F_WF8T : GLM53F_WF8);
         v.rows = m->geo.rows[i]; v.cols = m->geo.cols[i];
-        v.br = m->geo.br[i]; v.bc = m->geo.bc[i]; v.scols = m->geo.scols[i];
+        if (m->i4) {                                 /* glm53f_expert_i4_view's geometry */
+            v.br = 1; v.bc = GLM53F_I4_GROUP; v.scols = m->geo.cols[i] / GLM53F_I4_GROUP;
+        } else {
+            v.br = m->geo.br[i]; v.bc = m->geo.bc[i]; v.scols = m->geo.scols[i];
+        }
     }
 }
 
@@ -366,7 +392,7 @@ void cache_hint(Glm53fExpertSrc *self, int layer, const int *ids, int n)
 extern "C" int g53h_cache_is(const Glm53fExpertSrc *src) { return src && src->get == cache_get; }
 
 /* Common set-up once the store is known (m->store or m->ckpt). */
-static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t budget_bytes, int n_io)
+static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t budget_bytes, int n_io, int i4)
 {
     c->cfg = cfg;
     c->n_layers = cfg->n_layers + 1;       /* the MTP layer streams experts the same way */
@@ -404,11 +430,38 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
         off = al(off + m->geo.bytes[3 + i], 256);
     }
     c->slot_bytes = (int64_t)al(off, 4096);
+    m->i4 = i4 != 0;
+    c->i4 = m->i4 ? 1 : 0;
+    if (m->i4) {
+        for (int i = 0; i < 3; i++)
+            if (m->geo.cols[i] % GLM53F_I4_GROUP) {
+                fprintf(stderr, "glm53f_cache: int4 slots need columns a multiple of %d\n", GLM53F_I4_GROUP);
+                delete m;
+                return -1;
+            }
+        /* the reference's int4 slot (src/io/glm53f_load.c:141-163): per matrix the levels, then
+         * the steps, each 64-byte aligned; the slot rounded up to 4096 bytes */
+        size_t o = 0;
+        for (int i = 0; i < 3; i++) {
+            m->geo.fbytes[i] = m->geo.bytes[i];
+            m->geo.fbytes[3 + i] = m->geo.bytes[3 + i];
+            o = al(o, 64);
+            m->geo.off[i] = o;
+            m->geo.bytes[i] = (size_t)m->geo.rows[i] * (size_t)(m->geo.cols[i] / 2);
+            o += m->geo.bytes[i];
+            o = al(o, 64);
+            m->geo.off[3 + i] = o;
+            m->geo.bytes[3 + i] = (size_t)m->geo.rows[i] * (size_t)(m->geo.cols[i] / GLM53F_I4_GROUP) * 4;
+            o += m->geo.bytes[3 + i];
+        }
+        c->slot_bytes = (int64_t)al(o, 4096);
+    }
     /* slots octet-tiled at the shapes the one-launch tiled decode reads (hidden 4096, inter
      * 2048, 128 x 128 blocks), row-major otherwise or with GLM53F_CACHE_ROWMAJOR set */
     m->tiled = !getenv("GLM53F_CACHE_ROWMAJOR") && m->geo.rows[0] == 2048 && m->geo.cols[0] == 4096 &&
                m->geo.rows[1] == 2048 && m->geo.cols[1] == 4096 && m->geo.rows[2] == 4096 && m->geo.cols[2] == 2048;
     for (int i = 0; i < 3; i++) m->tiled = m->tiled && m->geo.br[i] == 128 && m->geo.bc[i] == 128;
+    if (m->i4) m->tiled = false;
     c->nslot = (int)(budget_bytes / c->slot_bytes);
     if (c->nslot < cfg->topk + 1) {
         fprintf(stderr, "glm53f_cache: budget %.2f GB gives %d slots of %.2f MB; top-%d needs at least %d\n",
@@ -437,8 +490,12 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
         ok = hipEventCreateWithFlags(&m->landed[i], hipEventDisableTiming) == hipSuccess;
     m->demand = g53h_copy_stream();
     ok = ok && hipStreamCreateWithFlags(&m->prefetch, hipStreamNonBlocking) == hipSuccess;
-    if (ok && m->tiled) {
-        const size_t sb = m->geo.bytes[0] > m->geo.bytes[2] ? m->geo.bytes[0] : m->geo.bytes[2];
+    if (ok && (m->tiled || m->i4)) {
+        size_t sb = 0;                               /* the largest matrix (with its scales) */
+        for (int i = 0; i < 3; i++) {
+            const size_t need = m->i4 ? al(m->geo.fbytes[i], 256) + m->geo.fbytes[3 + i] : m->geo.bytes[i];
+            if (need > sb) sb = need;
+        }
         m->stage_demand = (uint8_t *)g53h_alloc(sb);
         m->stage_prefetch = (uint8_t *)g53h_alloc(sb);
         ok = m->stage_demand && m->stage_prefetch;
@@ -472,10 +529,6 @@ extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53
                                  int n_io, int i4)
 {
     memset(c, 0, sizeof *c);
-    if (i4) {
-        fprintf(stderr, "glm53f_cache: int4 slots are not supported by the MI355X cache\n");
-        return -1;
-    }
     if (!st || !cfg) return -1;
     if (g53h_ready()) {
         fprintf(stderr, "glm53f_cache: %s\n", g53h_error());
@@ -490,12 +543,12 @@ extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53
         return -1;
     }
     c->st = st;
-    const int rc = cache_setup(c, m, cfg, budget_bytes, n_io);
+    const int rc = cache_setup(c, m, cfg, budget_bytes, n_io, i4);
     return rc;
 }
 
 extern "C" int g53h_cache_init_store(Glm53fCache *c, const G53hStore *store, const Glm53fCfg *cfg,
-                                     int64_t budget_bytes, int n_io)
+                                     int64_t budget_bytes, int n_io, int i4)
 {
     memset(c, 0, sizeof *c);
     if (!store || !store->view || !cfg) return -1;
@@ -505,7 +558,7 @@ extern "C" int g53h_cache_init_store(Glm53fCache *c, const G53hStore *store, con
     }
     Impl *m = new Impl();
     m->store = store;
-    return cache_setup(c, m, cfg, budget_bytes, n_io);
+    return cache_setup(c, m, cfg, budget_bytes, n_io, i4);
 }
 
 extern "C" int glm53f_cache_sync(Glm53fCache *c)

@@ -442,7 +442,8 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const
 /* A descriptor with the layout the grouped kernels assume. */
 __device__ __forceinline__ bool g53_grp_desc_ok(const G53hExpert &x, int E, int I)
 {
-    return x.gate.br == 128 && x.gate.bc == 128 && x.gate.rows == I && x.gate.cols == E &&
+    return !((x.gate.flags | x.up.flags | x.down.flags) & G53H_MAT_I4) &&
+           x.gate.br == 128 && x.gate.bc == 128 && x.gate.rows == I && x.gate.cols == E &&
            x.up.br == 128 && x.up.bc == 128 && x.up.rows == I && x.up.cols == E &&
            x.down.br == 128 && x.down.bc == 128 && x.down.rows == E && x.down.cols == I &&
            x.gate.scols >= E / 128 && x.up.scols >= E / 128 && x.down.scols >= I / 128;

@@ -274,13 +274,13 @@ static int g53_layer_body(float *out, const float *x, int T, const G53hMoeLayer 
         g53h_prof_mark(G53_PROF_COMBINE);
         return 0;
     }
-    /* any other shape: one thread per (token, slot, row), same arithmetic */
+    /* int4 experts and any other shape: the row-wave kernels, same arithmetic */
     float *g = (float *)(ws + align256((size_t)T * nslots * I * sizeof(float)));
     float *u = g + (size_t)T * nslots * I;
-    if (g53h_slot_mm_generic(g, x, T, K, nslots, L->experts, idx, L->shared, 0, I, E, 0)) return -1;
-    if (g53h_slot_mm_generic(u, x, T, K, nslots, L->experts, idx, L->shared, 1, I, E, 0)) return -1;
+    if (g53h_slot_rows(g, x, T, nslots, slots, 0, I, E, 0)) return -1;
+    if (g53h_slot_rows(u, x, T, nslots, slots, 1, I, E, 0)) return -1;
     if (g53h_swiglu_split(act, g, u, (long)T * nslots * I, L->swiglu_limit)) return -1;
-    if (g53h_slot_mm_generic(contrib, act, T, K, nslots, L->experts, idx, L->shared, 2, E, I, 1)) return -1;
+    if (g53h_slot_rows(contrib, act, T, nslots, slots, 2, E, I, 1)) return -1;
     g53h_prof_mark(G53_PROF_GENERIC);
     if (!fused) return 0;
     return g53h_combine_into(out, contrib, wts, T, E, K, nslots);

@@ -1,9 +1,9 @@
 /* g53h_ops.hip - the expert path's building blocks on gfx950, bit-exact with the reference:
  *
- *   k_mm_f8_generic   FP8 block-scaled matvec for any shape (ragged blocks, any br/bc),
- *                     one thread per (token, row). Used for odd shapes and as the
- *                     unit-level glm53f_mm; the decode layer uses the tiled kernels of
- *                     g53h_moe.hip for the expert shapes.
+ *   k_mm_f8_generic   FP8 block-scaled (or int4) matvec for any shape (ragged blocks, any
+ *                     br/bc), one thread per (token, row): the unit-level glm53f_mm. The
+ *                     layer paths use the kernels of g53h_moe.hip, g53h_rows.hip and the
+ *                     decode files.
  *   k_swiglu          clamped SwiGLU.
  *   k_router_scores   sigmoid(W x) and sigmoid + bias for T tokens, one wave per expert.
  *   k_router_select_w top-k by repeated argmax (strict >, lowest index), renormalise, scale.
@@ -18,23 +18,24 @@
 #include "g53h_runtime.h"
 
 /* ------------------------------------------------------------- FP8 matvec ---- */
-/* The reference's per-block arithmetic (src/core/glm53f_ops.c:195-227): eight fp32 lanes of
- * fused products stepping by 8 columns, reduced in double by a fixed tree, the block tail
- * added in double, the block sum scaled in double and accumulated over blocks in order. */
-__device__ double g53_block_dot(const uint8_t *row, const float *x, int j0, int j1)
+#include "g53h_rowdot.h"
+
+__device__ float g53_row_dot_i4(const G53hMat &m, int o, const float *x)
 {
-    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int j = j0;
-    for (; j + 8 <= j1; j += 8)
-        for (int l = 0; l < 8; l++) a[l] = __builtin_fmaf(g53_e4m3_to_f32(row[j + l]), x[j + l], a[l]);
-    double bsum = (((double)a[0] + a[4]) + ((double)a[2] + a[6]))
-                + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
-    for (; j < j1; j++) bsum += (double)g53_e4m3_to_f32(row[j]) * (double)x[j];
-    return bsum;
+    const uint8_t *row = m.w + (size_t)o * (m.cols / 2);
+    const float *srow = m.s + (size_t)o * m.scols;
+    double acc = 0.0;
+    for (int g = 0, j0 = 0; j0 < m.cols; g++, j0 += m.bc) {
+        const int j1 = (j0 + m.bc < m.cols) ? j0 + m.bc : m.cols;
+        const double p = g53_group_dot_i4(row, x, j0, j1) * (double)srow[g];
+        acc = acc + p;
+    }
+    return (float)acc;
 }
 
 __device__ float g53_row_dot(const G53hMat &m, int o, const float *x)
 {
+    if (m.flags & G53H_MAT_I4) return g53_row_dot_i4(m, o, x);
     const uint8_t *row = m.w + (size_t)o * m.cols;
     const float *srow = m.s + (size_t)(o / m.br) * m.scols;
     double acc = 0.0;
@@ -61,46 +62,14 @@ extern "C" int g53h_mm_f8(float *y, const float *x, int T, const G53hMat *m)
     if (T <= 0) return 0;
     if (!m || !m->w || !m->s) return g53h_fail("g53h_mm_f8: unbound matrix");
     if (m->rows <= 0 || m->cols <= 0 || m->br <= 0 || m->bc <= 0 ||
-        m->scols != (m->cols + m->bc - 1) / m->bc)
+        m->scols != (m->cols + m->bc - 1) / m->bc || ((m->flags & G53H_MAT_I4) && (m->cols & 1)))
         return g53h_fail("g53h_mm_f8: bad geometry %dx%d block %dx%d scols %d", m->rows, m->cols,
                          m->br, m->bc, m->scols);
+    if (m->flags & G53H_MAT_TILED) return g53h_fail("g53h_mm_f8: octet-tiled codes are read by the decode kernel only");
     const long n = (long)T * m->rows;
     hipLaunchKernelGGL(k_mm_f8_generic, dim3((unsigned)((n + 127) / 128)), dim3(128), 0,
                        g53h_stream(), y, x, T, *m);
     G53_LAUNCHED("k_mm_f8_generic");
-    return 0;
-}
-
-/* Generic per-slot expert matvec for the layer fallback: slot s of token t uses expert
- * idx[t][s] (s < K) or the shared expert (s == K). which: 0 gate, 1 up, 2 down. */
-__global__ void k_slot_mm_generic(float *__restrict__ y, const float *__restrict__ x, int T, int K,
-                                  int nslots, const G53hExpert *__restrict__ experts,
-                                  const int *__restrict__ idx, const G53hExpert *__restrict__ shared,
-                                  int which, int rows, int cols, int x_per_slot)
-{
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)T * nslots * rows) return;
-    const int o = (int)(i % rows);
-    const int s = (int)((i / rows) % nslots);
-    const int t = (int)(i / ((long)rows * nslots));
-    const G53hExpert *e = s < K ? &experts[idx[(size_t)t * K + s]] : shared;
-    const G53hMat &m = which == 0 ? e->gate : (which == 1 ? e->up : e->down);
-    const float *xt = x + ((size_t)t * (x_per_slot ? nslots : 1) + (x_per_slot ? s : 0)) * cols;
-    float v = 0.0f;
-    if (e->gate.w) v = g53_row_dot(m, o, xt);
-    else if (!(e->gate.flags & G53H_MAT_DROPPED)) return;      /* absent from this batch */
-    y[((size_t)t * nslots + s) * rows + o] = v;
-}
-
-int g53h_slot_mm_generic(float *y, const float *x, int T, int K, int nslots,
-                         const G53hExpert *experts, const int *idx, const G53hExpert *shared,
-                         int which, int rows, int cols, int x_per_slot)
-{
-    const long n = (long)T * nslots * rows;
-    hipLaunchKernelGGL(k_slot_mm_generic, dim3((unsigned)((n + 127) / 128)), dim3(128), 0,
-                       g53h_stream(), y, x, T, K, nslots, experts, idx, shared, which, rows, cols,
-                       x_per_slot);
-    G53_LAUNCHED("k_slot_mm_generic");
     return 0;
 }
 

@@ -82,7 +82,8 @@ __device__ __forceinline__ bool g53_wait_lds(int *flag, int want)
 /* A descriptor the fused path can use: 128 x 128 blocks and the released shapes. */
 __device__ __forceinline__ bool g53_desc_ok(const G53hExpert &e)
 {
-    return e.gate.br == 128 && e.gate.bc == 128 && e.gate.rows == G53_DEC_I && e.gate.cols == G53_DEC_E &&
+    return !((e.gate.flags | e.up.flags | e.down.flags) & G53H_MAT_I4) &&
+           e.gate.br == 128 && e.gate.bc == 128 && e.gate.rows == G53_DEC_I && e.gate.cols == G53_DEC_E &&
            e.up.br == 128 && e.up.bc == 128 && e.up.rows == G53_DEC_I && e.up.cols == G53_DEC_E &&
            e.down.br == 128 && e.down.bc == 128 && e.down.rows == G53_DEC_E && e.down.cols == G53_DEC_I &&
            e.gate.scols >= G53_DEC_NBE && e.up.scols >= G53_DEC_NBE && e.down.scols >= G53_DEC_NBI;

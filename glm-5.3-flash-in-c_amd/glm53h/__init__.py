@@ -163,6 +163,7 @@ _SIGS = {
     "g53h_mem_info": (C.c_int, [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
     # ops
     "g53h_mm_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.POINTER(G53hMat)]),
+    "g53h_i4_from_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(G53hMat)]),
     "g53h_swiglu": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_float]),
     "g53h_router": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                               C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_void_p]),
@@ -223,6 +224,7 @@ _SIGS = {
     "g53h_synth_uniform_host": (None, [C.c_void_p, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float]),
     # drop-in (glm53f.h)
     "glm53f_mm": (None, [C.c_void_p, C.c_void_p, C.POINTER(Glm53fMat)]),
+    "glm53f_i4_from_f8": (None, [C.c_void_p, C.c_void_p, C.POINTER(Glm53fMat)]),
     "glm53f_mm_batch": (None, [C.c_void_p, C.c_void_p, C.c_int, C.POINTER(Glm53fMat)]),
     "glm53f_e4m3f": (C.c_float, [C.c_uint8]),
     "glm53f_swiglu_clamp": (None, [C.c_void_p, C.c_void_p, C.c_int, C.c_float]),
@@ -246,7 +248,7 @@ _SIGS = {
     "glm53f_cache_sync": (C.c_int, [C.POINTER(Glm53fCache)]),
     "g53h_cache_is": (C.c_int, [C.POINTER(Glm53fExpertSrc)]),
     "g53h_cache_init_store": (C.c_int, [C.POINTER(Glm53fCache), C.POINTER(G53hStore), C.POINTER(Glm53fCfg),
-                                        C.c_int64, C.c_int]),
+                                        C.c_int64, C.c_int, C.c_int]),
     "g53h_st_open": (C.c_int, [C.POINTER(Glm53fSt), C.c_char_p, C.c_int]),
     "g53h_st_close": (None, [C.POINTER(Glm53fSt)]),
     "g53h_st_index": (C.c_int, [C.POINTER(Glm53fSt), C.c_char_p]),

@@ -46,6 +46,10 @@ class LayerSpec:
         sr = lambda r, c: ((r + self.br - 1) // self.br) * ((c + self.bc - 1) // self.bc) * 4
         return 3 * self.E * self.I + 2 * sr(self.I, self.E) + sr(self.E, self.I)
 
+    def expert_i4_bytes(self):
+        """Levels + steps of one int4 expert (14,155,776 B at the released shapes)."""
+        return 3 * (self.E * self.I // 2) + 3 * (self.E * self.I // 64) * 4
+
 
 CONFIG1 = dict(E=256, I=128, NE=16, K=8, router_sigma=0.02)
 CONFIG2 = dict(E=4096, I=2048, NE=288, K=8, router_sigma=1.0 / 64.0)
@@ -132,13 +136,19 @@ class DeviceLayer:
     bias_f32: np.ndarray = None
 
     tiled: bool = False
+    i4: bool = False
 
     @classmethod
-    def build(cls, sp: LayerSpec, n_experts_present=None, tiled=False):
+    def build(cls, sp: LayerSpec, n_experts_present=None, tiled=False, i4=False):
         """tiled: store every expert's codes octet-tiled (G53H_MAT_TILED), the layout the decode
-        kernel k_dec_tiled streams; the values are the same seeded codes either way."""
+        kernel k_dec_tiled streams; the values are the same seeded codes either way.
+        i4: re-quantise every routed expert on the device into the reference's int4 format
+        (G53H_MAT_I4: levels, and one step per row and 64 columns; the reference's
+        --experts int4), the shared expert staying FP8; the layer then has block_c 0."""
+        assert not (tiled and i4)
         self = cls(sp)
         self.tiled = bool(tiled)
+        self.i4 = bool(i4)
         E, I, NE = sp.E, sp.I, sp.NE
         shapes = _mat_shapes(sp)
         code_off, sc_off, off = [], [], 0
@@ -154,9 +164,28 @@ class DeviceLayer:
         L = lib()
         descs = (G53hExpert * (NE + 1))()
         stage = DevBuf(max(r * c for r, c in shapes)) if self.tiled else None
+        if self.i4:                              # FP8 staging of one matrix and its scales
+            s_stage = _align(max(r * c for r, c in shapes))
+            stage = DevBuf(s_stage + max(((r + sp.br - 1) // sp.br) * ((c + sp.bc - 1) // sp.bc) * 4
+                                         for r, c in shapes))
         for i in range(nslots):
             base = self.arena.ptr + i * self.slot_bytes
             mats = []
+            if self.i4 and i < NE:
+                off4 = 0
+                for m, (r, c) in enumerate(shapes):
+                    strm = stream(K_EXPERT, sp.layer, i * 3 + m)
+                    check(L.g53h_synth_f8(stage.ptr, stage.ptr + s_stage, r, c, sp.br, sp.bc, sp.seed, strm,
+                                          C.c_float(sp.expert_sigma)), "g53h_synth_f8")
+                    f = G53hMat(stage.ptr, stage.ptr + s_stage, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, 0)
+                    q = base + off4
+                    off4 = _align(off4 + r * c // 2)
+                    st = base + off4
+                    off4 = _align(off4 + r * (c // 64) * 4)
+                    check(L.g53h_i4_from_f8(q, st, C.byref(f)), "g53h_i4_from_f8")
+                    mats.append(G53hMat(q, st, r, c, 1, 64, c // 64, 4))
+                descs[i] = G53hExpert(*mats)
+                continue
             for m, (r, c) in enumerate(shapes):
                 strm = stream(K_SHARED, sp.layer, m) if i == NE else stream(K_EXPERT, sp.layer, i * 3 + m)
                 w, s = base + code_off[m], base + sc_off[m]
@@ -179,7 +208,7 @@ class DeviceLayer:
             routed_scale=sp.routed_scale, swiglu_limit=sp.limit, router=self.router.ptr, router_dt=1,
             bias=self.bias.ptr, experts=self.table.ptr,
             shared=(self.table.ptr + NE * C.sizeof(G53hExpert)) if sp.shared else None,
-            block_c=sp.bc, tiled=1 if self.tiled else 0)
+            block_c=0 if self.i4 else sp.bc, tiled=1 if self.tiled else 0)
         check(L.g53h_sync(), "g53h_sync")
         del stage
         return self
@@ -189,6 +218,13 @@ class DeviceLayer:
         d = self.experts[self.sp.NE if e == "shared" else e]
         out = []
         for m in (d.gate, d.up, d.down):
+            if m.flags & 4:                       # int4: levels [rows][cols/2], steps [rows][scols]
+                w = np.empty(m.rows * (m.cols // 2), np.uint8)
+                s = np.empty(m.rows * m.scols, np.float32)
+                check(lib().g53h_d2h(w.ctypes.data, m.w, w.nbytes), "d2h")
+                check(lib().g53h_d2h(s.ctypes.data, m.s, s.nbytes), "d2h")
+                out.append((w, s))
+                continue
             w = np.empty(m.rows * m.cols, np.uint8)
             s = np.empty(((m.rows + m.br - 1) // m.br) * m.scols, np.float32)
             check(lib().g53h_d2h(w.ctypes.data, m.w, w.nbytes), "d2h")
@@ -208,4 +244,5 @@ class DeviceLayer:
         """HBM bytes one layer call must read: each unique routed expert and the shared expert
         once, the bf16 router and the bias."""
         sp = self.sp
-        return (n_unique_routed + (1 if sp.shared else 0)) * sp.expert_bytes() + sp.NE * sp.E * 2 + sp.NE * 4
+        routed = sp.expert_i4_bytes() if self.i4 else sp.expert_bytes()
+        return n_unique_routed * routed + (sp.expert_bytes() if sp.shared else 0) + sp.NE * sp.E * 2 + sp.NE * 4

@@ -166,18 +166,33 @@ void glm53f_forget_host_weights(void)
     g_res_cap = g_res_n = 0;
 }
 
-static size_t mat_code_bytes(const Glm53fMat *m) { return (size_t)m->rows * (size_t)m->cols; }
+/* Bytes of a matrix's codes and scales: FP8 [rows][cols] codes and [ceil(rows/br)][scols]
+ * scales; int4 (GLM53F_WI4) [rows][cols/2] packed levels and [rows][scols] steps. */
+static size_t mat_code_bytes(const Glm53fMat *m)
+{
+    return m->dt == GLM53F_WI4 ? (size_t)m->rows * (size_t)(m->cols / 2) : (size_t)m->rows * (size_t)m->cols;
+}
 static size_t mat_scale_bytes(const Glm53fMat *m)
 {
-    return (size_t)((m->rows + m->br - 1) / m->br) * (size_t)m->scols * sizeof(float);
+    const size_t srows = m->dt == GLM53F_WI4 ? (size_t)m->rows : (size_t)((m->rows + m->br - 1) / m->br);
+    return srows * (size_t)m->scols * sizeof(float);
+}
+static int mat_flags(const Glm53fMat *m)
+{
+    return m->dt == GLM53F_WF8T ? G53H_MAT_TILED : (m->dt == GLM53F_WI4 ? G53H_MAT_I4 : 0);
 }
 
 static void check_f8(const Glm53fMat *m, const char *what)
 {
     if (!m->w) { fprintf(stderr, "glm53f: FATAL, multiply through an unbound matrix (%s)\n", what); abort(); }
-    if (m->dt != GLM53F_WF8 && m->dt != GLM53F_WF8T) {
+    if (m->dt != GLM53F_WF8 && m->dt != GLM53F_WF8T && m->dt != GLM53F_WI4) {
         fprintf(stderr, "glm53f: FATAL, %s has storage type %d; the MI355X expert path multiplies "
-                        "FP8 E4M3 matrices only\n", what, m->dt);
+                        "FP8 E4M3 and int4 (GLM53F_WI4) matrices only\n", what, m->dt);
+        abort();
+    }
+    if (m->dt == GLM53F_WI4 && (m->cols & 1)) {
+        fprintf(stderr, "glm53f: FATAL, %s is int4 with %d columns (two levels per byte need an even count)\n",
+                what, m->cols);
         abort();
     }
     if (m->br <= 0 || m->bc <= 0 || m->scols != (m->cols + m->bc - 1) / m->bc) {
@@ -195,7 +210,7 @@ static void check_f8(const Glm53fMat *m, const char *what)
 static void check_rowmajor(const Glm53fMat *m, const char *what)
 {
     check_f8(m, what);
-    if (m->dt != GLM53F_WF8) {
+    if (m->dt == GLM53F_WF8T) {
         fprintf(stderr, "glm53f: FATAL, %s is octet-tiled; layer weights are bound row-major (GLM53F_WF8)\n", what);
         abort();
     }
@@ -209,6 +224,7 @@ static G53hMat dev_mat_resident(const Glm53fMat *m, const char *what)
     d.w = (const uint8_t *)resident(m->w, mat_code_bytes(m));
     d.s = (const float *)resident(m->s, mat_scale_bytes(m));
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    d.flags = mat_flags(m);
     return d;
 }
 
@@ -218,7 +234,7 @@ static G53hMat view_mat_f8(const Glm53fMat *m)
     memset(&d, 0, sizeof d);
     d.w = (const uint8_t *)m->w; d.s = m->s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
-    d.flags = m->dt == GLM53F_WF8T ? G53H_MAT_TILED : 0;
+    d.flags = mat_flags(m);
     return d;
 }
 
@@ -243,6 +259,10 @@ static G53Buf g_tile_stage;
 static G53hMat dev_mat_resident_tiled(const Glm53fMat *m, const char *what)
 {
     check_rowmajor(m, what);
+    if (m->dt != GLM53F_WF8) {
+        fprintf(stderr, "glm53f: FATAL, %s: only FP8 matrices are kept octet-tiled\n", what);
+        abort();
+    }
     G53hMat d;
     memset(&d, 0, sizeof d);
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
@@ -290,11 +310,28 @@ static G53Buf g_mat[3];
 static G53hMat dev_mat_staged(const Glm53fMat *m, G53Buf *b, const char *what)
 {
     check_f8(m, what);
-    if (g53h_is_device_ptr(m->w)) return view_mat_f8(m);
+    const int dev = g53h_is_device_ptr(m->w);
+    if (dev && m->dt != GLM53F_WF8T) return view_mat_f8(m);
     const size_t cb = mat_code_bytes(m), sb = mat_scale_bytes(m);
     uint8_t *d = (uint8_t *)buf_get(b, ((cb + 255) & ~(size_t)255) + sb);
-    if (g53h_h2d(d, m->w, cb) || g53h_h2d(d + ((cb + 255) & ~(size_t)255), m->s, sb)) g53_die(what);
     G53hMat r = view_mat_f8(m);
+    if (m->dt == GLM53F_WF8T) {                      /* the unit kernels read row-major codes */
+        const uint8_t *src = (const uint8_t *)m->w;
+        if (!dev) {
+            uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
+            if (g53h_h2d(t, m->w, cb)) g53_die(what);
+            src = t;
+        }
+        if (g53h_untile_f8(d, src, m->rows, m->cols)) g53_die(what);
+        r.flags = 0;
+    } else if (g53h_h2d(d, m->w, cb)) {
+        g53_die(what);
+    }
+    if (dev) {
+        r.w = d;
+        return r;
+    }
+    if (g53h_h2d(d + ((cb + 255) & ~(size_t)255), m->s, sb)) g53_die(what);
     r.w = d;
     r.s = (const float *)(d + ((cb + 255) & ~(size_t)255));
     return r;
@@ -314,6 +351,26 @@ void glm53f_mm_batch(float *y, const float *x, int T, const Glm53fMat *m)
 }
 
 void glm53f_mm(float *y, const float *x, const Glm53fMat *m) { glm53f_mm_batch(y, x, 1, m); }
+
+void glm53f_i4_from_f8(unsigned char *q, float *steps, const Glm53fMat *src)
+{
+    ensure_device();
+    check_f8(src, "glm53f_i4_from_f8");
+    if (src->dt == GLM53F_WI4 || src->cols % GLM53F_I4_GROUP) {
+        fprintf(stderr, "glm53f: FATAL, glm53f_i4_from_f8 needs an FP8 matrix with columns a multiple of %d\n",
+                GLM53F_I4_GROUP);
+        abort();
+    }
+    const G53hMat d = dev_mat_staged(src, &g_mat[0], "glm53f_i4_from_f8");
+    const size_t qb = (size_t)src->rows * (size_t)(src->cols / 2);
+    const size_t sb = (size_t)src->rows * (size_t)(src->cols / GLM53F_I4_GROUP) * sizeof(float);
+    const int qdev = g53h_is_device_ptr(q), sdev = g53h_is_device_ptr(steps);
+    uint8_t *qd = qdev ? q : (uint8_t *)buf_get(&g_mat[1], qb);
+    float *sd = sdev ? steps : (float *)buf_get(&g_mat[2], sb);
+    if (g53h_i4_from_f8(qd, sd, &d)) g53_die("glm53f_i4_from_f8");
+    if ((!qdev && g53h_d2h(q, qd, qb)) || (!sdev && g53h_d2h(steps, sd, sb)) || g53h_sync())
+        g53_die("glm53f_i4_from_f8");
+}
 
 void glm53f_swiglu_clamp(float *y, const float *gu, int n, float limit)
 {
@@ -626,7 +683,8 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
             glm53f_expert_drops++;
             fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this output is CORRUPT\n", w->layer,
                     ids[j]);
-            continue;                               /* absent: its contribution is zero */
+            tab[j].gate.flags = G53H_MAT_DROPPED;  /* its contribution is zero */
+            continue;
         }
         held[nh++] = ids[j];
         check_expert_shape(&q, c, w->layer, ids[j]);
@@ -638,7 +696,8 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     HP(3);
     if (with_shared) {
         /* the shared expert resident in the layout of the routed slots */
-        const int tile_ok = tiled && w->sh_gate.rows % 8 == 0 && w->sh_gate.cols % 128 == 0 &&
+        const int tile_ok = tiled && w->sh_gate.dt == GLM53F_WF8 && w->sh_up.dt == GLM53F_WF8 &&
+                            w->sh_down.dt == GLM53F_WF8 && w->sh_gate.rows % 8 == 0 && w->sh_gate.cols % 128 == 0 &&
                             w->sh_down.rows % 8 == 0 && w->sh_down.cols % 128 == 0;
         if (tile_ok) {
             tab[K].gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
@@ -658,7 +717,8 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     L.router = gate; L.router_dt = dt; L.bias = bias; L.block_c = 128;
     for (int j = 0; j <= K; j++) {
         const G53hExpert *e = &tab[j];
-        if ((j < K || with_shared) && e->gate.w && (e->gate.bc != 128 || e->up.bc != 128 || e->down.bc != 128))
+        if ((j < K || with_shared) && e->gate.w && (e->gate.bc != 128 || e->up.bc != 128 || e->down.bc != 128 ||
+                                                    ((e->gate.flags | e->up.flags | e->down.flags) & G53H_MAT_I4)))
             L.block_c = 0;
     }
     G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
@@ -683,11 +743,14 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         G53hExpert chosen[GLM53F_MAX_TOPK + 1];
         memcpy(chosen, tab, (size_t)(K + 1) * sizeof(G53hExpert));
         memset(tab, 0, (size_t)(NE + 1) * sizeof(G53hExpert));
-        for (int j = 0; j < K; j++) if (chosen[j].gate.w) tab[ids[j]] = chosen[j];
+        for (int j = 0; j < K; j++) if (chosen[j].gate.w || chosen[j].gate.flags) tab[ids[j]] = chosen[j];
         tab[NE] = chosen[K];
         if (g53h_h2d_async(tab_d, tab, (size_t)(NE + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
         L.n_experts = NE; L.experts = tab_d; L.shared = with_shared ? tab_d + NE : NULL;
-        if (g53h_moe(od, xd, 1, &L, NULL, NULL)) g53_die("glm53f_moe");
+        /* FP8 with 128-column blocks: the one-launch decode (which routes again, to the same
+         * result); int4 experts and other blocks: the row kernels on the routing already made */
+        if (L.block_c == 128 ? g53h_moe(od, xd, 1, &L, NULL, NULL) : g53h_moe_routed_given(od, xd, 1, &L, idx_d, w_d))
+            g53_die("glm53f_moe");
     }
     HP(4);
     /* the HBM cache orders each slot's reuse after the kernels launched so far */
@@ -734,7 +797,18 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off)
     if (g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
     d.w = w; d.s = (const float *)s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
+    d.flags = m->dt == GLM53F_WI4 ? G53H_MAT_I4 : 0;
     return d;
+}
+
+/* Staging bytes of one expert's three matrices (stage_mat / rowmajor_view pad each part to 256). */
+static size_t expert_stage_bytes(const Glm53fExpertQ *q)
+{
+    const Glm53fMat *ms[3] = {&q->gate, &q->up, &q->down};
+    size_t n = 0;
+    for (int i = 0; i < 3; i++)
+        n += ((mat_code_bytes(ms[i]) + 255) & ~(size_t)255) + ((mat_scale_bytes(ms[i]) + 255) & ~(size_t)255);
+    return n;
 }
 
 /* An HBM view as the chunk kernels read it: row-major views as they are, octet-tiled ones
@@ -830,14 +904,14 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
     L.experts = table_d;
     L.block_c = 128;
     /* a chunk of tokens takes the grouped matrix-core kernels when the layer qualifies: every
-     * batch of fetched experts is multiplied for all its tokens at once */
-    const int grouped = T >= 2 && T <= g53h_grouped_max_tokens(&L) &&
-                        (!with_shared || (w->sh_gate.bc == 128 && w->sh_up.bc == 128 && w->sh_down.bc == 128));
-    float *contrib = grouped ? NULL : (float *)buf_get(&g_contrib, (size_t)T * nslots * E * sizeof(float));
-    if (grouped) {                               /* the plan reserves the shared expert's rows */
-        L.shared = with_shared ? table_d + NE : NULL;
-        if (g53h_grouped_begin(xd, T, &L, idx_d)) g53_die("glm53f_moe");
-    }
+     * batch of fetched experts is multiplied for all its tokens at once. The experts' format is
+     * known once the first batch is fetched: FP8 with 128-column blocks takes the grouped path,
+     * anything else (int4 experts, other blocks) the exact row kernels. */
+    int grouped = T >= 2 && T <= g53h_grouped_max_tokens(&L) &&
+                  (!with_shared || (w->sh_gate.dt == GLM53F_WF8 && w->sh_up.dt == GLM53F_WF8 &&
+                                    w->sh_down.dt == GLM53F_WF8 && w->sh_gate.bc == 128 && w->sh_up.bc == 128 &&
+                                    w->sh_down.bc == 128)) ? -1 : 0;
+    float *contrib = NULL;
     int held[GLM53F_MAX_TOPK];
     int first = 1;
     for (int g0 = 0; g0 < nu || (g0 == 0 && with_shared); g0 += G53_MOE_BATCH) {
@@ -859,8 +933,10 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                     continue;
                 }
                 check_expert_shape(&q, c, w->layer, e);
-                if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128) block_c = 0;
-                const size_t need = 3 * ((size_t)E * c->moe_inter + 256) + 3 * (mat_scale_bytes(&q.down) + 512);
+                if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128 || q.gate.dt == GLM53F_WI4 ||
+                    q.up.dt == GLM53F_WI4 || q.down.dt == GLM53F_WI4)
+                    block_c = 0;
+                const size_t need = expert_stage_bytes(&q);
                 const int dev = g53h_is_device_ptr(q.gate.w);
                 uint8_t *dst = (!dev || q.gate.dt == GLM53F_WF8T || q.up.dt == GLM53F_WF8T || q.down.dt == GLM53F_WF8T) ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
                 size_t off = 0;
@@ -884,13 +960,27 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                 sh.gate = dev_mat_resident(&w->sh_gate, "shared gate");
                 sh.up = dev_mat_resident(&w->sh_up, "shared up");
                 sh.down = dev_mat_resident(&w->sh_down, "shared down");
-                if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128) block_c = 0;
+                if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128 ||
+                    sh.gate.flags || sh.up.flags || sh.down.flags)
+                    block_c = 0;
                 table[NE] = sh;
                 if (g53h_h2d_async(table_d + NE, table + NE, sizeof sh)) g53_die("glm53f_moe");
                 L.shared = table_d + NE;
             }
             if (g53h_h2d_async(table_d, table, (size_t)NE * sizeof(G53hExpert))) g53_die("glm53f_moe");
             L.block_c = block_c;
+            if (grouped < 0) {                       /* decided by the first batch */
+                int present = 0;
+                for (int u = b0; u < b0 + bn; u++) if (table[uniq[u]].gate.w) present = 1;
+                grouped = block_c == 128 && present;
+                if (grouped) {                       /* the plan reserves the shared expert's rows */
+                    const G53hExpert *keep_shared = L.shared;
+                    L.shared = with_shared ? table_d + NE : NULL;
+                    if (g53h_grouped_begin(xd, T, &L, idx_d)) g53_die("glm53f_moe");
+                    L.shared = keep_shared;
+                }
+            }
+            if (!grouped && !contrib) contrib = (float *)buf_get(&g_contrib, (size_t)T * nslots * E * sizeof(float));
             if (grouped) {
                 if (block_c != 128) {
                     fprintf(stderr, "glm53f: FATAL, a routed expert of layer %d has no 128-column blocks\n", w->layer);

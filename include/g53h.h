@@ -66,6 +66,11 @@ int         g53h_mem_info(size_t *free_b, size_t *total_b);
  *               accumulators of one row (src/core/glm53f_ops.c:185-228), in order. */
 #define G53H_MAT_DROPPED 1      /* on an expert's gate: the expert failed to load             */
 #define G53H_MAT_TILED   2      /* codes in the octet-tiled layout                            */
+/* The reference's int4 format (GLM53F_WI4, include/glm53f/glm53f.h:115-125): w holds packed
+ * levels [rows][cols / 2] (element (i, j) is nibble j % 2 of byte i * cols / 2 + j / 2, the even
+ * column in the low nibble, minus 8), s one fp32 step per row and group of bc columns,
+ * [rows][scols]; br is ignored (one step row per matrix row). cols must be even. */
+#define G53H_MAT_I4      4
 typedef struct {
     const uint8_t *w;
     const float   *s;
@@ -88,8 +93,18 @@ typedef struct {
 } G53hExpert;
 
 /* y[T][rows] = M . x[T][cols], bit-exact with glm53f_mm per token
- * (replaces src/core/glm53f_ops.c:185-228 matmul_f8 and :376-444 matmul_f8_batch). */
+ * (replaces src/core/glm53f_ops.c:185-228 matmul_f8 and :376-444 matmul_f8_batch; for a
+ * G53H_MAT_I4 matrix src/core/glm53f_ops.c:236-296 matmul_i4). */
 int g53h_mm_f8(float *y_d, const float *x_d, int T, const G53hMat *m);
+
+/* FP8 -> int4 re-quantisation (replaces src/core/glm53f_ops.c:302-371 glm53f_i4_from_f8), bit-exact:
+ * per row and group of 64 columns, step = max|value| / 7 (the block scale folded into the step
+ * when the group lies in one scale block, else into the values; floor 1e-30), level =
+ * clamp(rint(value / step), -8, 7). q_d [rows][cols / 2], steps_d [rows][cols / 64]; src is a
+ * row-major FP8 matrix with cols a multiple of 64. Stream-ordered on the compute stream. NaN codes
+ * (E4M3 0x7f / 0xff) give level 0 and do not count towards the maximum (the reference's scalar
+ * build; its AVX2 build differs on them, and checkpoints hold none). */
+int g53h_i4_from_f8(uint8_t *q_d, float *steps_d, const G53hMat *src);
 
 /* y[T][n] = swiglu_clamp(gu[T][2n]) (replaces src/core/glm53f_ops.c:486-494). */
 int g53h_swiglu(float *y_d, const float *gu_d, int n, int T, float limit);
@@ -139,6 +154,9 @@ typedef struct {
                                        tiled kernels; any other value the generic ones)     */
     int               tiled;        /* 1: every expert matrix (routed and shared) is in the
                                        octet-tiled layout (G53H_MAT_TILED), 0: row-major     */
+    /* Experts in the int4 format (G53H_MAT_I4, per matrix) need block_c = 0 and tiled = 0: the
+       row-wave kernels then take them (and any FP8 matrix, such as the shared expert, in the
+       same layer), exactly as glm53f_mm on a GLM53F_WI4 matrix. */
 } G53hMoeLayer;
 
 /* Whole MoE layer on the device (replaces src/core/glm53f_ops.c:1144-1342 moe_chunk with

@@ -92,16 +92,23 @@ typedef struct {
     int   n_eos;
 } Glm53fCfg;
 
-/* Storage formats of a matrix. Only GLM53F_WF8 is multiplied on the GPU by this library;
- * the router is fp32 (GLM53F_WF32) or bf16 (GLM53F_WBF16) bit patterns. GLM53F_WF8T is this
+/* Storage formats of a matrix. GLM53F_WF8 and GLM53F_WI4 are multiplied on the GPU by this
+ * library; the router is fp32 (GLM53F_WF32) or bf16 (GLM53F_WBF16) bit patterns. GLM53F_WF8T is this
  * library's own: the expert views of its HBM cache (glm53f_cache.h) hold the same E4M3 codes in
  * the octet-tiled layout of g53h.h (G53H_MAT_TILED), for its kernels; the reference never makes
  * one. */
 enum { GLM53F_WF32 = 0, GLM53F_WBF16 = 1, GLM53F_WF8 = 2, GLM53F_WI4 = 3, GLM53F_WF8T = 0x102 };
 
+/* Group size of the GLM53F_WI4 matrices the reference's engine produces
+ * (include/glm53f/glm53f.h:124-125). */
+#define GLM53F_I4_GROUP 64
+
 /* A self-describing matrix. For GLM53F_WF8, w holds rows*cols E4M3 codes row-major and s
  * the fp32 block scales [ceil(rows/br)][scols]; element (i,j) = E4M3(w[i*cols+j]) *
- * s[(i/br)*scols + j/bc]. */
+ * s[(i/br)*scols + j/bc]. For GLM53F_WI4 (include/glm53f/glm53f.h:115-121), w holds
+ * rows*cols/2 bytes of signed 4-bit levels, two per byte (the even column in the low nibble,
+ * level = nibble - 8), and s one fp32 step per row and group of bc columns [rows][scols];
+ * element (i,j) = level(i,j) * s[i*scols + j/bc]. */
 typedef struct {
     const void  *w;
     const float *s;
@@ -125,13 +132,19 @@ static inline float glm53f_bf16f(uint16_t h)
     return v.f;
 }
 
+/* FP8 -> GLM53F_WI4 (include/glm53f/glm53f.h:144-147, src/core/glm53f_ops.c:302-371): q holds
+ * rows*(cols/2) bytes, steps rows*(cols/GLM53F_I4_GROUP) floats; per row and group of 64 columns
+ * step = max|w|/7, level = rint(w/step) clamped to [-8, 7]. cols must be a multiple of 64. Runs on
+ * the GPU (g53h_i4_from_f8); src, q and steps may each be host or HBM memory. */
+void glm53f_i4_from_f8(unsigned char *q, float *steps, const Glm53fMat *src);
+
 /* E4M3FN code -> float, exact; 0x7f and 0xff are NaN. */
 float glm53f_e4m3f(uint8_t b);
 
 /* y[i] = silu(min(g[i], limit)) * clamp(u[i], -limit, limit) over gu = [g | u] of 2n. */
 void glm53f_swiglu_clamp(float *y, const float *gu, int n, float limit);
 
-/* One routed expert: three FP8 matrices. */
+/* One routed expert: three FP8 (or int4) matrices. */
 typedef struct {
     Glm53fMat gate, up, down;
 } Glm53fExpertQ;

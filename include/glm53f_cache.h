@@ -24,7 +24,11 @@
  *     the released checkpoint stores them, else six), then copied to the slot;
  *   - g53h_cache_init_store takes any other source of host-resident experts (G53hStore
  *     below), e.g. experts already in pinned host memory;
- *   - int4 slots (i4 != 0) are not supported: init returns -1.
+ *   - int4 slots (i4 != 0, the reference's --experts int4): each FP8 expert read is staged in
+ *     HBM and re-quantised into the slot by the device quantiser (g53h_i4_from_f8, bit-exact
+ *     with the reference's glm53f_i4_from_f8), in the reference's int4 slot layout, so a budget
+ *     holds the reference's number of slots and get() returns its GLM53F_WI4 views. The
+ *     reference's pre-quantised int4 container files (glm53f_i4_dir) are not read.
  */
 #ifndef GLM53F_CACHE_H
 #define GLM53F_CACHE_H
@@ -54,7 +58,8 @@ extern "C" {
  *                      callers; clock is refreshed at each call)
  *   n_io               prefetch copies kept in flight (0: prefetch off)
  *   stage              this library's state (an opaque pointer; the int4 staging it names in
- *                      the reference does not exist here, i4 is always 0)
+ *                      the reference lives in HBM here, inside that state)
+ *   i4                 1 for int4 slots
  *   statistics         as the reference's, reset by glm53f_cache_reset_stats
  * Unused here, left zero: raw_bytes, stage_busy, nstage, stage_free, i4_fd, i4_layers, ref,
  * pad, mu, landed, work, io, stop, queue. */
@@ -110,7 +115,7 @@ typedef struct {
  * down}_proj.{weight,weight_scale_inv}", FP8 E4M3 codes with F32 scale grids); the slot geometry
  * comes from expert 0 of the first MoE layer (cfg->is_dense), as the reference probes it.
  * Fails (-1) if fewer than topk+1 slots fit, if HBM cannot hold the arena, if the probe expert
- * is missing or not FP8, or for i4 != 0. */
+ * is missing or not FP8, or (i4 != 0) if a matrix's columns are not a multiple of 64. */
 int  glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
                        int n_io, int i4);
 void glm53f_cache_free(Glm53fCache *c);
@@ -131,7 +136,7 @@ typedef struct G53hStore {
 /* glm53f_cache_init over a G53hStore instead of a checkpoint (no counterpart in the
  * reference, whose cache always reads the checkpoint). */
 int  g53h_cache_init_store(Glm53fCache *c, const G53hStore *store, const Glm53fCfg *cfg, int64_t budget_bytes,
-                           int n_io);
+                           int n_io, int i4);
 
 /* Wait until every copy the cache issued has landed (tests and benchmarks). */
 int  glm53f_cache_sync(Glm53fCache *c);

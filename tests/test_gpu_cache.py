@@ -74,12 +74,12 @@ class Layers:
 def new_cache(cf, st, slots, n_io):
     c = glm53h.Glm53fCache()
     L = glm53h.lib()
-    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), 0, 0) == -1   # no slot fits
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), 0, 0, 0) == -1   # no slot fits
     probe = glm53h.Glm53fCache()
-    assert L.g53h_cache_init_store(C.byref(probe), C.byref(st), C.byref(cf), 1 << 30, 0) == 0
+    assert L.g53h_cache_init_store(C.byref(probe), C.byref(st), C.byref(cf), 1 << 30, 0, 0) == 0
     budget = probe.slot_bytes * slots
     L.glm53f_cache_free(C.byref(probe))
-    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), budget, n_io) == 0
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), budget, n_io, 0) == 0
     assert c.nslot == slots and L.g53h_cache_is(C.byref(c.src)) == 1
     return c
 
@@ -170,19 +170,19 @@ def test_cache_drop_path_and_store_protocol(L):
         L.glm53f_cache_free(C.byref(c))
 
 
-def test_cache_rejects_int4_and_tiny_budgets(L):
+def test_cache_rejects_empty_index_and_tiny_budgets(L):
     sp = S.spec(1)
     cf = make_cfg(sp)
     ly = Layers(sp)
     store = PyStore(sp, ly.ex)
     c = glm53h.Glm53fCache()
     ckpt = glm53h.Glm53fSt()
-    assert L.glm53f_cache_init(C.byref(c), C.byref(ckpt), C.byref(cf), 1 << 30, 0, 1) == -1   # int4 slots
+    assert L.glm53f_cache_init(C.byref(c), C.byref(ckpt), C.byref(cf), 1 << 30, 0, 1) == -1   # no tensors
     probe = glm53h.Glm53fCache()
-    assert L.g53h_cache_init_store(C.byref(probe), C.byref(store.st), C.byref(cf), 1 << 30, 0) == 0
+    assert L.g53h_cache_init_store(C.byref(probe), C.byref(store.st), C.byref(cf), 1 << 30, 0, 0) == 0
     sb = probe.slot_bytes
     L.glm53f_cache_free(C.byref(probe))
-    assert L.g53h_cache_init_store(C.byref(c), C.byref(store.st), C.byref(cf), sb * sp.K, 0) == -1   # < topk+1
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(store.st), C.byref(cf), sb * sp.K, 0, 0) == -1   # < topk+1
 
 
 class PoolSrc:

@@ -77,7 +77,7 @@ def test_device_pointers_cached_decode(L):
           "store")
     cache = glm53h.Glm53fCache()
     try:
-        assert L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), 40 * 25174016, 2) == 0
+        assert L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), 40 * 25174016, 2, 0) == 0
         w = moe_w(sp, W, b, sh, cache.src)
         for t in range(3):
             x = np.ascontiguousarray(S.x_host(sp, 1, batch=30 + t), np.float32)

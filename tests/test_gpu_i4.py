@@ -1,0 +1,338 @@
+"""GPU parity of the int4 expert path: the reference's --experts int4 mode, GLM53F_WI4 routed
+experts re-quantised from FP8 by glm53f_i4_from_f8 (src/core/glm53f_ops.c:302-371) and
+multiplied by matmul_i4 (src/core/glm53f_ops.c:236-296), the shared expert staying FP8.
+
+Through the C ABI: the device quantiser, the int4 matvec, the MoE layer (g53h_moe with int4
+descriptors), the C drop-in with host int4 views, and the HBM cache in int4 mode
+(glm53f_cache_init / g53h_cache_init_store with i4 = 1). Bar: bit for bit against golden
+outputs of the compiled reference (tests/golden/i4.npz) and the pinned oracle."""
+import ctypes as C
+import hashlib
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import glm53h
+import glm53h.synth as S
+import oracle_lib as O
+from glm53h import DevBuf, G53hMat, check
+from test_gpu_cache import N_MOE_LAYERS, Layers, PyStore, make_cfg
+from test_gpu_parity import cfg_struct, fmat, same, say
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+G4 = np.load(os.path.join(HERE, "golden", "i4.npz"))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+from make_i4 import NAL_CASES, nal_inputs  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def L():
+    return glm53h.init(0)
+
+
+def dev_quant(w, s, rows, cols, br, bc):
+    """g53h_i4_from_f8 on FP8 (w, s) uploaded to HBM: (levels, steps) downloaded."""
+    L = glm53h.lib()
+    wd, sd = DevBuf.from_array(np.ascontiguousarray(w, np.uint8)), DevBuf.from_array(np.ascontiguousarray(s, np.float32))
+    qd, std = DevBuf(rows * cols // 2), DevBuf(rows * (cols // 64) * 4)
+    m = G53hMat(wd.ptr, sd.ptr, rows, cols, br, bc, (cols + bc - 1) // bc, 0)
+    check(L.g53h_i4_from_f8(qd.ptr, std.ptr, C.byref(m)), "g53h_i4_from_f8")
+    check(L.g53h_sync(), "sync")
+    return qd.download(np.uint8).reshape(rows, cols // 2), std.download(np.float32).reshape(rows, cols // 64)
+
+
+def imat(q, st, rows, cols):
+    return glm53h.Glm53fMat(q.ctypes.data, st.ctypes.data, glm53h.GLM53F_WI4, rows, cols, 1, 64, cols // 64)
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).digest()
+
+
+# ----------------------------------------------------------------- quantiser ----
+def test_quantiser_known_answer_and_unaligned_blocks(L):
+    _, c = O.i4_kat_cases()
+    say("int4 quantiser: the reference's known-answer case 512 x 4096")
+    q, st = dev_quant(c["w"], c["s"], c["rows"], c["cols"], c["br"], c["bc"])
+    assert sha(q) == G4["kat_quant_q_sha"].tobytes() and sha(st) == G4["kat_quant_steps_sha"].tobytes()
+    for i, (rows, cols, br, bc, seed) in enumerate(NAL_CASES):
+        say("int4 quantiser: unaligned scale blocks", rows, cols, br, bc)
+        w, s = nal_inputs(rows, cols, br, bc, seed)
+        q, st = dev_quant(w, s, rows, cols, br, bc)
+        assert np.array_equal(q, G4[f"nal{i}_q"]) and same(st, G4[f"nal{i}_steps"])
+
+
+def test_quantiser_released_shapes_against_oracle(L):
+    sp = S.spec(2)
+    (gw, gs), _, (dw, ds) = S.expert_host(sp, 5)
+    for w, s, r, c in [(gw, gs, sp.I, sp.E), (dw, ds, sp.E, sp.I)]:
+        say("int4 quantiser", r, "x", c)
+        q, st = dev_quant(w, s, r, c, sp.br, sp.bc)
+        qo, so = O.i4_from_f8(O.oracle(), w, s, r, c, sp.br, sp.bc)
+        assert np.array_equal(q, qo) and same(st, so)
+
+
+def test_quantiser_zero_groups_and_nan_codes(L):
+    """An all-zero group gets the floor step 1e-30 and level 0; NaN codes give level 0 and are
+    left out of the maximum (the reference's scalar build)."""
+    w = np.zeros((2, 128), np.uint8)
+    w[1, :64] = 0x38                                 # 1.0
+    w[1, 5], w[1, 9] = 0x7f, 0xff                    # NaN codes
+    w[1, 7] = 0x30                                   # 0.5 -> rint(3.5) = 4
+    s = np.array([2.0], np.float32)
+    q, st = dev_quant(w.ravel(), s, 2, 128, 128, 128)
+    assert np.all(q[0] == 0x88) and np.all(st[0] == np.float32(1e-30)) and st[1, 1] == np.float32(1e-30)
+    lv = np.empty((2, 128), np.int64)
+    lv[:, 0::2], lv[:, 1::2] = (q & 15).astype(np.int64) - 8, (q >> 4).astype(np.int64) - 8
+    assert lv[1, 5] == 0 and lv[1, 9] == 0 and lv[1, 7] == 4 and lv[1, 0] == 7
+    assert st[1, 0] == np.float32(np.float32(2.0) / np.float32(7.0))
+
+
+# -------------------------------------------------------------------- matvec ----
+def test_i4_matvec_known_answer_cases(L):
+    cases, _ = O.i4_kat_cases()
+    for i, c in enumerate(cases):
+        say("int4 matvec", c["rows"], "x", c["cols"])
+        qd, sd, xd = DevBuf.from_array(c["q"]), DevBuf.from_array(c["steps"]), DevBuf.from_array(c["x"])
+        yd = DevBuf(c["rows"] * 4)
+        m = G53hMat(qd.ptr, sd.ptr, c["rows"], c["cols"], 1, 64, c["cols"] // 64, 4)
+        check(L.g53h_mm_f8(yd.ptr, xd.ptr, 1, C.byref(m)), "g53h_mm_f8")
+        assert same(yd.download(np.float32), G4[f"kat_i4_y{i}"])
+    say("drop-in glm53f_mm on a host int4 matrix, and glm53f_i4_from_f8")
+    c = cases[2]
+    y = np.zeros(c["rows"], np.float32)
+    L.glm53f_mm(y.ctypes.data, c["x"].ctypes.data, C.byref(imat(c["q"], c["steps"], c["rows"], c["cols"])))
+    assert same(y, G4["kat_i4_y2"])
+    _, k = O.i4_kat_cases()
+    q = np.empty((k["rows"], k["cols"] // 2), np.uint8)
+    st = np.empty((k["rows"], k["cols"] // 64), np.float32)
+    L.glm53f_i4_from_f8(q.ctypes.data, st.ctypes.data,
+                        C.byref(fmat(k["w"], k["s"], k["rows"], k["cols"], k["br"], k["bc"])))
+    assert sha(q) == G4["kat_quant_q_sha"].tobytes() and sha(st) == G4["kat_quant_steps_sha"].tobytes()
+    L.glm53f_forget_host_weights()
+
+
+# --------------------------------------------------------------------- layer ----
+def test_layer_i4_config1(L):
+    sp = S.spec(1)
+    say("int4 layer, config 1 (experts quantised on the device)")
+    layer = S.DeviceLayer.build(sp, i4=True)
+    x = S.x_host(sp, 8, batch=0)
+    for t in range(8):
+        xd, out = DevBuf.from_array(x[t:t + 1]), DevBuf(sp.E * 4)
+        layer.forward(out, xd, 1)
+        assert same(out.download(np.float32), G4["c1_out"][t]), t
+    xb = S.x_host(sp, 5, batch=1)
+    xd, out = DevBuf.from_array(xb), DevBuf(5 * sp.E * 4)
+    layer.forward(out, xd, 5)
+    assert same(out.download(np.float32).reshape(5, sp.E), G4["c1b_out"])
+    lay = glm53h.G53hMoeLayer.from_buffer_copy(layer.layer)
+    lay.shared = None
+    check(L.g53h_moe(out.ptr, xd.ptr, 5, C.byref(lay), None, None), "g53h_moe")
+    assert same(out.download(np.float32).reshape(5, sp.E), G4["c1b_routed_out"])
+
+
+def test_layer_i4_config2(L):
+    sp = S.spec(2)
+    say("int4 layer, config 2: quantising 288 experts on the device")
+    layer = S.DeviceLayer.build(sp, i4=True)
+    x1 = S.x_host(sp, 1, batch=0)
+    xd, out = DevBuf.from_array(x1), DevBuf(sp.E * 4)
+    say("config 2 int4 decode token vs the reference")
+    layer.forward(out, xd, 1)
+    assert same(out.download(np.float32), G4["c2_out"])
+    say("config 2 int4, T = 4 against the oracle on the device's own levels")
+    x4 = S.x_host(sp, 4, batch=3)
+    xd4, out4, idx4 = DevBuf.from_array(x4), DevBuf(4 * sp.E * 4), DevBuf(4 * sp.K * 4)
+    layer.forward(out4, xd4, 4, idx4)
+    got = out4.download(np.float32).reshape(4, sp.E)
+    ids = idx4.download(np.int32).reshape(4, sp.K)
+    qm = {int(e): layer.fetch_expert(int(e)) for e in np.unique(ids)}
+    want, wi, _ = O.moe_i4(O.oracle(), x4, sp, layer.router_f32, layer.bias_f32, qm, layer.fetch_expert("shared"))
+    assert np.array_equal(ids, wi) and same(got, want)
+    say("config 2 int4, T = 64: each token as its own decode")
+    x64 = S.x_host(sp, 64, batch=4)
+    xd64, out64 = DevBuf.from_array(x64), DevBuf(64 * sp.E * 4)
+    layer.forward(out64, xd64, 64)
+    got64 = out64.download(np.float32).reshape(64, sp.E)
+    for t in (0, 17, 63):
+        xt, ot = DevBuf.from_array(x64[t:t + 1]), DevBuf(sp.E * 4)
+        layer.forward(ot, xt, 1)
+        assert same(ot.download(np.float32), got64[t]), t
+
+
+def test_layer_i4_other_group_counts(L):
+    """Rows of 10 and 5 groups (16 and 8 lanes per row in the row-wave kernel), a ragged
+    FP8 shared expert (320 columns over 128-column blocks), T = 1 and T = 3, against the oracle."""
+    sp = S.spec(1, E=640, I=320, NE=16, K=4, seed=21)
+    layer = S.DeviceLayer.build(sp, i4=True)
+    for T in (1, 3):
+        say("int4 layer hidden 640 inter 320, T =", T)
+        x = S.x_host(sp, T, batch=T)
+        xd, out, idx = DevBuf.from_array(x), DevBuf(T * sp.E * 4), DevBuf(T * sp.K * 4)
+        layer.forward(out, xd, T, idx)
+        ids = idx.download(np.int32).reshape(T, sp.K)
+        qm = {int(e): layer.fetch_expert(int(e)) for e in np.unique(ids)}
+        want, wi, _ = O.moe_i4(O.oracle(), x, sp, layer.router_f32, layer.bias_f32, qm, layer.fetch_expert("shared"))
+        assert np.array_equal(ids, wi) and same(out.download(np.float32).reshape(T, sp.E), want)
+
+
+# ------------------------------------------------------------- the C drop-in ----
+class HostSrcI4:
+    """An Glm53fExpertSrc serving host int4 views ({e: [(levels, steps)] x 3})."""
+
+    def __init__(self, cf, experts, drop=()):
+        self.cf, self.ex, self.drop = cf, experts, set(drop)
+        self.pinned = 0
+        self.src = glm53h.Glm53fExpertSrc()
+        self._get = glm53h.GET_FN(self.get)
+        self._rel = glm53h.RELEASE_FN(self.release)
+        self.src.get, self.src.release = self._get, self._rel
+
+    def get(self, selfp, layer, e, q):
+        if e in self.drop:
+            return -1
+        (gq, gs), (uq, us), (dq, ds) = self.ex[e]
+        E, I = self.cf.hidden, self.cf.moe_inter
+        q[0].gate, q[0].up, q[0].down = imat(gq, gs, I, E), imat(uq, us, I, E), imat(dq, ds, E, I)
+        self.pinned += 1
+        return 0
+
+    def release(self, selfp, layer, e):
+        self.pinned -= 1
+
+
+def c1_cfg(sp):
+    return cfg_struct(dict(E=sp.E, I=sp.I, NE=sp.NE, K=sp.K, routed_scale=sp.routed_scale, norm_topk=sp.norm_topk,
+                           limit=sp.limit, br=sp.br, bc=sp.bc))
+
+
+def test_dropin_int4_host_views(L):
+    from test_gpu_parity import dropin_moe
+    sp = S.spec(1)
+    cf = c1_cfg(sp)
+    W, b = S.router_host(sp), S.bias_host(sp)
+    qm = {e: O.quantise_expert(O.oracle(), S.expert_host(sp, e), sp) for e in range(sp.NE)}
+    sh = S.expert_host(sp, "shared")
+    xb = S.x_host(sp, 5, batch=1)
+    say("drop-in glm53f_moe, int4 host views, T=5")
+    src = HostSrcI4(cf, qm)
+    assert same(dropin_moe(cf, W, b, qm, sh, xb, src=src), G4["c1b_out"])
+    assert same(dropin_moe(cf, W, b, qm, sh, xb, shared=False, src=HostSrcI4(cf, qm)), G4["c1b_routed_out"])
+    say("drop-in int4 decode tokens")
+    x = S.x_host(sp, 8, batch=0)
+    for t in range(8):
+        assert same(dropin_moe(cf, W, b, qm, sh, x[t:t + 1], src=HostSrcI4(cf, qm))[0], G4["c1_out"][t]), t
+    say("drop-in int4 with experts 3 and 7 failing to load")
+    kept = {e: m for e, m in qm.items() if e not in (3, 7)}
+    want = O.moe_i4(O.oracle(), xb, sp, W, b, kept, sh)[0]
+    assert same(dropin_moe(cf, W, b, qm, sh, xb, src=HostSrcI4(cf, qm, drop=(3, 7))), want)
+
+
+# --------------------------------------------------------------- cache, int4 ----
+def ref_i4_slot_bytes(sp):
+    """The reference's int4 slot (src/io/glm53f_load.c:141-163): per matrix the levels, then the
+    steps, each 64-byte aligned; rounded up to 4096."""
+    off = 0
+    for r, c in [(sp.I, sp.E), (sp.I, sp.E), (sp.E, sp.I)]:
+        off = (off + 63) // 64 * 64 + r * (c // 2)
+        off = (off + 63) // 64 * 64 + r * (c // 64) * 4
+    return (off + 4095) // 4096 * 4096
+
+
+def new_cache_i4(cf, st, slots, n_io):
+    L = glm53h.lib()
+    probe = glm53h.Glm53fCache()
+    assert L.g53h_cache_init_store(C.byref(probe), C.byref(st), C.byref(cf), 1 << 30, 0, 1) == 0
+    sb = probe.slot_bytes
+    L.glm53f_cache_free(C.byref(probe))
+    c = glm53h.Glm53fCache()
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), sb * slots, n_io, 1) == 0
+    assert c.nslot == slots and c.i4 == 1
+    return c, sb
+
+
+def test_cache_int4_mode_config1(L):
+    """The HBM cache quantising FP8 reads into int4 slots: the reference's slot size, decode and
+    chunk outputs equal to the reference with int4 experts (golden), any budget and prefetch."""
+    sp = S.spec(1)
+    cf = make_cfg(sp)
+    ly = Layers(sp)
+    x = S.x_host(sp, 8, batch=0)
+    want = np.repeat(G4["c1_out"][:, None, :], N_MOE_LAYERS, axis=1)
+    store = PyStore(sp, ly.ex)
+    for slots, n_io, pf in [(sp.K + 1, 0, 0), (12, 2, 6), (80, 2, 6)]:
+        say("int4 cache: slots", slots, "prefetch", n_io, pf)
+        c, sb = new_cache_i4(cf, store.st, slots, n_io)
+        try:
+            assert sb == ref_i4_slot_bytes(sp)
+            got = ly.run(c.src, cf, x, prefetch_n=pf)
+            check(L.glm53f_cache_sync(C.byref(c)), "sync")
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+            assert c.hits + c.misses == x.shape[0] * N_MOE_LAYERS * sp.K
+            assert c.bytes_read == (c.misses + c.prefetch_reads) * sp.expert_bytes()   # FP8 bytes read
+            w = ly.moe_w(c.src, 0)
+            xb = np.ascontiguousarray(S.x_host(sp, 5, batch=1), np.float32)
+            out = np.zeros((5, sp.E), np.float32)
+            L.glm53f_moe(out.ctypes.data, xb.ctypes.data, C.byref(w), C.byref(cf), 5, None)
+            assert same(out, G4["c1b_out"])
+        finally:
+            L.glm53f_cache_free(C.byref(c))
+
+
+def test_cache_int4_mode_config2(L):
+    """Released shapes (14,155,776-byte int4 slots): two layers, three tokens, through the int4
+    cache, equal to host int4 views of the same experts quantised by the oracle."""
+    sp = S.spec(2)
+    NP = 12
+    cf = make_cfg(sp)
+    cf.n_layers = 2
+    pool = [O.quantise_expert(O.oracle(), S.expert_host(sp, p), sp) for p in range(NP)]
+    W = [S.router_host(S.spec(2, layer=l)) for l in range(2)]
+    B = [S.bias_host(S.spec(2, layer=l)) for l in range(2)]
+    sh = S.expert_host(sp, "shared")
+    x = S.x_host(sp, 3, batch=7)
+
+    class PoolI4(HostSrcI4):
+        def get(self, selfp, layer, e, q):
+            (gq, gs), (uq, us), (dq, ds) = pool[(layer * sp.NE + e) % NP]
+            q[0].gate, q[0].up, q[0].down = imat(gq, gs, sp.I, sp.E), imat(uq, us, sp.I, sp.E), imat(dq, ds, sp.E, sp.I)
+            return 0
+
+    def run(src, pf):
+        outs = []
+        for t in range(3):
+            for l in range(2):
+                w = glm53h.Glm53fMoeW()
+                w.gate, w.bias = W[l].ctypes.data, B[l].ctypes.data
+                (gw, gs), (uw, us), (dw, ds) = sh
+                w.sh_gate, w.sh_up = fmat(gw, gs, sp.I, sp.E, sp.br, sp.bc), fmat(uw, us, sp.I, sp.E, sp.br, sp.bc)
+                w.sh_down = fmat(dw, ds, sp.E, sp.I, sp.br, sp.bc)
+                w.src = C.pointer(src)
+                w.layer, w.prefetch_n = l, pf
+                if pf and l == 0:
+                    w.next_gate, w.next_bias = W[1].ctypes.data, B[1].ctypes.data
+                out = np.zeros((1, sp.E), np.float32)
+                xt = np.ascontiguousarray(x[t:t + 1])
+                L.glm53f_moe(out.ctypes.data, xt.ctypes.data, C.byref(w), C.byref(cf), 1, None)
+                outs.append(out[0])
+        return np.asarray(outs)
+
+    say("config 2 int4 through host views")
+    want = run(PoolI4(cf, {}).src, 0)
+    st = glm53h.G53hStore()
+    check(L.g53h_store_synth_init(C.byref(st), sp.E, sp.I, 3, sp.NE, NP, sp.seed, C.c_float(sp.expert_sigma)), "store")
+    try:
+        say("config 2 int4 through the cache")
+        c, sb = new_cache_i4(cf, st, 12, 2)
+        try:
+            assert sb == ref_i4_slot_bytes(sp) == 14155776
+            got = run(c.src, 6)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        finally:
+            L.glm53f_cache_free(C.byref(c))
+    finally:
+        L.g53h_store_synth_free(C.byref(st))

@@ -52,10 +52,10 @@ def test_stack_through_cache_with_misses(L):
     def run(slots, n_io, pf):
         cache = glm53h.Glm53fCache()
         probe = glm53h.Glm53fCache()
-        assert L.g53h_cache_init_store(C.byref(probe), C.byref(store), C.byref(cf), 1 << 30, 0) == 0
+        assert L.g53h_cache_init_store(C.byref(probe), C.byref(store), C.byref(cf), 1 << 30, 0, 0) == 0
         sb = probe.slot_bytes
         L.glm53f_cache_free(C.byref(probe))
-        assert L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), sb * slots, n_io) == 0
+        assert L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), sb * slots, n_io, 0) == 0
         outs = np.zeros((STEPS, NL, sp.E), np.float32)
         try:
             for t in range(STEPS):
