@@ -127,20 +127,22 @@ def cpu_baseline(layer, x, idx_all, seconds):
     mats = {e: layer.fetch_expert(e) for e in need}
     sh = layer.fetch_expert("shared")
     R = O.ref()
+    moe = O.moe_i4 if layer.i4 else O.moe             # int4 layers: the reference's int4 experts
     for i in range(3):
-        O.moe(R, x[toks[i % 4]:toks[i % 4] + 1], sp, layer.router_f32, layer.bias_f32, mats, sh)
+        moe(R, x[toks[i % 4]:toks[i % 4] + 1], sp, layer.router_f32, layer.bias_f32, mats, sh)
     times, t_end = [], time.perf_counter() + seconds
     while time.perf_counter() < t_end or len(times) < 20:
         t = toks[len(times) % len(toks)]
         t0 = time.perf_counter()
-        O.moe(R, x[t:t + 1], sp, layer.router_f32, layer.bias_f32, mats, sh)
+        moe(R, x[t:t + 1], sp, layer.router_f32, layer.bias_f32, mats, sh)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     threads = host_cpu()["omp_threads"]
     return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "host": host_cpu(), "kind": "reference",
             "sample": f"reference glm53f_moe (src/core/glm53f_ops.c) compiled -O3 -mavx2 -mfma -fopenmp "
                       f"-ffp-contract=off, OpenMP threads {threads}; config-2 decode of 4 seeded tokens cycled, "
-                      f"3 warm-up + median of {len(times)} calls ({sum(times):.1f} s), experts in host RAM",
+                      f"3 warm-up + median of {len(times)} calls ({sum(times):.1f} s), experts in host RAM"
+                      + (", routed experts int4 (GLM53F_WI4)" if layer.i4 else ""),
             "gbps": round(layer.algorithmic_bytes(sp.K) / med / 1e9, 2)}
 
 
@@ -528,6 +530,9 @@ def main():
                          "200 GB cache, which isolates the per-layer cost from host reads)")
     ap.add_argument("--layout", default="tiled", choices=["tiled", "rowmajor"],
                     help="expert code layout in HBM (config 2): octet-tiled (k_dec_tiled) or row-major (k_dec_layer)")
+    ap.add_argument("--experts", default="fp8", choices=["fp8", "int4"],
+                    help="config 2: routed experts as the checkpoint's FP8 (the metric) or re-quantised to the "
+                         "reference's int4 format (its --experts int4 mode; the row-wave kernels)")
     a = ap.parse_args()
     if a.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (expert-parallel "
@@ -540,9 +545,10 @@ def main():
         return bench_stack(a)
     L = glm53h.init(0)
     sp = S.spec(2)
-    tiled = a.layout == "tiled"
-    kname = "k_dec_tiled" if tiled else "k_dec_layer"
-    layer = S.DeviceLayer.build(sp, tiled=tiled)
+    i4 = a.experts == "int4"
+    tiled = a.layout == "tiled" and not i4
+    kname = "k_slot_rows" if i4 else ("k_dec_tiled" if tiled else "k_dec_layer")
+    layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4)
     cp = Copies(layer)
     x = S.x_host(sp, NTOK, batch=0)
     xs = DevBuf.from_array(x)
@@ -572,7 +578,8 @@ def main():
     cnt = (C.c_int * 8)()
     check(L.g53h_prof_collect(tms, cnt, 8), "collect")
     check(L.g53h_prof_enable(0), "prof")
-    per = {name: (tms[i] / cnt[i] * 1e3 if cnt[i] else None) for i, name in [(7, kname + "_us")]}
+    tags = [(1, "router_us"), (4, "row_kernels_us"), (6, "combine_us")] if i4 else [(7, kname + "_us")]
+    per = {name: (tms[i] / cnt[i] * 1e3 if cnt[i] else None) for i, name in tags}
     errs = L.g53h_decode_errors()
     if errs:
         sys.exit(f"the decode kernels reported error flags {errs}")
@@ -586,6 +593,11 @@ def main():
     # per-step time is the kernel's average duration (the per-kernel events of the separate
     # profiled run add a gap after every launch and are reported beside it)
     dom_us = us_layer
+    if i4:
+        # int4: the three row-wave launches (gate, up, down of 8 int4 experts + the FP8 shared
+        # expert) with the SwiGLU between them, timed together by the profiled run's events
+        dom_bytes = sp.K * sp.expert_i4_bytes() + eb
+        dom_us = per["row_kernels_us"]
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
@@ -609,7 +621,8 @@ def main():
         "data": "synthetic (seeded FP8 E4M3 experts N(0,0.02) absmax-quantised per 128x128 block; bf16 x ~N(0,1))",
         "config": {"workload": "BASELINE config 2: single-token decode of one MoE layer, hidden 4096, "
                                "moe_inter 2048, 288 experts resident in HBM, top-8 + 1 shared",
-                   "tokens_cycled": NTOK, "router_shared_copies": NCOPY, "expert_layout": a.layout,
+                   "tokens_cycled": NTOK, "router_shared_copies": NCOPY,
+                   "expert_layout": "int4 row-major" if i4 else a.layout, "routed_experts": a.experts,
                    "parallelism": "single GPU"},
         "hbm_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),

@@ -6,10 +6,10 @@
 
 #define GLM53F_MAX_TOPK_DEV 64
 
-/* y [T][nslots][rows] = matrix `which` (0 gate, 1 up, 2 down) of slots[t][s] times x (per
- * token, or per (token, slot) when x_per_slot) by the row-wave kernel (any FP8 geometry, int4). */
-int g53h_slot_rows(float *y, const float *x, int T, int nslots, const G53hExpert *slots, int which, int rows,
-                   int cols, int x_per_slot);
+/* The experts of a layer by the row-wave kernels (int4, and FP8 of any geometry): act [T][nslots][I]
+ * = swiglu(gate . x, up . x), contrib [T][nslots][E] = down . act, for descriptors slots [T][nslots]. */
+int g53h_rows_layer(float *contrib, float *act, const float *x, int T, int nslots, const G53hExpert *slots, int E,
+                    int I, float limit);
 int g53h_combine_into(float *out, const float *contrib, const float *wts, int T, int E, int K, int nslots);
 int g53h_resolve_slots(G53hExpert *slots, const G53hExpert *experts, const int *idx, const G53hExpert *shared,
                        int T, int K);

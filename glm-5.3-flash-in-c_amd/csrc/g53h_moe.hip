@@ -275,12 +275,7 @@ static int g53_layer_body(float *out, const float *x, int T, const G53hMoeLayer 
         return 0;
     }
     /* int4 experts and any other shape: the row-wave kernels, same arithmetic */
-    float *g = (float *)(ws + align256((size_t)T * nslots * I * sizeof(float)));
-    float *u = g + (size_t)T * nslots * I;
-    if (g53h_slot_rows(g, x, T, nslots, slots, 0, I, E, 0)) return -1;
-    if (g53h_slot_rows(u, x, T, nslots, slots, 1, I, E, 0)) return -1;
-    if (g53h_swiglu_split(act, g, u, (long)T * nslots * I, L->swiglu_limit)) return -1;
-    if (g53h_slot_rows(contrib, act, T, nslots, slots, 2, E, I, 1)) return -1;
+    if (g53h_rows_layer(contrib, act, x, T, nslots, slots, E, I, L->swiglu_limit)) return -1;
     g53h_prof_mark(G53_PROF_GENERIC);
     if (!fused) return 0;
     return g53h_combine_into(out, contrib, wts, T, E, K, nslots);

@@ -8,6 +8,10 @@
 
 #include "g53h_core.h"
 
+/* E4M3FN code -> float by the gfx950 conversion instruction (exact; 0x7f / 0xff give NaN, as
+ * g53_e4m3_to_f32 and the reference's table). */
+__device__ __forceinline__ static float g53_e4m3_hw(uint8_t b) { return __builtin_amdgcn_cvt_f32_fp8((int)b, 0); }
+
 /* The reference's per-block arithmetic (src/core/glm53f_ops.c:195-227): eight fp32 lanes of
  * fused products stepping by 8 columns, reduced in double by a fixed tree, the block tail
  * added in double, the block sum scaled in double and accumulated over blocks in order. */
@@ -16,10 +20,10 @@ __device__ __forceinline__ static double g53_block_dot(const uint8_t *row, const
     float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int j = j0;
     for (; j + 8 <= j1; j += 8)
-        for (int l = 0; l < 8; l++) a[l] = __builtin_fmaf(g53_e4m3_to_f32(row[j + l]), x[j + l], a[l]);
+        for (int l = 0; l < 8; l++) a[l] = __builtin_fmaf(g53_e4m3_hw(row[j + l]), x[j + l], a[l]);
     double bsum = (((double)a[0] + a[4]) + ((double)a[2] + a[6]))
                 + (((double)a[1] + a[5]) + ((double)a[3] + a[7]));
-    for (; j < j1; j++) bsum += (double)g53_e4m3_to_f32(row[j]) * (double)x[j];
+    for (; j < j1; j++) bsum += (double)g53_e4m3_hw(row[j]) * (double)x[j];
     return bsum;
 }
 

@@ -186,15 +186,18 @@ class DeviceLayer:
                     mats.append(G53hMat(q, st, r, c, 1, 64, c // 64, 4))
                 descs[i] = G53hExpert(*mats)
                 continue
+            # an int4 layer keeps its FP8 shared expert octet-tiled where the shapes allow (the
+            # row-wave kernel's fast FP8 path), as the drop-in does
+            tile = self.tiled or (self.i4 and sp.bc == 128 and all(r % 8 == 0 and c % 128 == 0 for r, c in shapes))
             for m, (r, c) in enumerate(shapes):
                 strm = stream(K_SHARED, sp.layer, m) if i == NE else stream(K_EXPERT, sp.layer, i * 3 + m)
                 w, s = base + code_off[m], base + sc_off[m]
-                gen = stage.ptr if self.tiled else w
+                gen = stage.ptr if tile else w
                 check(L.g53h_synth_f8(gen, s, r, c, sp.br, sp.bc, sp.seed, strm, C.c_float(sp.expert_sigma)),
                       "g53h_synth_f8")
-                if self.tiled:
+                if tile:
                     check(L.g53h_tile_f8(w, gen, r, c), "g53h_tile_f8")
-                mats.append(G53hMat(w, s, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, 2 if self.tiled else 0))
+                mats.append(G53hMat(w, s, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, 2 if tile else 0))
             descs[i] = G53hExpert(*mats)
         self.experts = descs
         self.table = DevBuf.from_array(np.frombuffer(bytes(descs), np.uint8))

@@ -612,6 +612,15 @@ void g53h_host_prof(double *out) { for (int i = 0; i < 16; i++) out[i] = g_hp_n 
 #define HP(i) do { } while (0)
 #endif
 
+/* The shared expert can be kept octet-tiled: FP8 with 128-column blocks, whole row octets. */
+static int shared_tileable(const Glm53fMoeW *w)
+{
+    const Glm53fMat *ms[3] = {&w->sh_gate, &w->sh_up, &w->sh_down};
+    for (int i = 0; i < 3; i++)
+        if (ms[i]->dt != GLM53F_WF8 || ms[i]->bc != 128 || ms[i]->rows % 8 || ms[i]->cols % 128) return 0;
+    return 1;
+}
+
 static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int with_shared)
 {
     const int E = c->hidden, K = c->topk, NE = c->n_experts;
@@ -674,7 +683,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     HP(2);
     /* the chosen experts' views (slot order), the shared expert after them */
     G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
-    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1;
+    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1, i4r = 1;
     memset(tab, 0, (size_t)(K + 1) * sizeof(G53hExpert));
     for (int j = 0; j < K; j++) {
         Glm53fExpertQ q;
@@ -692,13 +701,14 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         tab[j].up = view_mat_f8(&q.up);
         tab[j].down = view_mat_f8(&q.down);
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_TILED)) tiled = 0;
+        if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4)) i4r = 0;
     }
+    if (!nh) i4r = 0;
     HP(3);
     if (with_shared) {
         /* the shared expert resident in the layout of the routed slots */
-        const int tile_ok = tiled && w->sh_gate.dt == GLM53F_WF8 && w->sh_up.dt == GLM53F_WF8 &&
-                            w->sh_down.dt == GLM53F_WF8 && w->sh_gate.rows % 8 == 0 && w->sh_gate.cols % 128 == 0 &&
-                            w->sh_down.rows % 8 == 0 && w->sh_down.cols % 128 == 0;
+        /* (int4 routed experts: the row-wave kernel's fast FP8 path reads it octet-tiled too) */
+        const int tile_ok = (tiled || i4r) && shared_tileable(w);
         if (tile_ok) {
             tab[K].gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
             tab[K].up = dev_mat_resident_tiled(&w->sh_up, "shared up");
@@ -709,6 +719,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
             tab[K].down = dev_mat_resident(&w->sh_down, "shared down");
             tiled = 0;
         }
+        if (i4r) tiled = 0;
     }
     G53hMoeLayer L;
     memset(&L, 0, sizeof L);
@@ -919,7 +930,7 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
         if (gn > 0 && !prefetch && src->getmany) src->getmany(src, w->layer, uniq + g0, gn);
         for (int b0 = g0; b0 < g0 + gn || (first && with_shared); b0 += B) {
             const int bn = (g0 + gn - b0) < B ? (g0 + gn - b0) : B;
-            int nh = 0, block_c = 128;
+            int nh = 0, block_c = 128, any_i4 = 0;
             memset(table, 0, (size_t)NE * sizeof(G53hExpert));
             for (int u = b0; u < b0 + bn; u++) {
                 const int e = uniq[u];
@@ -933,9 +944,8 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                     continue;
                 }
                 check_expert_shape(&q, c, w->layer, e);
-                if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128 || q.gate.dt == GLM53F_WI4 ||
-                    q.up.dt == GLM53F_WI4 || q.down.dt == GLM53F_WI4)
-                    block_c = 0;
+                if (q.gate.dt == GLM53F_WI4 || q.up.dt == GLM53F_WI4 || q.down.dt == GLM53F_WI4) any_i4 = 1;
+                if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128 || any_i4) block_c = 0;
                 const size_t need = expert_stage_bytes(&q);
                 const int dev = g53h_is_device_ptr(q.gate.w);
                 uint8_t *dst = (!dev || q.gate.dt == GLM53F_WF8T || q.up.dt == GLM53F_WF8T || q.down.dt == GLM53F_WF8T) ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
@@ -957,9 +967,15 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
             L.shared = NULL;
             if (with_shared && first) {              /* the shared expert rides with the first batch */
                 G53hExpert sh;
-                sh.gate = dev_mat_resident(&w->sh_gate, "shared gate");
-                sh.up = dev_mat_resident(&w->sh_up, "shared up");
-                sh.down = dev_mat_resident(&w->sh_down, "shared down");
+                if (any_i4 && shared_tileable(w)) {  /* the row-wave kernel's fast FP8 path */
+                    sh.gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
+                    sh.up = dev_mat_resident_tiled(&w->sh_up, "shared up");
+                    sh.down = dev_mat_resident_tiled(&w->sh_down, "shared down");
+                } else {
+                    sh.gate = dev_mat_resident(&w->sh_gate, "shared gate");
+                    sh.up = dev_mat_resident(&w->sh_up, "shared up");
+                    sh.down = dev_mat_resident(&w->sh_down, "shared down");
+                }
                 if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128 ||
                     sh.gate.flags || sh.up.flags || sh.down.flags)
                     block_c = 0;

@@ -56,7 +56,7 @@ int         g53h_mem_info(size_t *free_b, size_t *total_b);
  *
  * Code layouts (flags bit G53H_MAT_TILED):
  *   row-major   w[r * cols + c];
- *   octet-tiled (rows a multiple of 8, cols of 128, 128 x 128 blocks): the matrix is cut into
+ *   octet-tiled (rows a multiple of 8, cols of 128, 128-column blocks): the matrix is cut into
  *               units of 8 rows x 128 columns (1 KB), stored unit (r / 8, c / 128) at byte
  *               ((r / 8) * (cols / 128) + c / 128) * 1024, so one row octet's units follow
  *               each other. Inside a unit, row r % 8 holds 128 bytes: eight 16-byte runs, run
@@ -156,7 +156,8 @@ typedef struct {
                                        octet-tiled layout (G53H_MAT_TILED), 0: row-major     */
     /* Experts in the int4 format (G53H_MAT_I4, per matrix) need block_c = 0 and tiled = 0: the
        row-wave kernels then take them (and any FP8 matrix, such as the shared expert, in the
-       same layer), exactly as glm53f_mm on a GLM53F_WI4 matrix. */
+       same layer; an octet-tiled one streams fastest), exactly as glm53f_mm on a GLM53F_WI4
+       matrix. */
 } G53hMoeLayer;
 
 /* Whole MoE layer on the device (replaces src/core/glm53f_ops.c:1144-1342 moe_chunk with

@@ -115,6 +115,20 @@ def test_i4_matvec_known_answer_cases(L):
     L.glm53f_forget_host_weights()
 
 
+def test_dropin_mm_on_tiled_views(L):
+    """glm53f_mm on an octet-tiled host matrix (GLM53F_WF8T, the HBM cache's view layout)
+    equals the row-major product: the unit operation converts the layout first."""
+    c = O.fp8_kat_cases()[0]
+    t = np.empty_like(c["w"])
+    assert L.g53h_tile_f8_host(t.ctypes.data, c["w"].ctypes.data, c["rows"], c["cols"], 0) == 0
+    m = fmat(t, c["s"], c["rows"], c["cols"], c["br"], c["bc"])
+    m.dt = glm53h.GLM53F_WF8T
+    y = np.zeros(c["rows"], np.float32)
+    L.glm53f_mm(y.ctypes.data, c["x"].ctypes.data, C.byref(m))
+    gold = np.load(os.path.join(HERE, "golden", "golden.npz"))["kat_y0"]
+    assert same(y, gold)
+
+
 # --------------------------------------------------------------------- layer ----
 def test_layer_i4_config1(L):
     sp = S.spec(1)
