@@ -3,7 +3,7 @@
  *
  *   k_rows_gateup   gate and up rows and their SwiGLU, k_rows_down the down rows, for the
  *                   (token, slot) pairs of a MoE layer: one one-wave workgroup per (token,
- *                   slot) and 8 rows of gate and up (16 rows of down). Every lane computes the
+ *                   slot) and 4 rows of gate and up (8 rows of down). Every lane computes the
  *                   reference's sum of one column group of one row (the eight fp32 lanes, the
  *                   double tree, the tail) times its scale in double; the row's groups are then
  *                   added in order by one lane per row from LDS, as the reference's loop over
@@ -28,9 +28,12 @@
 #define G53_RW_LD    65                 /* LDS row stride of the partials (doubles) */
 
 typedef unsigned int g53_v4u __attribute__((ext_vector_type(4)));
+#ifndef G53_RW_RB
+#define G53_RW_RB 4                     /* octet-tiled rows whose 16-byte runs are loaded together */
+#endif
 
 /* One group of 64 int4 columns (32 bytes c0, c1) against 64 activations xr: the reference's
- * eight lanes stepping by 8 columns, then the double tree. */
+ * eight lanes stepping by 8 columns (src/core/glm53f_ops.c:247-282), then the double tree. */
 __device__ __forceinline__ double g53_i4_group64(const g53_v4u &c0, const g53_v4u &c1, const float (&xr)[64])
 {
     const uint32_t d[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
@@ -128,10 +131,11 @@ __device__ __forceinline__ double g53_pass(const G53hMat &m, const float *__rest
                     const int b = st * 8 + j;
                     xr[st * 16 + k] = b < nbc ? xt[(c0 + b) * 128 + l + 8 * k] : 0.0f;
                 }
-            for (int r4 = 0; r4 < NR; r4 += 4) {
-                g53_v4u c[4][4];                                   /* 4 rows' runs in flight */
+            constexpr int RB = NR < G53_RW_RB ? NR : G53_RW_RB;  /* rows whose runs are in flight */
+            for (int r4 = 0; r4 < NR; r4 += RB) {
+                g53_v4u c[RB][4];
 #pragma unroll
-                for (int i = 0; i < 4; i++)
+                for (int i = 0; i < RB; i++)
 #pragma unroll
                     for (int st = 0; st < 4; st++) {
                         const int r = row0 + r4 + i, b = st * 8 + j;
@@ -142,7 +146,7 @@ __device__ __forceinline__ double g53_pass(const G53hMat &m, const float *__rest
                             c[i][st] = g53_v4u{0, 0, 0, 0};
                     }
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < RB; i++) {
                     const int r = row0 + r4 + i;
                     const float *srow = m.s + (size_t)(r / m.br) * nb + c0;
 #pragma unroll
@@ -235,26 +239,60 @@ __device__ __forceinline__ bool g53_rows_ok(const G53hMat &m)
     return m.bc == 128 && m.cols == 128 * m.scols && (m.rows & 7) == 0 && ((uintptr_t)m.w & 15) == 0;
 }
 
-#define G53_GU_ROWS 8                   /* gate rows (and as many up rows) per wave */
-#define G53_DN_ROWS 16                  /* down rows per wave                      */
+/* Sizes measured on MI355X (config-2 int4 decode): one wave per workgroup, 4 gate rows (and 4
+ * up rows) or 8 down rows per wave keep the kernels at 3 waves per SIMD for the down rows and 2
+ * for gate/up; 8-wave workgroups, or 8 gate / 16 down rows per wave, were slower. */
+#ifndef G53_RW_NW
+#define G53_RW_NW 1                     /* waves per workgroup, each with rows of its own */
+#endif
+#ifndef G53_GU_ROWS
+#define G53_GU_ROWS 4                   /* gate rows (and as many up rows) per wave */
+#endif
+#ifndef G53_DN_ROWS
+#define G53_DN_ROWS 8                   /* down rows per wave                      */
+#endif
 
-/* Gate, up and SwiGLU: (token, slot) pair blockIdx.y = t * nslots + s of descriptors slots[]
- * times x [T][E]; act [T][nslots][I] = swiglu_clamp(gate row, up row). One wave (one
- * workgroup) per 8 rows of both matrices, lanes 0-7 summing the gate rows and 8-15 the up rows;
- * with int4 experts every load of both matrices is issued before any is used. A descriptor with
- * gate.w NULL is absent from this call (nothing written) unless marked dropped (zeros). */
-__global__ void __launch_bounds__(64)
+/* blockIdx.y = t * (nslots + 1) + r -> (token t, slot s, half h): r = 0 and 1 are the two halves
+ * of the last slot, r >= 2 slot nslots - r, whole. The last slot is the shared expert when there
+ * is one (FP8, twice the bytes of an int4 expert): dispatched first, it overlaps the routed
+ * experts instead of trailing them, and octet-tiled it is split over two workgroups so that
+ * no workgroup carries more bytes than an int4 one. Any other matrix takes half 0 whole (its
+ * half 1 workgroup exits at once). */
+__device__ __forceinline__ void g53_rows_slot(int nslots, int &t, int &s, int &h)
+{
+    const int per = nslots + 1, r = (int)(blockIdx.y % per);
+    t = (int)(blockIdx.y / per);
+    s = r <= 1 ? nslots - 1 : nslots - r;
+    h = r <= 1 ? r : 0;
+}
+
+__device__ __forceinline__ bool g53_split(const G53hMat &m)
+{
+    return !(m.flags & G53H_MAT_I4) && (m.flags & G53H_MAT_TILED);
+}
+
+/* Gate, up and SwiGLU for (token, slot) of descriptors slots [T][nslots] times x [T][E]:
+ * act [T][nslots][I] = swiglu_clamp(gate row, up row). One wave per G53_GU_ROWS rows of both
+ * matrices (half as many for a split octet-tiled slot), lanes 0-3 summing the gate rows and 4-7 the
+ * up rows; with int4 experts every load of both matrices is issued before any is used. A
+ * descriptor with gate.w NULL is absent from this call (nothing written) unless marked dropped
+ * (zeros). */
+__global__ void __launch_bounds__(64 * G53_RW_NW)
 k_rows_gateup(float *__restrict__ act, const float *__restrict__ x, int nslots, const G53hExpert *__restrict__ slots,
               int I, int E, float limit)
 {
-    __shared__ double buf[2 * G53_GU_ROWS * G53_RW_LD];
-    /* slots in reverse order: the shared expert (the last slot, FP8, twice the bytes of an int4
-     * expert) is dispatched first and overlaps the routed experts instead of trailing them */
-    const int t = blockIdx.y / nslots, ts = t * nslots + (nslots - 1 - (int)(blockIdx.y % nslots)), lane = threadIdx.x;
-    const int row0 = blockIdx.x * G53_GU_ROWS;
+    __shared__ double bufs[G53_RW_NW][2 * G53_GU_ROWS * G53_RW_LD];
+    int t, s, h;
+    g53_rows_slot(nslots, t, s, h);
+    const int ts = t * nslots + s, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    double *buf = bufs[wv];
     const G53hExpert &e = slots[ts];
+    const bool split = e.gate.w && g53_split(e.gate) && g53_split(e.up);
+    if (h && !split) return;
+    const int nr = split ? G53_GU_ROWS / 2 : G53_GU_ROWS, row0 = (blockIdx.x * G53_RW_NW + wv) * G53_GU_ROWS + h * nr;
+    if (row0 >= I) return;
     float *at = act + (size_t)ts * I;
-    const bool write = lane < G53_GU_ROWS && row0 + lane < I;
+    const bool write = lane < nr && row0 + lane < I;
     if (!e.gate.w) {
         if ((e.gate.flags & G53H_MAT_DROPPED) && write) at[row0 + lane] = 0.0f;
         return;
@@ -297,6 +335,9 @@ k_rows_gateup(float *__restrict__ act, const float *__restrict__ x, int nslots, 
                     g53_i4_group64(c0[k], c1[k], xr) * (double)stp[k];
         }
         acc = g53_chain(buf, ng, lane, 0, 2 * G53_GU_ROWS, acc);
+    } else if (split) {
+        acc = g53_pass<G53_GU_ROWS / 2>(g, xt, row0, I, buf, 0, lane, acc);
+        acc = g53_pass<G53_GU_ROWS / 2>(u, xt, row0, I, buf, G53_GU_ROWS, lane, acc);
     } else {
         acc = g53_pass<G53_GU_ROWS>(g, xt, row0, I, buf, 0, lane, acc);
         acc = g53_pass<G53_GU_ROWS>(u, xt, row0, I, buf, G53_GU_ROWS, lane, acc);
@@ -305,17 +346,24 @@ k_rows_gateup(float *__restrict__ act, const float *__restrict__ x, int nslots, 
     if (write) at[row0 + lane] = g53_swiglu1((float)acc, (float)au, limit);
 }
 
-/* Down: y [T][nslots][E] = down(slot) . act [T][nslots][I], one wave per 16 rows. */
-__global__ void __launch_bounds__(64)
+/* Down: y [T][nslots][E] = down(slot) . act [T][nslots][I], one wave per G53_DN_ROWS rows (half for a split
+ * octet-tiled slot; the slot order of k_rows_gateup). */
+__global__ void __launch_bounds__(64 * G53_RW_NW)
 k_rows_down(float *__restrict__ y, const float *__restrict__ act, int nslots, const G53hExpert *__restrict__ slots,
             int E, int I)
 {
-    __shared__ double buf[G53_DN_ROWS * G53_RW_LD];
-    const int t = blockIdx.y / nslots, ts = t * nslots + (nslots - 1 - (int)(blockIdx.y % nslots)), lane = threadIdx.x;
-    const int row0 = blockIdx.x * G53_DN_ROWS;
+    __shared__ double bufs[G53_RW_NW][G53_DN_ROWS * G53_RW_LD];
+    int t, s, h;
+    g53_rows_slot(nslots, t, s, h);
+    const int ts = t * nslots + s, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    double *buf = bufs[wv];
     const G53hExpert &e = slots[ts];
+    const bool split = e.gate.w && g53_split(e.down);
+    if (h && !split) return;
+    const int nr = split ? G53_DN_ROWS / 2 : G53_DN_ROWS, row0 = (blockIdx.x * G53_RW_NW + wv) * G53_DN_ROWS + h * nr;
+    if (row0 >= E) return;
     float *yt = y + (size_t)ts * E;
-    const bool write = lane < G53_DN_ROWS && row0 + lane < E;
+    const bool write = lane < nr && row0 + lane < E;
     if (!e.gate.w) {
         if ((e.gate.flags & G53H_MAT_DROPPED) && write) yt[row0 + lane] = 0.0f;
         return;
@@ -325,7 +373,9 @@ k_rows_down(float *__restrict__ y, const float *__restrict__ act, int nslots, co
         if (write) yt[row0 + lane] = __builtin_nanf("");
         return;
     }
-    const double a = g53_pass<G53_DN_ROWS>(d, act + (size_t)ts * I, row0, E, buf, 0, lane, 0.0);
+    const float *xt = act + (size_t)ts * I;
+    const double a = split ? g53_pass<G53_DN_ROWS / 2>(d, xt, row0, E, buf, 0, lane, 0.0)
+                           : g53_pass<G53_DN_ROWS>(d, xt, row0, E, buf, 0, lane, 0.0);
     if (write) yt[row0 + lane] = (float)a;
 }
 
@@ -333,12 +383,14 @@ int g53h_rows_layer(float *contrib, float *act, const float *x, int T, int nslot
                     int I, float limit)
 {
     if (T <= 0 || nslots <= 0) return 0;
-    if ((long)T * nslots > 65535) return g53h_fail("g53h_rows_layer: %d (token, slot) pairs", T * nslots);
-    hipLaunchKernelGGL(k_rows_gateup, dim3((unsigned)((I + G53_GU_ROWS - 1) / G53_GU_ROWS), (unsigned)(T * nslots)),
-                       dim3(64), 0, g53h_stream(), act, x, nslots, slots, I, E, limit);
+    if ((long)T * (nslots + 1) > 65535) return g53h_fail("g53h_rows_layer: %d (token, slot) pairs", T * nslots);
+    const unsigned ny = (unsigned)(T * (nslots + 1));
+    const int gu = G53_GU_ROWS * G53_RW_NW, dn = G53_DN_ROWS * G53_RW_NW;
+    hipLaunchKernelGGL(k_rows_gateup, dim3((unsigned)((I + gu - 1) / gu), ny), dim3(64 * G53_RW_NW), 0,
+                       g53h_stream(), act, x, nslots, slots, I, E, limit);
     G53_LAUNCHED("k_rows_gateup");
-    hipLaunchKernelGGL(k_rows_down, dim3((unsigned)((E + G53_DN_ROWS - 1) / G53_DN_ROWS), (unsigned)(T * nslots)),
-                       dim3(64), 0, g53h_stream(), contrib, act, nslots, slots, E, I);
+    hipLaunchKernelGGL(k_rows_down, dim3((unsigned)((E + dn - 1) / dn), ny), dim3(64 * G53_RW_NW), 0,
+                       g53h_stream(), contrib, act, nslots, slots, E, I);
     G53_LAUNCHED("k_rows_down");
     return 0;
 }
