@@ -547,7 +547,7 @@ def main():
     sp = S.spec(2)
     i4 = a.experts == "int4"
     tiled = a.layout == "tiled" and not i4
-    kname = "k_slot_rows" if i4 else ("k_dec_tiled" if tiled else "k_dec_layer")
+    kname = "k_rows" if i4 else ("k_dec_tiled" if tiled else "k_dec_layer")
     layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4)
     cp = Copies(layer)
     x = S.x_host(sp, NTOK, batch=0)
@@ -602,7 +602,7 @@ def main():
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
     traffic = None                      # HBM bytes per launch from the committed counter summary
-    tp = os.path.join(ROOT, "profiles", f"{kname}_config2_traffic.json")
+    tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 else ''}_traffic.json")
     if os.path.exists(tp):
         with open(tp) as f:
             traffic = json.load(f).get("traffic_bytes")
@@ -628,7 +628,8 @@ def main():
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes_per_layer": layer_bytes,
         "kernels_us": {k: (round(v, 2) if v else v) for k, v in per.items()},
-        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(dom_gbps, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_rows_gateup + k_rows_down" if i4 else kname,
+                     "achieved": round(dom_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 2)},
         "cpu_baseline": cpu,
