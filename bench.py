@@ -197,7 +197,7 @@ def bench_grouped(a):
     T = 64 if cfg == 3 else 2048
     steps = a.steps if a.steps != 400 else (200 if cfg == 3 else 30)
     warm = a.warmup if a.warmup != 50 else 5
-    layer = S.DeviceLayer.build(sp)
+    layer = S.DeviceLayer.build(sp, tiled=a.layout == "tiled")
     nb = 4
     xs = [S.x_host(sp, T, batch=b) for b in range(nb)]
     xd = [DevBuf.from_array(x) for x in xs]
@@ -253,7 +253,7 @@ def bench_grouped(a):
         "config": {"workload": (f"BASELINE config 3: batched decode, {T} tokens x top-8, Zipf(1.1) popularity"
                                 if cfg == 3 else f"BASELINE config 4: prefill, {T} tokens, uniform routing, + shared"),
                    "tokens": T, "token_batches_cycled": nb, "unique_routed_experts": D,
-                   "parallelism": "single GPU"},
+                   "expert_layout": a.layout, "parallelism": "single GPU"},
         "tokens_per_s": round(T / (ms * 1e-3), 1),
         "tflops": round(tflops, 2),
         "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
@@ -529,7 +529,8 @@ def main():
                     help="config 5: layers in the stack (42 is BASELINE's; fewer, e.g. 24, fit every expert in the "
                          "200 GB cache, which isolates the per-layer cost from host reads)")
     ap.add_argument("--layout", default="tiled", choices=["tiled", "rowmajor"],
-                    help="expert code layout in HBM (config 2): octet-tiled (k_dec_tiled) or row-major (k_dec_layer)")
+                    help="expert code layout in HBM: octet-tiled (the cache's slots; k_dec_tiled at config 2) or row-major "
+                         "(k_dec_layer at config 2)")
     ap.add_argument("--experts", default="fp8", choices=["fp8", "int4"],
                     help="config 2: routed experts as the checkpoint's FP8 (the metric) or re-quantised to the "
                          "reference's int4 format (its --experts int4 mode; the row-wave kernels)")

@@ -37,6 +37,12 @@
  * product. Here group g of step s covers bytes g*64 + s*32 .. +32 of a 128-byte scale block,
  * so a lane reads 64 consecutive bytes of its weight row per block. Result: lane l, register
  * r holds C[8*(r/4) + 4*(l/32) + r%4][l % 32].
+ *
+ * Octet-tiled layers (G53H_MAT_TILED, the HBM cache's slots): a row's 128 bytes of a block are
+ * the tiled unit's row, whose byte b holds column sigma(b / 16) + 8 (b % 16) of the block
+ * (include/g53h.h). The activation planes are then written in that same order within every
+ * 128-column block, so weight byte b meets activation byte b as before, and a wave's 32 rows of
+ * a block are four whole 1 KB units instead of 32 rows 4 KB apart.
  */
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -238,9 +244,30 @@ __device__ __forceinline__ void g53_split_planes(const float (&v)[4], uint32_t (
 
 /* Token t's row of x as NPX planes xq[p][t][E] with scale 2^k, k = 8 - exponent(absmax), so
  * every |x| * 2^k < 256; xinv[t] = 2^-k. Grid T, 256 threads, E a multiple of 16. */
+/* Byte position of column c of a 128-column block in the octet-tiled order: run sigma(c % 8)
+ * (sigma is its own inverse), element c / 8 of the run. */
+__device__ __forceinline__ int g53_grp_tpos(int c)
+{
+    const int a = c & 7;
+    return 16 * (((a & 1) << 2) | (a & 2) | (a >> 2)) + (c >> 3);
+}
+
+/* Four consecutive E4M3 codes (one word, column c0 .. c0 + 3 of a row) stored at dst: as they
+ * are, or (tiled) each at its octet-tiled position within its 128-column block. */
+__device__ __forceinline__ void g53_grp_st4(uint8_t *row, int c0, uint32_t q, int tiled)
+{
+    if (!tiled) {
+        *(uint32_t *)(row + c0) = q;
+        return;
+    }
+    uint8_t *blk = row + (c0 & ~127);
+#pragma unroll
+    for (int k = 0; k < 4; k++) blk[g53_grp_tpos((c0 + k) & 127)] = (uint8_t)(q >> (8 * k));
+}
+
 template <int NP>
 __global__ void __launch_bounds__(256)
-k_grp_xq(const float *__restrict__ x, int E, int T, uint8_t *__restrict__ xq, float *__restrict__ xinv)
+k_grp_xq(const float *__restrict__ x, int E, int T, uint8_t *__restrict__ xq, float *__restrict__ xinv, int tiled)
 {
     __shared__ float red[4];
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -265,7 +292,7 @@ k_grp_xq(const float *__restrict__ x, int E, int T, uint8_t *__restrict__ xq, fl
         uint32_t q[NP];
         g53_split_planes<NP>(s, q);
 #pragma unroll
-        for (int p = 0; p < NP; p++) *(uint32_t *)(xq + ((size_t)p * T + t) * E + i) = q[p];
+        for (int p = 0; p < NP; p++) g53_grp_st4(xq + ((size_t)p * T + t) * E, i, q[p], tiled);
     }
 }
 
@@ -340,12 +367,13 @@ struct G53GrpLd {
 };
 
 /* acc[h][r] += scale_r * (A_rows x B_tile-half-h), h < NH, over NKB blocks of 128 bytes.
- *   arow    this lane's weight row + (l / 32) * 64
+ *   arow    this lane's weight row + (l / 32) * 64 (block 0), kst bytes to the next block
+ *           (128 row-major, 1024 octet-tiled)
  *   s0, s1  scale rows for C registers 0-7 and 8-15 (one float per block)
  *   ld      this thread's slice loader; plane p of a source row at + p * xps
  *   NH      32-position halves the tile has (positions beyond the tile's count are padding) */
 template <int NW, int NP, int NKB, int NH>
-__device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const uint8_t *arow, const float *s0,
+__device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const uint8_t *arow, int kst, const float *s0,
                                               const float *s1, const G53GrpLd<NW> &ld, size_t xps, uint8_t *xs,
                                               int *flags, int &spin_err, int lane)
 {
@@ -373,7 +401,7 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const
     gptr xg[RPT];
 #pragma unroll
     for (int j = 0; j < RPT; j++) xg[j] = (gptr)ld.src[j];
-#define G53_LDA(sl, k) do { a[sl][0] = *(g53_gv8i *)(ag + (k) * 128); a[sl][1] = *(g53_gv8i *)(ag + (k) * 128 + 32); } while (0)
+#define G53_LDA(sl, k) do { a[sl][0] = *(g53_gv8i *)(ag + (size_t)(k) * kst); a[sl][1] = *(g53_gv8i *)(ag + (size_t)(k) * kst + 32); } while (0)
 #define G53_LDX(sl, k) do { _Pragma("unroll") for (int j = 0; j < RPT; j++) {                                  \
                                 xr[sl][j][0] = *(g53_gv4i *)(xg[j] + (k) * 128);                               \
                                 xr[sl][j][1] = *(g53_gv4i *)(xg[j] + xps + (k) * 128);                         \
@@ -439,10 +467,13 @@ __device__ __forceinline__ void g53_grp_kloop(g53_v16f (&acc)[G53_GRP_NH], const
 #undef G53_STX
 }
 
-/* A descriptor with the layout the grouped kernels assume. */
-__device__ __forceinline__ bool g53_grp_desc_ok(const G53hExpert &x, int E, int I)
+/* A descriptor with the layout the grouped kernels assume (octet-tiled iff the pass is). */
+__device__ __forceinline__ bool g53_grp_desc_ok(const G53hExpert &x, int E, int I, int tiled)
 {
+    const int want = tiled ? G53H_MAT_TILED : 0;
     return !((x.gate.flags | x.up.flags | x.down.flags) & G53H_MAT_I4) &&
+           (x.gate.flags & G53H_MAT_TILED) == want && (x.up.flags & G53H_MAT_TILED) == want &&
+           (x.down.flags & G53H_MAT_TILED) == want &&
            x.gate.br == 128 && x.gate.bc == 128 && x.gate.rows == I && x.gate.cols == E &&
            x.up.br == 128 && x.up.bc == 128 && x.up.rows == I && x.up.cols == E &&
            x.down.br == 128 && x.down.bc == 128 && x.down.rows == E && x.down.cols == I &&
@@ -463,6 +494,7 @@ struct G53GrpArgs {
     float *contrib;                /* [P][E]                                             */
     int T, P, E, I, NE;
     float limit, aq_scale, aq_inv;
+    int tiled;                     /* 1: experts octet-tiled, planes in the tiled column order */
     int partial;                   /* 1: experts without weights are outside this batch and
                                       left alone, unless marked dropped (gate.flags & G53H_MAT_DROPPED)    */
     int *ctr;                      /* [16] item counters: 0-7 gate/up, 8-15 down; each
@@ -525,7 +557,7 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
         if (threadIdx.x == 0) nxt = g53_grp_claim(ctr);
         G53_GTRACE(4, (uint64_t)__smid() << 32 | (uint32_t)(tl.y << 8 | tl.z));
         const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
-        const bool usable = ex && ex->gate.w != nullptr && g53_grp_desc_ok(*ex, a.E, a.I);
+        const bool usable = ex && ex->gate.w != nullptr && g53_grp_desc_ok(*ex, a.E, a.I, a.tiled);
         if (!usable) {                                       /* absent expert: down writes zeros */
             if (ex && ex->gate.w && threadIdx.x == 0) atomicOr(&a.meta_w[1], G53_GRP_EDESC);
             if (threadIdx.x == 0) claim[(kk + 1) & 1] = nxt;
@@ -545,7 +577,10 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
         const int i = lane & 31, g = lane >> 5;
         const int r0 = mb * 16 * NW + w * 16;                /* first intermediate row of the wave */
         const G53hMat &m = i < 16 ? ex->gate : ex->up;
-        const uint8_t *arow = m.w + (size_t)(r0 + (i & 15)) * a.E + g * 64;
+        const int wr = r0 + (i & 15);
+        const uint8_t *arow = a.tiled ? m.w + (size_t)(wr >> 3) * NKB * 1024 + (wr & 7) * 128 + g * 64
+                                      : m.w + (size_t)wr * a.E + g * 64;
+        const int kst = a.tiled ? 1024 : 128;
         const float *s0 = (const float *)ex->gate.s + (size_t)(r0 / 128) * ex->gate.scols;
         const float *s1 = (const float *)ex->up.s + (size_t)(r0 / 128) * ex->up.scols;
         g53_v16f acc[G53_GRP_NH] = {};
@@ -559,10 +594,10 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
         __syncthreads();
         int spin_err = 0;
         switch ((n + 31) >> 5) {
-        case 1: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 1>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
-        case 2: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 2>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
-        case 3: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 3>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
-        default: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 4>(acc, arow, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        case 1: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 1>(acc, arow, kst, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        case 2: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 2>(acc, arow, kst, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        case 3: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 3>(acc, arow, kst, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
+        default: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 4>(acc, arow, kst, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
         }
         if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
         G53_GTRACE(2, __builtin_amdgcn_s_memrealtime());
@@ -584,8 +619,7 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
                 g53_split_planes<G53_GRP_NPA>(v, pk);
                 const int row = r0 + q * 8 + g * 4;
 #pragma unroll
-                for (int p = 0; p < G53_GRP_NPA; p++)
-                    *(uint32_t *)(a.aq + ((size_t)p * a.P + pos) * a.I + row) = pk[p];
+                for (int p = 0; p < G53_GRP_NPA; p++) g53_grp_st4(a.aq + ((size_t)p * a.P + pos) * a.I, row, pk[p], a.tiled);
             }
         }
         G53_GTRACE(3, __builtin_amdgcn_s_memrealtime());
@@ -621,7 +655,7 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
             if (tid == 0) claim[(kk + 1) & 1] = nxt;
             continue;
         }
-        const bool ok = present && g53_grp_desc_ok(*ex, a.E, a.I);
+        const bool ok = present && g53_grp_desc_ok(*ex, a.E, a.I, a.tiled);
         if (!ok) {                                           /* zero contributions */
             for (int q = tid; q < n * (MR / 4); q += 64 * NW) {
                 const int j = q / (MR / 4), c = (q % (MR / 4)) * 4;
@@ -639,7 +673,10 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
         }
         const size_t xps = (size_t)a.P * a.I;
         const int r0 = mb * MR + w * 32;
-        const uint8_t *arow = ex->down.w + (size_t)(r0 + i) * a.I + g * 64;
+        const int wr = r0 + i;
+        const uint8_t *arow = a.tiled ? ex->down.w + (size_t)(wr >> 3) * NKB * 1024 + (wr & 7) * 128 + g * 64
+                                      : ex->down.w + (size_t)wr * a.I + g * 64;
+        const int kst = a.tiled ? 1024 : 128;
         const float *s0 = (const float *)ex->down.s + (size_t)(r0 / 128) * ex->down.scols;
         g53_v16f acc[G53_GRP_NH] = {};
         if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
@@ -647,10 +684,10 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_down(G53GrpArgs a)
         __syncthreads();
         int spin_err = 0;
         switch ((n + 31) >> 5) {
-        case 1: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 1>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
-        case 2: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 2>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
-        case 3: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 3>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
-        default: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 4>(acc, arow, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        case 1: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 1>(acc, arow, kst, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        case 2: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 2>(acc, arow, kst, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        case 3: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 3>(acc, arow, kst, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
+        default: g53_grp_kloop<NW, G53_GRP_NPA, NKB, 4>(acc, arow, kst, s0, s0, ld, xps, xs, flags, spin_err, lane); break;
         }
         if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
 #pragma unroll
@@ -784,7 +821,7 @@ static int g53_grp_plan_pass(const float *x, int tc, const G53hMoeLayer *L, cons
     hipLaunchKernelGGL(k_grp_plan, dim3(1), dim3(1024), lds, st, idx, tc, K, NE, hs, tok_of, pos_of, tiles, meta,
                        I / (16 * G53_GRP_NW), E / (32 * G53_GRP_NW));
     G53_LAUNCHED("k_grp_plan");
-    hipLaunchKernelGGL(k_grp_xq<G53_GRP_NPX>, dim3(tc), dim3(256), 0, st, x, E, tc, xq, xinv);
+    hipLaunchKernelGGL(k_grp_xq<G53_GRP_NPX>, dim3(tc), dim3(256), 0, st, x, E, tc, xq, xinv, L->tiled ? 1 : 0);
     G53_LAUNCHED("k_grp_xq");
     g53h_prof_mark(G53_PROF_GROUPED);
     float bound = L->swiglu_limit > 0.28f ? L->swiglu_limit : 0.28f;
@@ -797,6 +834,7 @@ static int g53_grp_plan_pass(const float *x, int tc, const G53hMoeLayer *L, cons
     a.T = tc; a.P = P; a.E = E; a.I = I; a.NE = NE;
     a.limit = L->swiglu_limit; a.aq_scale = ldexpf(1.0f, 8 - ex); a.aq_inv = ldexpf(1.0f, ex - 8);
     a.partial = 0;
+    a.tiled = L->tiled ? 1 : 0;
     a.trace = g_grp_trace;
     g_pass.active = 1; g_pass.tc = tc; g_pass.K = K; g_pass.hs = hs; g_pass.maxtiles = maxtiles;
     g_pass.pos_of = pos_of; g_pass.meta = meta; g_pass.contrib = contrib;
@@ -871,7 +909,6 @@ extern "C" int g53h_moe_grouped(float *out, const float *x, int T, const G53hMoe
 {
     if (g53h_ready()) return -1;
     if (!g53h_grouped_ok(L)) return g53h_fail("g53h_moe_grouped: layer shapes not supported");
-    if (L->tiled) return g53h_fail("g53h_moe_grouped: the grouped kernels read row-major expert codes, not octet-tiled");
     if (T < 0) return g53h_fail("g53h_moe_grouped: T %d", T);
     if (T == 0) return 0;
     const int K = L->topk, NE = L->n_experts;
@@ -932,7 +969,8 @@ extern "C" int g53h_grouped_begin(const float *x, int T, const G53hMoeLayer *L, 
 extern "C" int g53h_grouped_batch(const G53hMoeLayer *L)
 {
     if (!g_pass.active) return g53h_fail("g53h_grouped_batch: no pass begun");
-    if (L && L->tiled) return g53h_fail("g53h_grouped_batch: the grouped kernels read row-major expert codes, not octet-tiled");
+    if (L && (L->tiled ? 1 : 0) != g_pass.a.tiled)
+        return g53h_fail("g53h_grouped_batch: the pass was planned for %s experts", g_pass.a.tiled ? "octet-tiled" : "row-major");
     if (!L || L->n_experts != g_pass.a.NE || L->hidden != g_pass.a.E || L->inter != g_pass.a.I)
         return g53h_fail("g53h_grouped_batch: another layer than the pass's");
     if (L->shared && !g_pass.hs) return g53h_fail("g53h_grouped_batch: the pass was planned without a shared expert");

@@ -317,13 +317,14 @@ static int g53_check_layer(const G53hMoeLayer *L, int T)
     return 0;
 }
 
-/* Octet-tiled experts are read only by the single-token decode kernel k_dec_tiled (released
- * shapes); every other kernel assumes row-major codes, so any other case is refused. */
+/* Octet-tiled experts are read by the single-token decode kernel k_dec_tiled (released
+ * shapes) and the grouped kernels (T >= 2 where the grouped path takes the layer); the
+ * per-token kernels of this file assume row-major codes, so any other case is refused. */
 static int g53_tiled_refused(const char *fn, int T)
 {
     return g53h_fail("%s: octet-tiled experts are read only by the single-token decode kernel (T = 1, hidden %d, "
-                     "inter %d, 128x128 blocks, top-k <= 15, bf16 router or given routing); this call has T = %d",
-                     fn, 4096, 2048, T);
+                     "inter %d, 128x128 blocks, top-k <= 15, bf16 router or given routing) and the grouped kernels "
+                     "(T >= 2, grouped path on); this call has T = %d", fn, 4096, 2048, T);
 }
 
 extern "C" int g53h_moe_routed_given(float *out, const float *x, int T, const G53hMoeLayer *L,
@@ -377,8 +378,8 @@ extern "C" int g53h_moe(float *out, const float *x, int T, const G53hMoeLayer *L
                                : g53h_decode_fused(out, x, L, idx_out, w_out);
         if (r <= 0) return r;
     }
-    if (L->tiled) return g53_tiled_refused("g53h_moe", T);
     if (g53h_grouped_use(L, T)) return g53h_moe_grouped(out, x, T, L, idx_out, w_out);
+    if (L->tiled) return g53_tiled_refused("g53h_moe", T);
     const int K = L->topk, NE = L->n_experts;
     const size_t rsz = align256((size_t)2 * T * NE * 4), isz = align256((size_t)T * K * 4);
     const size_t ssz = g53_slots_bytes(L, T), csz = g53_contrib_bytes(L, T);

@@ -790,7 +790,9 @@ typedef struct { G53Buf b; } G53Slot;
 static G53Slot *g_hslots = NULL;
 static int g_nhslots = 0;
 
-static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off)
+/* A host view copied into the staging slot at dst + *off, its FP8 codes in the layout the
+ * chunk's kernels read (tiled != 0: octet-tiled, for a tiled grouped pass; else row-major). */
+static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off, int tiled)
 {
     G53hMat d;
     memset(&d, 0, sizeof d);
@@ -799,20 +801,23 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off)
     *off += (cb + 255) & ~(size_t)255;
     uint8_t *s = dst + *off;
     *off += (sb + 255) & ~(size_t)255;
-    if (m->dt == GLM53F_WF8T) {                 /* the chunk kernels read row-major codes */
+    const int is_t = m->dt == GLM53F_WF8T;
+    if (m->dt != GLM53F_WI4 && is_t != (tiled != 0)) {         /* convert on the way in */
         uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
-        if (g53h_h2d(t, m->w, cb) || g53h_untile_f8(w, t, m->rows, m->cols)) g53_die("copying a host expert to HBM");
+        if (g53h_h2d(t, m->w, cb) ||
+            (is_t ? g53h_untile_f8(w, t, m->rows, m->cols) : g53h_tile_f8(w, t, m->rows, m->cols)))
+            g53_die("copying a host expert to HBM");
     } else if (g53h_h2d(w, m->w, cb)) {
         g53_die("copying a host expert to HBM");
     }
     if (g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
     d.w = w; d.s = (const float *)s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
-    d.flags = m->dt == GLM53F_WI4 ? G53H_MAT_I4 : 0;
+    d.flags = m->dt == GLM53F_WI4 ? G53H_MAT_I4 : (tiled ? G53H_MAT_TILED : 0);
     return d;
 }
 
-/* Staging bytes of one expert's three matrices (stage_mat / rowmajor_view pad each part to 256). */
+/* Staging bytes of one expert's three matrices (stage_mat / chunk_view pad each part to 256). */
 static size_t expert_stage_bytes(const Glm53fExpertQ *q)
 {
     const Glm53fMat *ms[3] = {&q->gate, &q->up, &q->down};
@@ -822,17 +827,21 @@ static size_t expert_stage_bytes(const Glm53fExpertQ *q)
     return n;
 }
 
-/* An HBM view as the chunk kernels read it: row-major views as they are, octet-tiled ones
- * converted into the staging slot (ordered on the stream before the kernels that read it). */
-static G53hMat rowmajor_view(const Glm53fMat *m, uint8_t *dst, size_t *off)
+/* An HBM view as the chunk's kernels read it: in place when its FP8 layout is the one they read
+ * (tiled != 0: octet-tiled, else row-major), otherwise converted into the staging slot (ordered
+ * on the stream before the kernels that read it). Int4 views are used as they are. */
+static G53hMat chunk_view(const Glm53fMat *m, uint8_t *dst, size_t *off, int tiled)
 {
     G53hMat d = view_mat_f8(m);
-    if (m->dt != GLM53F_WF8T) return d;
+    const int is_t = m->dt == GLM53F_WF8T;
+    if (m->dt == GLM53F_WI4 || is_t == (tiled != 0)) return d;
     uint8_t *w = dst + *off;
     *off += (mat_code_bytes(m) + 255) & ~(size_t)255;
-    if (g53h_untile_f8(w, (const uint8_t *)m->w, m->rows, m->cols)) g53_die("converting a tiled expert view");
+    if (is_t ? g53h_untile_f8(w, (const uint8_t *)m->w, m->rows, m->cols)
+             : g53h_tile_f8(w, (const uint8_t *)m->w, m->rows, m->cols))
+        g53_die("converting an expert view");
     d.w = w;
-    d.flags = 0;
+    d.flags = tiled ? G53H_MAT_TILED : 0;
     return d;
 }
 
@@ -925,6 +934,10 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
     float *contrib = NULL;
     int held[GLM53F_MAX_TOPK];
     int first = 1;
+    /* the FP8 layout the chunk's kernels read: octet-tiled when a grouped pass is possible and
+     * the first expert view is tiled (the HBM cache's slots: used in place) and the shared
+     * expert can be kept tiled; row-major otherwise. Views of the other layout are converted. */
+    int want_tiled = grouped ? -1 : 0;
     for (int g0 = 0; g0 < nu || (g0 == 0 && with_shared); g0 += G53_MOE_BATCH) {
         const int gn = (nu - g0) < G53_MOE_BATCH ? (nu - g0) : G53_MOE_BATCH;
         if (gn > 0 && !prefetch && src->getmany) src->getmany(src, w->layer, uniq + g0, gn);
@@ -944,21 +957,35 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                     continue;
                 }
                 check_expert_shape(&q, c, w->layer, e);
-                if (q.gate.dt == GLM53F_WI4 || q.up.dt == GLM53F_WI4 || q.down.dt == GLM53F_WI4) any_i4 = 1;
+                const int q_i4 = q.gate.dt == GLM53F_WI4 || q.up.dt == GLM53F_WI4 || q.down.dt == GLM53F_WI4;
+                if (q_i4) any_i4 = 1;
                 if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128 || any_i4) block_c = 0;
+                if (want_tiled < 0)
+                    want_tiled = q.gate.dt == GLM53F_WF8T && q.up.dt == GLM53F_WF8T && q.down.dt == GLM53F_WF8T &&
+                                 (!with_shared || shared_tileable(w));
+                if (want_tiled == 1 && block_c != 128) {
+                    fprintf(stderr, "glm53f: FATAL, layer %d mixes octet-tiled FP8 experts with other formats in one "
+                                    "chunk\n", w->layer);
+                    abort();
+                }
+                const int tl = want_tiled == 1;
                 const size_t need = expert_stage_bytes(&q);
                 const int dev = g53h_is_device_ptr(q.gate.w);
-                uint8_t *dst = (!dev || q.gate.dt == GLM53F_WF8T || q.up.dt == GLM53F_WF8T || q.down.dt == GLM53F_WF8T) ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
                 size_t off = 0;
                 if (dev) {
+                    const int conv = (q.gate.dt != GLM53F_WI4 && (q.gate.dt == GLM53F_WF8T) != tl) ||
+                                     (q.up.dt != GLM53F_WI4 && (q.up.dt == GLM53F_WF8T) != tl) ||
+                                     (q.down.dt != GLM53F_WI4 && (q.down.dt == GLM53F_WF8T) != tl);
+                    uint8_t *dst = conv ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
                     held[nh++] = e;                      /* released once its kernels are queued */
-                    table[e].gate = rowmajor_view(&q.gate, dst, &off);
-                    table[e].up = rowmajor_view(&q.up, dst, &off);
-                    table[e].down = rowmajor_view(&q.down, dst, &off);
+                    table[e].gate = chunk_view(&q.gate, dst, &off, tl);
+                    table[e].up = chunk_view(&q.up, dst, &off, tl);
+                    table[e].down = chunk_view(&q.down, dst, &off, tl);
                 } else {
-                    table[e].gate = stage_mat(&q.gate, dst, &off);
-                    table[e].up = stage_mat(&q.up, dst, &off);
-                    table[e].down = stage_mat(&q.down, dst, &off);
+                    uint8_t *dst = (uint8_t *)buf_get(&g_hslots[u - b0].b, need);
+                    table[e].gate = stage_mat(&q.gate, dst, &off, tl);
+                    table[e].up = stage_mat(&q.up, dst, &off, tl);
+                    table[e].down = stage_mat(&q.down, dst, &off, tl);
                     /* the copies have completed: hand the views back at once, in the reference's
                      * get / release order (src/core/glm53f_ops.c:1256-1328) */
                     if (src->release) src->release(src, w->layer, e);
@@ -967,7 +994,8 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
             L.shared = NULL;
             if (with_shared && first) {              /* the shared expert rides with the first batch */
                 G53hExpert sh;
-                if (any_i4 && shared_tileable(w)) {  /* the row-wave kernel's fast FP8 path */
+                if (want_tiled < 0) want_tiled = 0;   /* no routed view in the first batch */
+                if ((any_i4 || want_tiled == 1) && shared_tileable(w)) {  /* tiled kernels, or the row-wave fast path */
                     sh.gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
                     sh.up = dev_mat_resident_tiled(&w->sh_up, "shared up");
                     sh.down = dev_mat_resident_tiled(&w->sh_down, "shared down");
@@ -977,7 +1005,7 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                     sh.down = dev_mat_resident(&w->sh_down, "shared down");
                 }
                 if (w->sh_gate.bc != 128 || w->sh_up.bc != 128 || w->sh_down.bc != 128 ||
-                    sh.gate.flags || sh.up.flags || sh.down.flags)
+                    (sh.gate.flags && want_tiled != 1))
                     block_c = 0;
                 table[NE] = sh;
                 if (g53h_h2d_async(table_d + NE, table + NE, sizeof sh)) g53_die("glm53f_moe");
@@ -989,6 +1017,12 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                 int present = 0;
                 for (int u = b0; u < b0 + bn; u++) if (table[uniq[u]].gate.w) present = 1;
                 grouped = block_c == 128 && present;
+                if (want_tiled == 1 && !grouped) {
+                    fprintf(stderr, "glm53f: FATAL, layer %d: octet-tiled experts without a grouped pass\n", w->layer);
+                    abort();
+                }
+                L.tiled = grouped && want_tiled == 1;
+                if (!grouped) want_tiled = 0;        /* the exact kernels read row-major codes */
                 if (grouped) {                       /* the plan reserves the shared expert's rows */
                     const G53hExpert *keep_shared = L.shared;
                     L.shared = with_shared ? table_d + NE : NULL;

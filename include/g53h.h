@@ -183,6 +183,8 @@ int g53h_moe_combine(float *out_d, const float *contrib_d, const float *w_d, int
                      const G53hMoeLayer *L);
 
 /* Batched decode and prefill (T >= 2) as token-sorted grouped GEMMs on the FP8 matrix cores
+ * (row-major experts, or octet-tiled ones when L->tiled: every expert matrix, routed and shared,
+ * in the layout L->tiled names; a descriptor of the other layout counts as unusable, flag 8)
  * (replaces src/core/glm53f_ops.c:1144-1342 moe_chunk with :376-444 matmul_f8_batch for a chunk
  * of tokens): every expert's weights are read once per call of up to 2048 tokens. Routing is the
  * exact router's (top-k indices and weights bit-exact); the expert products run on
