@@ -245,7 +245,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
     __shared__ int sidx[16], ebuf[64];
     __shared__ uint32_t kbuf[64];
     __shared__ uint64_t etab[32];
-    __shared__ int qctr, ndone, routed, inited, gdone;
+    __shared__ int qctr, ndone, routed, inited;
 
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int o = lane >> 3, p = lane & 7;
@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
     const int n_setup = G53_DT_NW - 1 - nR;        /* waves that set up the workgroup's LDS */
 
     G53_TTRACE(0);
-    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; inited = 0; gdone = 0; }
+    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; inited = 0; }
     __syncthreads();
     /* router rows first: waves 0 .. nR-1 take rows b, b + G, ... */
     g53_u4 cr[8];
@@ -417,11 +417,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
         }
         const bool present = __builtin_amdgcn_readfirstlane((int)usable) != 0;
         if (is_g) {
-            if (!present) {                           /* its activations are never read */
-                G53_CBAR();
-                if (lane == 0) g53_lds_add(&gdone, 1);
-                continue;
-            }
+            if (!present) continue;                   /* its activations are never read */
             const int ogl = idx >> 1, og = go_lo + ogl, m = idx & 1;
             const G53hMat &mat = m ? ex.up : ex.gate;
             const uint8_t *pu = mat.w + (size_t)og * (G53_DEC_NBE * 1024);
@@ -445,16 +441,10 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
                 }
             }
             if (t < 32) G53_TTRACE(65 + 2 * t);
-            G53_CBAR();
-            if (lane == 0) g53_lds_add(&gdone, 1);
             continue;
         }
         const int oa = do_lo + 2 * idx, ob = oa + 1 < do_lo + n_do ? oa + 1 : oa;
         float va = 0.0f, vb = 0.0f;
-        /* the down products start once every G task of the workgroup is done, so that they do
-         * not take memory bandwidth from the last G tasks, which every workgroup waits for */
-        if (s < K && g53_lds_ld(&gdone) < nslot * ng && !g53_wait_lds(&gdone, nslot * ng) && lane == 0)
-            g53_flag_err(a.err, 1);
         if (present) {
             const uint8_t *pa = ex.down.w + (size_t)oa * (G53_DEC_NBI * 1024);
             const uint8_t *pb = ex.down.w + (size_t)ob * (G53_DEC_NBI * 1024);

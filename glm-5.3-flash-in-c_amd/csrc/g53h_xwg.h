@@ -141,6 +141,13 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
         if ((unsigned)(t >> 32) != epoch) pend |= 1u << v;
     }
     int spins = 0;
+    int pos = 0;
+    /* two passes of the selection: the first on whatever the first read returned, while the
+     * scores are still being computed (it runs the selection's code once, so that its
+     * instructions are cached when the real pass runs), the second once every score is current */
+#pragma clang loop unroll(disable)
+    for (int pass = 0; pass < 2; pass++) {
+    if (pass == 1) {
     while (__ballot(pend != 0)) {
         if (++spins > limit) return false;
         n_polls++;
@@ -156,6 +163,7 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
             }
     }
     t_seen = __builtin_amdgcn_s_memrealtime();
+    }
     uint32_t key[NV];
 #pragma unroll
     for (int v = 0; v < NV; v++) {
@@ -188,7 +196,7 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
     uint32_t hk = key[0];
     int hv = vid[0];
     float hs = vsc[0];
-    int pos = 0;
+    pos = 0;
     for (int j = 0; j < K; j++) {
         const uint32_t m = __ockl_wfred_max_u32(hk);
         if (m == 0) break;                                /* fewer than K selectable */
@@ -205,6 +213,7 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
         for (int q = 0; q < NV; q++)
             if (q == hp) { hk = key[q]; hv = vid[q]; hs = vsc[q]; }
         pos++;
+    }
     }
     t_tau = __builtin_amdgcn_s_memrealtime();
     if (lane == 0)
@@ -224,127 +233,6 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
     __builtin_amdgcn_wave_barrier();
     if (lane < K) sw[lane] = wj * routed_scale;
     if (pos < K && lane == 0) g53_flag_err(err, 2);
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    return true;
-}
-
-/* The same routing with a faster selection (no K serial rounds of wave reductions):
- *   1. the K-th largest key T, by bisection over the key's 32 bits, MSB first: each step counts
- *      the keys >= a candidate with one ballot per key slot and a scalar popcount;
- *   2. the chosen set: every key > T, and the keys equal to T with the lowest expert indices
- *      (index lane + 64 v: slot-major, then lane) until K are chosen;
- *   3. their order (larger key first, the lower index among equal keys, as K rounds of
- *      "first strictly greater" arg-max give): lane j of the chosen, gathered in index order,
- *      counts the chosen that precede it.
- * The scores, keys, weights and error convention are those of g53_route_wave. Returns false when
- * the scores did not all arrive in time. */
-template <int NV>
-__device__ __forceinline__ bool g53_route_bisect(const g53_u64 *score, const float *bias, int NE, int K, int norm_topk,
-                                                 float routed_scale, unsigned epoch, int *sidx, float *sw,
-                                                 uint32_t *kbuf, int *ebuf, float *fbuf, int *err, int lane,
-                                                 g53_u64 &t_seen, int limit, g53_u64 *tr = nullptr)
-{
-    const __amdgpu_buffer_rsrc_t rs = g53_rsrc(score);
-    float scv[NV];
-    uint32_t pend = 0;
-#pragma unroll
-    for (int v = 0; v < NV; v++) {
-        const int e = min(lane + 64 * v, NE - 1);
-        const g53_u64 t = g53_ld_coh64(rs, 8 * e);
-        scv[v] = __uint_as_float((uint32_t)t);
-        if ((unsigned)(t >> 32) != epoch) pend |= 1u << v;
-    }
-    int spins = 0;
-    while (__ballot(pend != 0)) {
-        if (++spins > limit) return false;
-        __builtin_amdgcn_s_sleep(2);
-        g53_u64 t[NV];
-#pragma unroll
-        for (int v = 0; v < NV; v++) t[v] = g53_ld_coh64(rs, 8 * min(lane + 64 * v, NE - 1));
-#pragma unroll
-        for (int v = 0; v < NV; v++)
-            if ((pend & (1u << v)) && (unsigned)(t[v] >> 32) == epoch) {
-                scv[v] = __uint_as_float((uint32_t)t[v]);
-                pend &= ~(1u << v);
-            }
-    }
-    t_seen = __builtin_amdgcn_s_memrealtime();
-    uint32_t key[NV];
-#pragma unroll
-    for (int v = 0; v < NV; v++) {
-        const int e = lane + 64 * v;
-        const float ch = e < NE ? scv[v] + bias[e] : -INFINITY;
-        key[v] = (ch > -INFINITY) ? g53_fkey(ch) : 0u;    /* 0: never chosen (NaN, -inf) */
-    }
-    if (tr && lane == 0) tr[0] = __builtin_amdgcn_s_memrealtime();
-    auto count_ge = [&](uint32_t c) -> int {
-        int n = 0;
-#pragma unroll
-        for (int v = 0; v < NV; v++) n += __popcll(__ballot(key[v] >= c));
-        return n;
-    };
-    const int nsel = count_ge(1u);
-    const int Kt = nsel < K ? nsel : K;
-    uint32_t T = 0xffffffffu;
-    if (Kt > 0) {
-        T = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t c = T | (1u << bit);
-            if (count_ge(c) >= Kt) T = c;
-        }
-    }
-    if (tr && lane == 0) tr[1] = __builtin_amdgcn_s_memrealtime();
-    int need = Kt - (T == 0xffffffffu ? 0 : count_ge(T + 1u));
-    int n = 0;
-#pragma unroll
-    for (int v = 0; v < NV; v++) {
-        const uint64_t gt = __ballot(key[v] > T);
-        uint64_t eq = __ballot(key[v] == T && key[v] != 0u), take = 0;
-        while (need > 0 && eq) {
-            take |= eq & (~eq + 1);                       /* lowest lane first */
-            eq &= eq - 1;
-            need--;
-        }
-        const uint64_t m = gt | take;
-        if ((m >> lane) & 1) {
-            const int at = n + __popcll(m & ((1ull << lane) - 1));
-            kbuf[at] = key[v];
-            ebuf[at] = lane + 64 * v;
-            fbuf[at] = scv[v];
-        }
-        n += __popcll(m);
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    if (tr && lane == 0) tr[2] = __builtin_amdgcn_s_memrealtime();
-    if (lane < n) {
-        const uint32_t kj = kbuf[lane];
-        const int ej = ebuf[lane];
-        int r = 0;
-        for (int i = 0; i < n; i++) {
-            const uint32_t ki = kbuf[i];
-            r += (ki > kj) || (ki == kj && ebuf[i] < ej);
-        }
-        sidx[r] = ej;
-        sw[r] = fbuf[lane];
-    }
-    if (lane >= n && lane < K) { sidx[lane] = -1; sw[lane] = 0.0f; }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    if (tr && lane == 0) tr[3] = __builtin_amdgcn_s_memrealtime();
-    /* the weights: every lane forms the sum in slot order, lane j divides weight j */
-    float wj = 0.0f;
-    if (lane < K) wj = sw[lane];
-    if (norm_topk) {
-        double sum = 0.0;
-        for (int q = 0; q < K; q++) sum += (double)sw[q];
-        if (lane < K) wj = (float)((double)wj / (sum + 1e-20));
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < K) sw[lane] = wj * routed_scale;
-    if (n < K && lane == 0) g53_flag_err(err, 2);
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
     return true;
