@@ -81,7 +81,7 @@ typedef __attribute__((address_space(1))) const float g53_gflt;
 #define G53_GRP_LXS   2       /* activation slices in a thread's ring                        */
 #endif
 #ifndef G53_GRP_NS
-#define G53_GRP_NS    4       /* activation slices in the workgroup's LDS ring               */
+#define G53_GRP_NS    2       /* activation slices in the workgroup's LDS ring               */
 #endif
 
 /* error flags (meta[1]) */
