@@ -59,6 +59,14 @@
 #define G53_DT_DTAB 24576          /* bytes of the expert table staged in LDS            */
 #define G53_DT_ROT 16              /* copies of the tagged activations, used in rotation  */
 
+#ifndef G53_DT_NTW
+#define G53_DT_NTW 1
+#endif
+#if G53_DT_NTW
+#define G53_DT_LD(p) __builtin_nontemporal_load(p)  /* codes are read once: stream past the caches */
+#else
+#define G53_DT_LD(p) (*(p))
+#endif
 #if defined(__HIP_DEVICE_COMPILE__)
 typedef __attribute__((address_space(1))) const g53_u4 g53_gv4t;
 #else
@@ -167,7 +175,7 @@ __device__ __forceinline__ double g53_oct_stream(const uint8_t *pu, const float 
     g53_gv4t *q = (g53_gv4t *)(g53_uniform_ptr(pu) + 16 * lane);
     g53_u4 r[P];
 #pragma unroll
-    for (int j = 0; j < P; j++) r[j] = q[64 * j];
+    for (int j = 0; j < P; j++) r[j] = G53_DT_LD(q + 64 * j);
     ready();
     double acc = 0.0;
     const int sbits = __float_as_int(scv);
@@ -177,8 +185,8 @@ __device__ __forceinline__ double g53_oct_stream(const uint8_t *pu, const float 
         const float4 xb[4] = {x1[0], x1[1], x1[2], x1[3]};
         const float fa = g53_oct_acc(r[j], xa), fb = g53_oct_acc(r[j + 1], xb);
         if (refill) {
-            r[j] = q[64 * (u + P)];
-            r[j + 1] = q[64 * (u + 1 + P)];
+            r[j] = G53_DT_LD(q + 64 * (u + P));
+            r[j + 1] = G53_DT_LD(q + 64 * (u + 1 + P));
         }
         const double ta = g53_oct_tree(fa), tb = g53_oct_tree(fb);
         acc = acc + ta * (double)__int_as_float(__builtin_amdgcn_readlane(sbits, u));
@@ -209,8 +217,8 @@ __device__ __forceinline__ void g53_oct_stream2(const uint8_t *pa, const uint8_t
     g53_u4 ra[NU], rb[NU];
 #pragma unroll
     for (int u = 0; u < NU; u++) {
-        ra[u] = qa[64 * u];
-        rb[u] = qb[64 * u];
+        ra[u] = G53_DT_LD(qa + 64 * u);
+        rb[u] = G53_DT_LD(qb + 64 * u);
     }
     ready();
     double sa = 0.0, sb = 0.0;

@@ -75,7 +75,7 @@ typedef __attribute__((address_space(1))) const float g53_gflt;
 #define G53_GRP_PERS  1       /* workgroups per CU in the grid: each loops over its items  */
 #endif
 #ifndef G53_GRP_RS
-#define G53_GRP_RS    4       /* weight blocks in a lane's ring                              */
+#define G53_GRP_RS    2       /* weight blocks in a lane's ring                              */
 #endif
 #ifndef G53_GRP_LXS
 #define G53_GRP_LXS   2       /* activation slices in a thread's ring                        */

@@ -28,6 +28,14 @@
 #define G53_RW_LD    65                 /* LDS row stride of the partials (doubles) */
 
 typedef unsigned int g53_v4u __attribute__((ext_vector_type(4)));
+#ifndef G53_RW_NT
+#define G53_RW_NT 1
+#endif
+#if G53_RW_NT
+#define G53_RW_W(p) __builtin_nontemporal_load(p)   /* weights are read once */
+#else
+#define G53_RW_W(p) (*(p))
+#endif
 #ifndef G53_RW_RB
 #define G53_RW_RB 4                     /* octet-tiled rows whose 16-byte runs are loaded together */
 #endif
@@ -140,8 +148,8 @@ __device__ __forceinline__ double g53_pass(const G53hMat &m, const float *__rest
                     for (int st = 0; st < 4; st++) {
                         const int r = row0 + r4 + i, b = st * 8 + j;
                         if (st < nst && b < nbc && r < rows)
-                            c[i][st] = *(const g53_v4u *)(m.w + ((size_t)(r >> 3) * nb + c0 + b) * 1024 + (r & 7) * 128 +
-                                                          run * 16);
+                            c[i][st] = G53_RW_W((const g53_v4u *)(m.w + ((size_t)(r >> 3) * nb + c0 + b) * 1024 +
+                                                                  (r & 7) * 128 + run * 16));
                         else
                             c[i][st] = g53_v4u{0, 0, 0, 0};
                     }
@@ -192,8 +200,8 @@ __device__ __forceinline__ double g53_pass(const G53hMat &m, const float *__rest
             const int r = row0 + st * rps + sub;
             if (st < nst && g < ng && r < rows) {
                 const g53_v4u *w = (const g53_v4u *)(m.w + (size_t)r * rb + (size_t)g * 32);
-                c0[st] = w[0];
-                c1[st] = w[1];
+                c0[st] = G53_RW_W(w);
+                c1[st] = G53_RW_W(w + 1);
                 stp[st] = m.s[(size_t)r * ng + g];
             } else {
                 c0[st] = g53_v4u{0, 0, 0, 0};
@@ -316,8 +324,8 @@ k_rows_gateup(float *__restrict__ act, const float *__restrict__ x, int nslots, 
             const int st = k % G53_GU_ROWS, r = row0 + st * rps + sub;
             if (st < nst && gi < ng && r < I) {
                 const g53_v4u *w = (const g53_v4u *)(m.w + (size_t)r * rb + (size_t)gi * 32);
-                c0[k] = w[0];
-                c1[k] = w[1];
+                c0[k] = G53_RW_W(w);
+                c1[k] = G53_RW_W(w + 1);
                 stp[k] = m.s[(size_t)r * ng + gi];
             } else {
                 c0[k] = g53_v4u{0, 0, 0, 0};
