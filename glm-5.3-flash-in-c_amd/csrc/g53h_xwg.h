@@ -116,6 +116,9 @@ __device__ __forceinline__ double g53_router_row(const g53_u4 (&c)[8], const flo
 extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
 
 /* ------------------------------------------------------------------ routing ---- */
+#ifndef G53_POLL_GAP
+#define G53_POLL_GAP 8             /* s_sleep units (64 clocks) between two reads of the scores */
+#endif
 /* Top-k of score + bias by one wave (reference src/core/glm53f_ops.c:957-969: K rounds of
  * "first strictly greater" arg-max, so the larger value first, the lower index among equal
  * values, NaN and -inf never), then the weights (:970-975). The scores are the tagged words
@@ -148,19 +151,34 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
 #pragma clang loop unroll(disable)
     for (int pass = 0; pass < 2; pass++) {
     if (pass == 1) {
-    while (__ballot(pend != 0)) {
-        if (++spins > limit) return false;
-        n_polls++;
-        __builtin_amdgcn_s_sleep(2);
-        g53_u64 t[NV];                                    /* every load in flight at once */
+    /* two reads of the scores in flight at a time, issued a short sleep apart: a score that
+     * lands is seen one memory latency later, not up to two */
+    g53_u64 ta[NV], tb[NV];
+    auto issue = [&](g53_u64 (&t)[NV]) {
 #pragma unroll
         for (int v = 0; v < NV; v++) t[v] = g53_ld_coh64(rs, 8 * min(lane + 64 * v, NE - 1));
+    };
+    auto take = [&](const g53_u64 (&t)[NV]) {
 #pragma unroll
         for (int v = 0; v < NV; v++)
             if ((pend & (1u << v)) && (unsigned)(t[v] >> 32) == epoch) {
                 scv[v] = __uint_as_float((uint32_t)t[v]);
                 pend &= ~(1u << v);
             }
+        return __ballot(pend != 0) == 0;
+    };
+    if (__ballot(pend != 0)) {
+        issue(ta);
+        for (;;) {
+            if (++spins > limit) return false;
+            n_polls++;
+            __builtin_amdgcn_s_sleep(G53_POLL_GAP);
+            issue(tb);
+            if (take(ta)) break;
+            __builtin_amdgcn_s_sleep(G53_POLL_GAP);
+            issue(ta);
+            if (take(tb)) break;
+        }
     }
     t_seen = __builtin_amdgcn_s_memrealtime();
     }
