@@ -15,8 +15,10 @@
  * leaves in every lane exactly the 16 codes of one of the reference's eight fp32 accumulators
  * of one row and block; the lane multiplies them in column order, the eight lanes of a row join
  * their accumulators by the reference's pairwise double tree through DPP exchanges, scale the
- * block sum in double and add it to the row's double sum in block order. Nothing is traded
- * through LDS and every load instruction of the kernel reads whole 1 KB runs.
+ * block sum in double and add it to the row's double sum in block order (a D task runs its two
+ * octets' units of one block through one tree: half of a row's lanes finish each octet's block
+ * sum). Nothing is traded through LDS and every load instruction of the kernel reads whole 1 KB
+ * runs.
  *
  * Workgroup b of G (one per CU) owns gate/up octets [256 b / G, 256 (b+1) / G) and down octets
  * [512 b / G, 512 (b+1) / G) of every slot: its down rows' contributions of every slot stay in
@@ -203,6 +205,22 @@ __device__ __forceinline__ double g53_oct_stream(const uint8_t *pu, const float 
     return acc;
 }
 
+/* Two units' block sums through one tree: each lane holds accumulator sigma(p) of unit A (fa)
+ * and of unit B (fb). Lanes of role 0 (run p with (p ^ p >> 2) & 1 == 0) end with A's block
+ * sum, lanes of role 1 with B's. The first level trades one float with the neighbour (which
+ * has the other role) and adds in the lane; the pairs and the halves (quad_perm 2301,
+ * row_half_mirror) join lanes of the same role. The additions and their grouping are those
+ * of g53_oct_tree, ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) (reference :206-209). */
+__device__ __forceinline__ double g53_oct_tree2(float fa, float fb, bool r1)
+{
+    const float send = r1 ? fa : fb, own = r1 ? fb : fa;
+    const float got = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xf, 0xf, true));
+    double t = (double)own + (double)got;
+    t = t + g53_dpp64<0x4E>(t);
+    t = t + g53_dpp64<0x141>(t);
+    return t;
+}
+
 /* The same for two row octets at once (pa, pb), unit u of both against block u: their sums in
  * block order come back in acc_a and acc_b. sp points lane u at sequence a's unit u scale and
  * lane 32 + u at b's. All 2 NU units are in flight before ready() runs. */
@@ -221,19 +239,24 @@ __device__ __forceinline__ void g53_oct_stream2(const uint8_t *pa, const uint8_t
         rb[u] = G53_DT_LD(qb + 64 * u);
     }
     ready();
-    double sa = 0.0, sb = 0.0;
     const int sbits = __float_as_int(scv);
+    /* one tree for both units; this lane's role keeps one octet's sum */
+    const int pr = lane & 7;
+    const bool r1 = ((pr ^ (pr >> 2)) & 1) != 0;
+    double acc = 0.0;
 #pragma unroll
     for (int u = 0; u < NU; u++) {
         const float4 *xr = (const float4 *)(xv + u * VBLK);
         const float4 x4[4] = {xr[0], xr[1], xr[2], xr[3]};
         const float fa = g53_oct_acc(ra[u], x4), fb = g53_oct_acc(rb[u], x4);
-        const double ta = g53_oct_tree(fa), tb = g53_oct_tree(fb);
-        sa = sa + ta * (double)__int_as_float(__builtin_amdgcn_readlane(sbits, u));
-        sb = sb + tb * (double)__int_as_float(__builtin_amdgcn_readlane(sbits, 32 + u));
+        const double t = g53_oct_tree2(fa, fb, r1);
+        const float sa = __int_as_float(__builtin_amdgcn_readlane(sbits, u));
+        const float sb = __int_as_float(__builtin_amdgcn_readlane(sbits, 32 + u));
+        acc = acc + t * (double)(r1 ? sb : sa);
     }
-    acc_a = sa;
-    acc_b = sb;
+    const double other = g53_dpp64<0xB1>(acc);          /* the neighbour has the other role */
+    acc_a = r1 ? other : acc;
+    acc_b = r1 ? acc : other;
 }
 
 #define G53_TTRACE(k) do { if (a.trace && lane == 0) \
