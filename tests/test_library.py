@@ -35,6 +35,7 @@ def test_declared_globals_exported():
     L = C.CDLL(glm53h.LIB_PATH)
     assert C.c_long.in_dll(L, "glm53f_expert_drops").value >= 0
     assert C.c_int.in_dll(L, "glm53f_quiet").value in (0, 1)
+    assert C.c_char_p.in_dll(L, "glm53f_i4_dir").value is None
 
 
 def test_python_mirror_covers_the_abi():
