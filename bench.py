@@ -269,6 +269,37 @@ def bench_grouped(a):
     print(json.dumps(line), flush=True)
 
 
+def prefill_beside(L, layer, sp, steps=10, warm=3):
+    """BASELINE config 4 (2048-token prefill, uniform routing) on the config-2 layer just timed
+    (config 4 has config 2's layer), so the default line carries the prefill FP8 TFLOP/s that
+    BASELINE's metric names. Two token batches cycled; the same figures as --workload 4."""
+    T = 2048
+    xd = [DevBuf.from_array(S.x_host(sp, T, batch=b)) for b in range(2)]
+    out = DevBuf(T * sp.E * 4)
+    idx = DevBuf(T * sp.K * 4)
+    check(L.g53h_moe(out.ptr, xd[0].ptr, T, C.byref(layer.layer), idx.ptr, None), "g53h_moe")
+    D = float(len(np.unique(idx.download(np.int32))))
+    for i in range(warm):
+        check(L.g53h_moe(out.ptr, xd[i % 2].ptr, T, C.byref(layer.layer), None, None), "g53h_moe")
+    glm53h.sync()
+    check(L.g53h_mark(), "mark")
+    for i in range(steps):
+        check(L.g53h_moe(out.ptr, xd[i % 2].ptr, T, C.byref(layer.layer), None, None), "g53h_moe")
+    check(L.g53h_mark(), "mark")
+    ms = L.g53h_elapsed_ms() / steps
+    glm53h.sync()
+    if L.g53h_grouped_errors():
+        sys.exit("the grouped kernels reported error flags")
+    flops = 2.0 * (T * sp.K + T) * 3 * sp.E * sp.I
+    layer_bytes = (D + 1) * sp.expert_bytes() + sp.NE * sp.E * 2 + sp.NE * 4 + T * sp.E * 4 * 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "BASELINE config 4: prefill of 2048 tokens on the same layer, uniform routing, + shared",
+            "steps": steps, "warmup": warm, "ms_per_layer": round(ms, 4), "tflops": round(tflops, 2),
+            "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+            "hbm_floor_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "unique_routed_experts": D}
+
+
 def _traffic(cfg):
     """HBM bytes per launch of the dominant kernel from the committed counter summary, if any."""
     tp = os.path.join(ROOT, "profiles", f"k_grp_gateup_config{cfg}_traffic.json")
@@ -521,6 +552,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="config 2: leave out the config-4 prefill figures measured beside the decode line")
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
     ap.add_argument("--route-trace", default=None,
                     help="config 5: write the decode routing trace (GLM53F_ROUTE_TOP16 format) to this file and "
@@ -602,6 +635,7 @@ def main():
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
+    prefill = None if (i4 or a.no_prefill) else prefill_beside(L, layer, sp)
     traffic = None                      # HBM bytes per launch from the committed counter summary
     tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 else ''}_traffic.json")
     if os.path.exists(tp):
@@ -634,6 +668,7 @@ def main():
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 2)},
         "cpu_baseline": cpu,
+        "prefill_config4": prefill,
     }
     print(json.dumps(line), flush=True)
 
