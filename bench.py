@@ -300,6 +300,41 @@ def prefill_beside(L, layer, sp, steps=10, warm=3):
             "unique_routed_experts": D}
 
 
+def batched_beside(L, layer, steps=100, warm=5):
+    """BASELINE config 3 (64 tokens, Zipf(1.1) popularity) on the config-2 layer just timed: config
+    3 is config 2 with the calibrated Zipf selection bias, so only the bias is swapped in. Four
+    token batches cycled; the same figures as --workload 3."""
+    sp3 = S.spec(3)
+    T = 64
+    bias = DevBuf.from_array(S.bias_host(sp3))
+    l3 = G53hMoeLayer.from_buffer_copy(layer.layer)
+    l3.bias = bias.ptr
+    xd = [DevBuf.from_array(S.x_host(sp3, T, batch=b)) for b in range(4)]
+    out = DevBuf(T * sp3.E * 4)
+    idx = DevBuf(T * sp3.K * 4)
+    uniq = []
+    for b in range(4):
+        check(L.g53h_moe(out.ptr, xd[b].ptr, T, C.byref(l3), idx.ptr, None), "g53h_moe")
+        uniq.append(len(np.unique(idx.download(np.int32))))
+    for i in range(warm):
+        check(L.g53h_moe(out.ptr, xd[i % 4].ptr, T, C.byref(l3), None, None), "g53h_moe")
+    glm53h.sync()
+    check(L.g53h_mark(), "mark")
+    for i in range(steps):
+        check(L.g53h_moe(out.ptr, xd[i % 4].ptr, T, C.byref(l3), None, None), "g53h_moe")
+    check(L.g53h_mark(), "mark")
+    ms = L.g53h_elapsed_ms() / steps
+    glm53h.sync()
+    if L.g53h_grouped_errors():
+        sys.exit("the grouped kernels reported error flags")
+    D = float(np.mean(uniq))
+    layer_bytes = (D + 1) * sp3.expert_bytes() + sp3.NE * sp3.E * 2 + sp3.NE * 4 + T * sp3.E * 4 * 2
+    return {"workload": "BASELINE config 3: 64 tokens x top-8, Zipf(1.1) popularity (the calibrated bias), same layer",
+            "steps": steps, "warmup": warm, "us_per_layer": round(ms * 1e3, 2),
+            "hbm_floor_frac": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "unique_routed_experts": D}
+
+
 def _traffic(cfg):
     """HBM bytes per launch of the dominant kernel from the committed counter summary, if any."""
     tp = os.path.join(ROOT, "profiles", f"k_grp_gateup_config{cfg}_traffic.json")
@@ -553,7 +588,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--no-prefill", action="store_true",
-                    help="config 2: leave out the config-4 prefill figures measured beside the decode line")
+                    help="config 2: leave out the config-3 and config-4 figures measured beside the decode line")
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
     ap.add_argument("--route-trace", default=None,
                     help="config 5: write the decode routing trace (GLM53F_ROUTE_TOP16 format) to this file and "
@@ -636,6 +671,7 @@ def main():
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
     prefill = None if (i4 or a.no_prefill) else prefill_beside(L, layer, sp)
+    batched = None if (i4 or a.no_prefill) else batched_beside(L, layer)
     traffic = None                      # HBM bytes per launch from the committed counter summary
     tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 else ''}_traffic.json")
     if os.path.exists(tp):
@@ -668,6 +704,7 @@ def main():
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 2)},
         "cpu_baseline": cpu,
+        "batched_config3": batched,
         "prefill_config4": prefill,
     }
     print(json.dumps(line), flush=True)
