@@ -460,7 +460,7 @@ def bench_stack(a):
     base = S.spec(3)
     E, I, NE, K = base.E, base.I, base.NE, base.K
     from glm53h import zipf
-    rho, pf, n_io = zipf.table(NE, K, base.zipf_s)["rho"], 6, 4
+    rho, pf, n_io = zipf.table(NE, K, base.zipf_s)["rho"], a.prefetch, 4
     cf = glm53h.Glm53fCfg()
     cf.hidden, cf.n_layers, cf.n_experts, cf.topk, cf.n_shared, cf.moe_inter = E, NL, NE, K, 1, I
     cf.routed_scale, cf.norm_topk, cf.swiglu_limit = base.routed_scale, base.norm_topk, base.limit
@@ -593,6 +593,9 @@ def main():
     ap.add_argument("--route-trace", default=None,
                     help="config 5: write the decode routing trace (GLM53F_ROUTE_TOP16 format) to this file and "
                          "report LRU vs Belady misses per token on it (the trace costs time: not for timing)")
+    ap.add_argument("--prefetch", type=int, default=6,
+                    help="workload 5: next-layer experts hinted per layer (the reference's --prefetch, "
+                         "src/cli/glm53f_run.c:258,284; 0 hints nothing)")
     ap.add_argument("--stack-layers", type=int, default=42,
                     help="config 5: layers in the stack (42 is BASELINE's; fewer, e.g. 24, fit every expert in the "
                          "200 GB cache, which isolates the per-layer cost from host reads)")
