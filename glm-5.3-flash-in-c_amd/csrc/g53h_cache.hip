@@ -35,7 +35,6 @@
 #include "g53h_runtime.h"
 #include "glm53f.h"
 #include "glm53f_cache.h"
-#include "glm53f_i4file.h"
 #include <unistd.h>
 extern "C" {
 #include "../host/g53h_ckpt.h"
@@ -79,20 +78,9 @@ struct Impl {
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
     std::mutex mu;
-    /* int4 containers (glm53f_i4_dir): a descriptor per layer (-1: quantised on the way in) and
-     * one pinned buffer per copy stream, reused once its last copy is done */
-    std::vector<int> i4_fd;
-    uint8_t *i4_host[2] = {nullptr, nullptr};
-    hipEvent_t i4_ev[2] = {nullptr, nullptr};
-    bool i4_ev_rec[2] = {false, false};
     ~Impl()
     {
         g53h_ckpt_free(ckpt);
-        for (int fd : i4_fd) if (fd >= 0) close(fd);
-        for (int k = 0; k < 2; k++) {
-            if (i4_host[k]) (void)hipHostFree(i4_host[k]);
-            if (i4_ev[k]) (void)hipEventDestroy(i4_ev[k]);
-        }
     }
 };
 
@@ -176,28 +164,7 @@ int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t 
 {
     *nread = 0;
     uint8_t *const base0 = m->arena + (size_t)slot * (size_t)c->slot_bytes;
-    if (m->i4 && layer < (int)m->i4_fd.size() && m->i4_fd[layer] >= 0) {
-        /* the int4 container: the slot's bytes as they are, one read, no arithmetic (reference
-         * src/cache/glm53f_cache.c:105-111) */
-        const int k = s == m->prefetch ? 1 : 0;
-        if (m->i4_ev_rec[k] && hipEventSynchronize(m->i4_ev[k]) != hipSuccess) return 0;
-        const int64_t n = c->slot_bytes, off = glm53f_i4file_offset(expert, n);
-        for (int64_t got = 0; got < n;) {
-            const ssize_t r = pread(m->i4_fd[layer], m->i4_host[k] + got, (size_t)(n - got), off + got);
-            if (r <= 0) return 0;
-            got += r;
-        }
-        if (m->used[slot] >= 0) {
-            if (hipStreamWaitEvent(s, m->used_ev[m->used[slot]], 0) != hipSuccess) return 0;
-            unuse(m, slot);
-        }
-        if (m->landed_ok[slot] && hipStreamWaitEvent(s, m->landed[slot], 0) != hipSuccess) return 0;
-        if (hipMemcpyAsync(base0, m->i4_host[k], (size_t)n, hipMemcpyHostToDevice, s) != hipSuccess ||
-            hipEventRecord(m->i4_ev[k], s) != hipSuccess)
-            return 0;
-        m->i4_ev_rec[k] = true;
-        *nread = n;
-    } else if (!issue_reads(c, m, slot, layer, expert, s, nread)) {
+    if (!issue_reads(c, m, slot, layer, expert, s, nread)) {
         return 0;
     }
     if (hipEventRecord(m->landed[slot], s) != hipSuccess) return 0;
@@ -593,27 +560,7 @@ extern "C" int glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53
         return -1;
     }
     c->st = st;
-    const int rc = cache_setup(c, m, cfg, budget_bytes, n_io, i4);
-    if (rc || !c->i4 || !glm53f_i4_dir || !impl_of(c)) return rc;
-    /* int4 containers: the layers found in glm53f_i4_dir are read as they are (reference
-     * src/cache/glm53f_cache.c:363-378); the others are quantised on the way in */
-    m = impl_of(c);
-    m->i4_fd.assign(c->n_layers, -1);
-    for (int L = 0; L < c->n_layers; L++) {
-        if (L >= cfg->n_layers || cfg->is_dense[L]) continue;
-        m->i4_fd[L] = glm53f_i4file_open_layer(st, cfg, L, glm53f_i4_dir);
-        if (m->i4_fd[L] >= 0) c->i4_layers++;
-    }
-    if (c->i4_layers) {
-        for (int k = 0; k < 2; k++)
-            if (hipHostMalloc((void **)&m->i4_host[k], (size_t)c->slot_bytes, hipHostMallocDefault) != hipSuccess ||
-                hipEventCreateWithFlags(&m->i4_ev[k], hipEventDisableTiming) != hipSuccess) {
-                fprintf(stderr, "glm53f_cache: cannot allocate pinned buffers for the int4 containers\n");
-                glm53f_cache_free(c);
-                return -1;
-            }
-    }
-    return 0;
+    return cache_setup(c, m, cfg, budget_bytes, n_io, i4);
 }
 
 extern "C" int g53h_cache_init_store(Glm53fCache *c, const G53hStore *store, const Glm53fCfg *cfg,

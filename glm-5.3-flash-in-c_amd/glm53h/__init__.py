@@ -250,9 +250,6 @@ _SIGS = {
     "g53h_cache_init_store": (C.c_int, [C.POINTER(Glm53fCache), C.POINTER(G53hStore), C.POINTER(Glm53fCfg),
                                         C.c_int64, C.c_int, C.c_int]),
     "g53h_st_open": (C.c_int, [C.POINTER(Glm53fSt), C.c_char_p, C.c_int]),
-    "glm53f_i4file_write_layer": (C.c_int, [C.POINTER(Glm53fSt), C.POINTER(Glm53fCfg), C.c_int, C.c_char_p]),
-    "glm53f_i4file_open_layer": (C.c_int, [C.POINTER(Glm53fSt), C.POINTER(Glm53fCfg), C.c_int, C.c_char_p]),
-    "glm53f_i4file_verify_layer": (C.c_int, [C.POINTER(Glm53fSt), C.POINTER(Glm53fCfg), C.c_int, C.c_char_p]),
     "g53h_st_close": (None, [C.POINTER(Glm53fSt)]),
     "g53h_st_index": (C.c_int, [C.POINTER(Glm53fSt), C.c_char_p]),
     "g53h_st_expert_bytes": (C.c_size_t, [C.POINTER(Glm53fCfg)]),

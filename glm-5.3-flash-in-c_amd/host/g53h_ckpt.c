@@ -74,12 +74,19 @@ static int js_str(Js *j, char *out, size_t cap)
 
 static int64_t js_int(Js *j)
 {
+    /* parsed by hand within [p, end): the header buffer is not NUL-terminated */
     js_ws(j);
-    char *e = NULL;
-    const long long v = strtoll(j->p, &e, 10);
-    if (e == j->p) { j->bad = 1; return 0; }
-    j->p = e;
-    return (int64_t)v;
+    const char *q = j->p;
+    const int neg = q < j->end && *q == '-';
+    if (neg) q++;
+    if (q >= j->end || *q < '0' || *q > '9') { j->bad = 1; return 0; }
+    uint64_t v = 0;
+    for (; q < j->end && *q >= '0' && *q <= '9'; q++) {
+        if (v > (UINT64_C(1) << 62) / 10) { j->bad = 1; return 0; }
+        v = v * 10 + (uint64_t)(*q - '0');
+    }
+    j->p = q;
+    return neg ? -(int64_t)v : (int64_t)v;
 }
 
 /* Skip any value. */
@@ -90,7 +97,8 @@ static void js_skip(Js *j)
     const char ch = *j->p;
     if (ch == '"') {
         j->p++;
-        while (j->p < j->end && *j->p != '"') { if (*j->p == '\\') j->p++; j->p++; }
+        while (j->p < j->end && *j->p != '"') j->p += (*j->p == '\\' && j->end - j->p > 1) ? 2 : 1;
+        if (j->p >= j->end) { j->bad = 1; return; }
         j->p++;
     } else if (ch == '{' || ch == '[') {
         const char close = ch == '{' ? '}' : ']';

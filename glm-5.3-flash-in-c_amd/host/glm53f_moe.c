@@ -25,6 +25,7 @@
 
 long glm53f_expert_drops = 0;
 int  glm53f_quiet = 0;
+const char *glm53f_i4_dir = NULL;     /* not read: int4 layers are quantised as they land */
 
 #define G53_MOE_CHUNK 64                /* reference chunk (src/core/glm53f_ops.c:988) */
 

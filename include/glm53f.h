@@ -178,8 +178,9 @@ typedef struct {
 extern long glm53f_expert_drops;
 /* Non-zero silences progress lines. */
 extern int glm53f_quiet;
-/* Directory of int4 expert containers (include/glm53f_i4file.h), or NULL: the HBM cache in int4
- * mode reads the layers found there instead of quantising them (include/glm53f/glm53f.h:297). */
+/* Directory of int4 expert containers (include/glm53f/glm53f.h:297). Kept so that callers built
+ * against the reference link; the on-disk container is outside this library, so the HBM cache in
+ * int4 mode always re-quantises the FP8 experts on the device as they land. */
 extern const char *glm53f_i4_dir;
 
 /* Router: idx/w get topk entries; selection by sigmoid(W x) + bias, weights from the

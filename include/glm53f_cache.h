@@ -27,10 +27,9 @@
  *   - int4 slots (i4 != 0, the reference's --experts int4): each FP8 expert read is staged in
  *     HBM and re-quantised into the slot by the device quantiser (g53h_i4_from_f8, bit-exact
  *     with the reference's glm53f_i4_from_f8), in the reference's int4 slot layout, so a budget
- *     holds the reference's number of slots and get() returns its GLM53F_WI4 views. With
- *     glm53f_i4_dir set (glm53f_cache_init over a checkpoint), a layer that has a container
- *     there (include/glm53f_i4file.h, written from this checkpoint) is read from it: one read
- *     of the slot's bytes, no quantising; i4_layers counts those layers.
+ *     holds the reference's number of slots and get() returns its GLM53F_WI4 views. The
+ *     reference's on-disk int4 container (glm53f_i4_dir) is not read: every layer is quantised
+ *     on the way in, and i4_layers stays zero.
  */
 #ifndef GLM53F_CACHE_H
 #define GLM53F_CACHE_H

@@ -10,7 +10,6 @@
 #include "glm53f.h"
 #include "glm53f_load.h"
 #include "glm53f_st.h"
-#include "glm53f_i4file.h"
 
 /* The reference's index of dir: per tensor (discovery order) 7 int64 (shard, dtype, ndim,
  * shape[0], shape[1], off, nbytes) into meta, names '\n'-separated into names. Returns the
@@ -75,21 +74,4 @@ long long ref_expert_read(const char *dir, int hidden, int inter, int n_experts,
     }
     glm53f_st_close(&st);
     return o;
-}
-
-/* The reference's int4 container writer (src/io/glm53f_i4file.c) on a checkpoint directory:
- * layer `layer` of n_layers (all MoE) into out_dir. Returns its return code (0 written, 1
- * skipped, -1 failed), or -2 when the checkpoint cannot be opened. */
-int ref_i4_write(const char *dir, int hidden, int inter, int n_experts, int br, int bc, int n_layers, int layer,
-                 const char *out_dir)
-{
-    Glm53fSt st;
-    if (glm53f_st_open(&st, dir) != 0) return -2;
-    Glm53fCfg c;
-    memset(&c, 0, sizeof c);
-    c.hidden = hidden; c.moe_inter = inter; c.n_experts = n_experts; c.fp8_block_r = br; c.fp8_block_c = bc;
-    c.n_layers = n_layers;
-    const int rc = glm53f_i4file_write_layer(&st, &c, layer, out_dir);
-    glm53f_st_close(&st);
-    return rc;
 }
