@@ -163,7 +163,6 @@ int issue_reads(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStr
 int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t s, int background, int64_t *nread)
 {
     *nread = 0;
-    uint8_t *const base0 = m->arena + (size_t)slot * (size_t)c->slot_bytes;
     if (!issue_reads(c, m, slot, layer, expert, s, nread)) {
         return 0;
     }

@@ -276,7 +276,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
     __shared__ int sidx[16], ebuf[64];
     __shared__ uint32_t kbuf[64];
     __shared__ uint64_t etab[32];
-    __shared__ int qctr, ndone, routed, inited;
+    __shared__ int qctr, ndone, routed, nrouted, inited;
 
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int o = lane >> 3, p = lane & 7;
@@ -299,7 +299,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
     const int n_setup = G53_DT_NW - 1 - nR;        /* waves that set up the workgroup's LDS */
 
     G53_TTRACE(0);
-    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; inited = 0; }
+    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; nrouted = 0; inited = 0; }
     __syncthreads();
     /* router rows first: waves 0 .. nR-1 take rows b, b + G, ... */
     g53_u4 cr[8];
@@ -378,15 +378,21 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
             __builtin_amdgcn_wave_barrier();
         } else if (a.NE <= 64 * 5)
             ok = g53_route_wave<5>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx, sw, kbuf, ebuf,
-                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin);
+                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted);
         else
             ok = g53_route_wave<G53_DEC_MAXNE / 64>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch,
-                                                    sidx, sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin);
+                                                    sidx, sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted);
         if (!ok) {                                    /* scores missing: no routed slots */
             if (lane == 0) g53_flag_err(a.err, 1);
             if (lane < K) { sidx[lane] = -1; sw[lane] = 0.0f; }
             __builtin_amdgcn_s_waitcnt(0xc07f);
             __builtin_amdgcn_wave_barrier();
+        }
+        /* every slot handed over (given routing, missing scores, fewer selectable experts) */
+        G53_CBAR();
+        if (lane == 0) {
+            const int have = g53_lds_ld(&nrouted);
+            if (have < K) (void)g53_lds_add(&nrouted, K - have);
         }
         /* the routing is handed over as the chosen experts' indices; every task looks its
          * descriptor up itself */
@@ -429,8 +435,8 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
         else if (t < i_rg) { s = K; is_g = false; idx = t - i_sd; }
         else if (t < i_rd) { s = (t - i_rg) / ng; is_g = true; idx = (t - i_rg) - s * ng; }
         else { s = (t - i_rd) / nd; is_g = false; idx = (t - i_rd) - s * nd; }
-        if (s < K && g53_lds_ld(&routed) == 0) {
-            if (!g53_wait_lds(&routed, 1) && lane == 0) g53_flag_err(a.err, 1);
+        if (s < K && g53_lds_ld(&nrouted) <= s) {          /* slot s is chosen: its index is in */
+            if (!g53_wait_lds(&nrouted, s + 1) && lane == 0) g53_flag_err(a.err, 1);
         }
         /* the slot's descriptor: the shared expert's in LDS; a routed one from the staged
          * table (or memory) by the chosen index; an unusable one is flagged and skipped */
@@ -572,6 +578,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
             /* every contribution of the workgroup's rows is in: the combine (reference
              * :1329-1340), double in slot order, then the shared expert in float */
             G53_CBAR();
+            if (g53_lds_ld(&routed) == 0 && !g53_wait_lds(&routed, 1) && lane == 0) g53_flag_err(a.err, 1);
             if (lane < n_do * 8) {
                 double acc = 0.0;
                 for (int j = 0; j < K; j++) acc = acc + (double)sw[j] * (double)cvals[lane][j];

@@ -21,6 +21,8 @@ int g53h_decode_fused(float *out, const float *x, const G53hMoeLayer *L, int *id
 int g53h_decode_tiled(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out,
                       const int *idx_in, const float *w_in);
 int g53h_decode_tiled_grid(void);
+int g53h_decode_mtiled(float *out, const float *x, const G53hMoeLayer *L, int *idx_out, float *w_out,
+                       const int *idx_in, const float *w_in);
 int g53h_grouped_use(const G53hMoeLayer *L, int T);
 int g53h_swiglu_split(float *y, const float *g, const float *u, long m, float limit);
 

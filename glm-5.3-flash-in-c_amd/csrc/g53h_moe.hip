@@ -333,7 +333,8 @@ extern "C" int g53h_moe_routed_given(float *out, const float *x, int T, const G5
     if (g53h_ready() || g53_check_layer(L, T)) return -1;
     if (T == 0) return 0;
     if (T == 1 && L->tiled) {                    /* one launch that skips the routing */
-        const int r = g53h_decode_tiled(out, x, L, nullptr, nullptr, idx, wts);
+        const int r = L->tiled == 2 ? g53h_decode_mtiled(out, x, L, nullptr, nullptr, idx, wts)
+                                    : g53h_decode_tiled(out, x, L, nullptr, nullptr, idx, wts);
         if (r <= 0) return r;
     }
     if (L->tiled) return g53_tiled_refused("g53h_moe_routed_given", T);
@@ -374,8 +375,9 @@ extern "C" int g53h_moe(float *out, const float *x, int T, const G53hMoeLayer *L
     if (T == 0) return 0;
     if (!L->router || !L->bias) return g53h_fail("g53h_moe: no router");
     if (T == 1) {                                    /* single-token decode: one fused launch */
-        const int r = L->tiled ? g53h_decode_tiled(out, x, L, idx_out, w_out, nullptr, nullptr)
-                               : g53h_decode_fused(out, x, L, idx_out, w_out);
+        const int r = L->tiled == 2 ? g53h_decode_mtiled(out, x, L, idx_out, w_out, nullptr, nullptr)
+                      : L->tiled  ? g53h_decode_tiled(out, x, L, idx_out, w_out, nullptr, nullptr)
+                                  : g53h_decode_fused(out, x, L, idx_out, w_out);
         if (r <= 0) return r;
     }
     if (g53h_grouped_use(L, T)) return g53h_moe_grouped(out, x, T, L, idx_out, w_out);

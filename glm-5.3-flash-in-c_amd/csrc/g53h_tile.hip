@@ -103,3 +103,65 @@ extern "C" int g53h_tile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int
     }
     return 0;
 }
+
+/* ---------------------------------------------------------- MFMA-tiled layout ---- */
+/* The same 1 KB units (8 rows x 128 columns at ((r / 8) * (cols / 128) + c / 128) KB), with the
+ * bytes inside a unit in the order the matrix cores take them (G53H_MAT_MTILED): column
+ * c = 32 g + 16 i + j of unit row m sits at i * 512 + (8 g + m) * 16 + j. Sixteen-byte piece q
+ * of a unit is (i, g, m) = (q / 32, (q / 8) % 4, q % 8). */
+namespace {
+
+__host__ __device__ inline void g53_mtile_piece(long q, int nb, int &row, int &col0)
+{
+    const long u = q >> 6;
+    const int pc = (int)(q & 63), i = pc >> 5, g = (pc >> 3) & 3, m = pc & 7;
+    row = (int)(u / nb) * 8 + m;
+    col0 = (int)(u % nb) * 128 + 32 * g + 16 * i;
+}
+
+__global__ void __launch_bounds__(256) k_mtile_f8(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                  int cols, long npc, int inverse)
+{
+    const long q = (long)blockIdx.x * 256 + threadIdx.x;
+    if (q >= npc) return;
+    int row, c0;
+    g53_mtile_piece(q, cols / 128, row, c0);
+    uint4 *rm = (uint4 *)(inverse ? dst : src) + ((size_t)row * cols + c0) / 16;
+    uint4 *tl = (uint4 *)(inverse ? src : dst) + q;
+    if (inverse) *rm = *tl;
+    else *tl = *rm;
+}
+
+} /* namespace */
+
+int g53h_mtile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse, hipStream_t s)
+{
+    if (g53h_ready() || g53_tile_shape(rows, cols)) return -1;
+    if (dst_d == src_d) return g53h_fail("g53h_mtile_f8: in-place conversion is not supported");
+    const long npc = (long)rows * cols / 16;
+    hipLaunchKernelGGL(k_mtile_f8, dim3((unsigned)((npc + 255) / 256)), dim3(256), 0, s, dst_d, src_d, cols, npc,
+                       inverse);
+    G53_LAUNCHED("k_mtile_f8");
+    return 0;
+}
+
+extern "C" int g53h_mtile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse)
+{
+    if (g53h_ready()) return -1;
+    return g53h_mtile_f8_on(dst_d, src_d, rows, cols, inverse, g53h_stream());
+}
+
+extern "C" int g53h_mtile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse)
+{
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128 || dst == src) return -1;
+    const long npc = (long)rows * cols / 16;
+    for (long q = 0; q < npc; q++) {
+        int row, c0;
+        g53_mtile_piece(q, cols / 128, row, c0);
+        for (int j = 0; j < 16; j++) {
+            if (inverse) dst[(size_t)row * cols + c0 + j] = src[16 * q + j];
+            else dst[16 * q + j] = src[(size_t)row * cols + c0 + j];
+        }
+    }
+    return 0;
+}

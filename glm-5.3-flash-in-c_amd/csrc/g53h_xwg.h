@@ -126,12 +126,16 @@ extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
  * tag carries this launch's epoch. Each lane sorts its keys; K rounds then take the wave
  * maximum of the lanes' first untaken keys (the lowest expert index among equal ones). sidx[j] = -1
  * where fewer than K experts are selectable (the reference aborts there; bit 2 of the error
- * flags is then set). Returns false when the scores did not all arrive in time. */
+ * flags is then set). Returns false when the scores did not all arrive in time. With nrouted
+ * (an LDS counter), slot j is handed over as soon as its round ends: the counter reaches j + 1
+ * once sidx[j] (and its pre-normalisation score in sw[j]) is written, and K at the end; the
+ * normalised weights are final only when the function returns. */
 template <int NV>
 __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float *bias, int NE, int K, int norm_topk,
                                                float routed_scale, unsigned epoch, int *sidx, float *sw,
                                                uint32_t *kbuf, int *ebuf, int *err, int lane, g53_u64 &t_seen,
-                                               int &n_polls, g53_u64 &t_tau, g53_u64 &t_rank, int limit)
+                                               int &n_polls, g53_u64 &t_tau, g53_u64 &t_rank, int limit,
+                                               int *nrouted = nullptr, int *seenf = nullptr)
 {
     const __amdgpu_buffer_rsrc_t rs = g53_rsrc(score);
     float scv[NV];
@@ -181,6 +185,7 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
         }
     }
     t_seen = __builtin_amdgcn_s_memrealtime();
+    if (seenf && lane == 0) (void)g53_lds_add(seenf, 1);     /* every score is in */
     }
     uint32_t key[NV];
 #pragma unroll
@@ -225,6 +230,10 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
         const int e = __builtin_amdgcn_readlane(hv, win);
         const float wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(hs), win));
         if (lane == 0) { sidx[j] = e; sw[j] = wsc; }
+        if (pass == 1 && nrouted && lane == 0) {    /* slot j is known: its tasks may start */
+            G53_CBAR();
+            (void)g53_lds_add(nrouted, 1);
+        }
         hp += lane == win;                                /* the winner moves to its next key */
         hk = 0u;
 #pragma unroll
@@ -236,6 +245,10 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
     t_tau = __builtin_amdgcn_s_memrealtime();
     if (lane == 0)
         for (int j = pos; j < K; j++) { sidx[j] = -1; sw[j] = 0.0f; }
+    if (nrouted && lane == 0 && pos < K) {
+        G53_CBAR();
+        (void)g53_lds_add(nrouted, K - pos);
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
     t_rank = __builtin_amdgcn_s_memrealtime();

@@ -207,6 +207,9 @@ _SIGS = {
     "g53h_d2h_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_moe_decode_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(G53hMoeLayer), C.c_void_p, C.c_void_p]),
     "g53h_set_tiled_decode_trace": (C.c_int, [C.c_void_p]),
+    "g53h_set_mfma_decode_trace": (C.c_int, [C.c_void_p]),
+    "g53h_mtile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "g53h_mtile_f8_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "g53h_tile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "g53h_untile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "g53h_tile_f8_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),

@@ -137,16 +137,20 @@ class DeviceLayer:
 
     tiled: bool = False
     i4: bool = False
+    mfma: bool = False
 
     @classmethod
-    def build(cls, sp: LayerSpec, n_experts_present=None, tiled=False, i4=False):
+    def build(cls, sp: LayerSpec, n_experts_present=None, tiled=False, i4=False, mfma=False):
         """tiled: store every expert's codes octet-tiled (G53H_MAT_TILED), the layout the decode
         kernel k_dec_tiled streams; the values are the same seeded codes either way.
+        mfma: MFMA-tiled instead (G53H_MAT_MTILED), the layout of k_dec_mfma.
         i4: re-quantise every routed expert on the device into the reference's int4 format
         (G53H_MAT_I4: levels, and one step per row and 64 columns; the reference's
         --experts int4), the shared expert staying FP8; the layer then has block_c 0."""
-        assert not (tiled and i4)
+        assert not (tiled and i4) and not (mfma and (tiled or i4))
         self = cls(sp)
+        self.mfma = bool(mfma)
+        tiled = tiled or mfma
         self.tiled = bool(tiled)
         self.i4 = bool(i4)
         E, I, NE = sp.E, sp.I, sp.NE
@@ -195,9 +199,12 @@ class DeviceLayer:
                 gen = stage.ptr if tile else w
                 check(L.g53h_synth_f8(gen, s, r, c, sp.br, sp.bc, sp.seed, strm, C.c_float(sp.expert_sigma)),
                       "g53h_synth_f8")
-                if tile:
+                if tile and self.mfma:
+                    check(L.g53h_mtile_f8(w, gen, r, c, 0), "g53h_mtile_f8")
+                elif tile:
                     check(L.g53h_tile_f8(w, gen, r, c), "g53h_tile_f8")
-                mats.append(G53hMat(w, s, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, 2 if tile else 0))
+                flag = (8 if self.mfma else 2) if tile else 0
+                mats.append(G53hMat(w, s, r, c, sp.br, sp.bc, (c + sp.bc - 1) // sp.bc, flag))
             descs[i] = G53hExpert(*mats)
         self.experts = descs
         self.table = DevBuf.from_array(np.frombuffer(bytes(descs), np.uint8))
@@ -211,7 +218,7 @@ class DeviceLayer:
             routed_scale=sp.routed_scale, swiglu_limit=sp.limit, router=self.router.ptr, router_dt=1,
             bias=self.bias.ptr, experts=self.table.ptr,
             shared=(self.table.ptr + NE * C.sizeof(G53hExpert)) if sp.shared else None,
-            block_c=0 if self.i4 else sp.bc, tiled=1 if self.tiled else 0)
+            block_c=0 if self.i4 else sp.bc, tiled=(2 if self.mfma else 1) if self.tiled else 0)
         check(L.g53h_sync(), "g53h_sync")
         del stage
         return self
@@ -235,6 +242,10 @@ class DeviceLayer:
             if m.flags & 2:                       # tiled in HBM: the row-major codes for the oracle
                 rm = np.empty_like(w)
                 assert lib().g53h_tile_f8_host(rm.ctypes.data, w.ctypes.data, m.rows, m.cols, 1) == 0
+                w = rm
+            elif m.flags & 8:                     # MFMA-tiled
+                rm = np.empty_like(w)
+                assert lib().g53h_mtile_f8_host(rm.ctypes.data, w.ctypes.data, m.rows, m.cols, 1) == 0
                 w = rm
             out.append((w, s))
         return out

@@ -66,6 +66,13 @@ int         g53h_mem_info(size_t *free_b, size_t *total_b);
  *               accumulators of one row (src/core/glm53f_ops.c:185-228), in order. */
 #define G53H_MAT_DROPPED 1      /* on an expert's gate: the expert failed to load             */
 #define G53H_MAT_TILED   2      /* codes in the octet-tiled layout                            */
+/* MFMA-tiled (rows a multiple of 8, cols of 128, 128-column blocks): the octet-tiled units,
+ * with the bytes inside a unit in the operand order of the FP8 matrix cores: column
+ * c = 32 g + 16 i + j (g < 4, i < 2, j < 16) of unit row m at byte i * 512 + (8 g + m) * 16 + j.
+ * One 64-lane load of 16 bytes per lane reads half a unit, and lane 8 g + m of the two halves
+ * holds the 32 consecutive columns 32 g .. 32 g + 31 of row m. The decode kernel k_dec_mfma
+ * streams it (results within the north-star tolerance, not bit-exact). */
+#define G53H_MAT_MTILED  8
 /* The reference's int4 format (GLM53F_WI4, include/glm53f/glm53f.h:115-125): w holds packed
  * levels [rows][cols / 2] (element (i, j) is nibble j % 2 of byte i * cols / 2 + j / 2, the even
  * column in the low nibble, minus 8), s one fp32 step per row and group of bc columns,
@@ -153,7 +160,8 @@ typedef struct {
     int               block_c;      /* FP8 column block of every expert matrix (128 takes the
                                        tiled kernels; any other value the generic ones)     */
     int               tiled;        /* 1: every expert matrix (routed and shared) is in the
-                                       octet-tiled layout (G53H_MAT_TILED), 0: row-major     */
+                                       octet-tiled layout (G53H_MAT_TILED), 2: MFMA-tiled
+                                       (G53H_MAT_MTILED), 0: row-major                       */
     /* Experts in the int4 format (G53H_MAT_I4, per matrix) need block_c = 0 and tiled = 0: the
        row-wave kernels then take them (and any FP8 matrix, such as the shared expert, in the
        same layer; an octet-tiled one streams fastest), exactly as glm53f_mm on a GLM53F_WI4
@@ -273,6 +281,7 @@ int g53h_inject_errors(int word, int bits);
  * record 100 MHz timestamps at their phase boundaries; NULL turns it off. */
 int g53h_set_decode_trace(void *dev_buf);
 int g53h_set_tiled_decode_trace(void *dev_buf);   /* the same for the octet-tiled kernel   */
+int g53h_set_mfma_decode_trace(void *dev_buf);    /* the same for the MFMA-tiled kernel    */
 
 /* ------------------------------------------------------------- code layouts ---- */
 /* Row-major FP8 codes [rows][cols] -> octet-tiled (see G53hMat), and back; stream-ordered on
@@ -281,6 +290,9 @@ int g53h_set_tiled_decode_trace(void *dev_buf);   /* the same for the octet-tile
 int g53h_tile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols);
 int g53h_untile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols);
 int g53h_tile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse);
+/* The same for the MFMA-tiled layout (G53H_MAT_MTILED); inverse != 0 converts back. */
+int g53h_mtile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse);
+int g53h_mtile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse);
 
 /* -------------------------------------------------------- checks and inputs ---- */
 /* y[i] = expf(x[i]) by the device restatement of glibc's expf (for exhaustive checks). */

@@ -120,3 +120,44 @@ def test_tiled_decode_absent_and_unusable_experts(L):
     assert L.g53h_decode_errors() == 8
     oracle_check(layer, x, out.download(np.float32).reshape(1, sp.E), idd.download(np.int32).reshape(1, sp.K),
                  wd.download(np.float32).reshape(1, sp.K), drop=(gone, bad, rowmajor))
+
+
+def test_tiled_decode_ties(L, layers):
+    """Equal choice values (identical router rows and biases): the reference's arg-max rounds
+    take the lower expert index first (src/core/glm53f_ops.c:961-969, strict '>'). One tied
+    group sits at the top of the ranking, one straddles the top-k boundary, so both the order
+    of the slots and which of the tied experts make the cut are checked against the oracle."""
+    _, base = layers
+    sp = base.sp
+    x = S.x_host(sp, 1, batch=77)
+    _, idx0, _ = run_layer(base, x, 1)
+    top, cut = int(idx0[0][0]), int(idx0[0][sp.K - 3])
+    chosen = set(int(e) for e in idx0[0])
+    free = [e for e in range(sp.NE) if e not in chosen]
+    grp_top = [free[0], free[len(free) // 2], top]           # ties with the first choice
+    grp_cut = [free[1], free[-1], cut]       # ties with the third-last: shifted two places by grp_top
+    rf, bf = base.router_f32.copy(), base.bias_f32.copy()
+    for grp in (grp_top, grp_cut):
+        for e in grp[:-1]:
+            rf[e] = rf[grp[-1]]
+            bf[e] = bf[grp[-1]]
+    router = DevBuf.from_array((rf.view(np.uint32) >> 16).astype(np.uint16))
+    bias = DevBuf.from_array(bf)
+    lay = glm53h.G53hMoeLayer.from_buffer_copy(bytes(base.layer))
+    lay.router, lay.bias = router.ptr, bias.ptr
+    xd = DevBuf.from_array(x)
+    out, idd, wd = DevBuf(sp.E * 4), DevBuf(sp.K * 4), DevBuf(sp.K * 4)
+    say("tiled decode with tied choices", grp_top, grp_cut)
+    check(L.g53h_moe(out.ptr, xd.ptr, 1, C.byref(lay), idd.ptr, wd.ptr), "g53h_moe")
+    glm53h.sync()
+    assert L.g53h_decode_errors() == 0
+    idx = idd.download(np.int32).reshape(1, sp.K)
+    mats = {int(e): base.fetch_expert(int(e)) for e in idx[0]}
+    want, wi, ww = O.moe(O.oracle(), x, sp, rf, bf, mats, base.fetch_expert("shared"))
+    assert np.array_equal(idx, wi), (idx, wi)
+    assert same(wd.download(np.float32).reshape(1, sp.K), ww)
+    assert same(out.download(np.float32).reshape(1, sp.E), want)
+    # the ties did shape the selection: the top group fills the first three slots in index order
+    assert list(wi[0][:3]) == sorted(grp_top), wi[0]
+    # the cut group now holds places K .. K + 2: only its lowest index is taken, in the last slot
+    assert [int(e) for e in wi[0] if int(e) in grp_cut] == [min(grp_cut)] and int(wi[0][-1]) == min(grp_cut), wi[0]

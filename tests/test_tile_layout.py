@@ -60,3 +60,35 @@ def test_tree_pairing():
     assert level1 == {frozenset(s) for s in ((0, 4), (2, 6), (1, 5), (3, 7))}
     level2 = {frozenset(acc[q] for q in range(8) if q >> 2 == p >> 2) for p in range(8)}
     assert level2 == {frozenset((0, 4, 2, 6)), frozenset((1, 5, 3, 7))}
+
+
+def mtile(a, rows, cols, inverse=0):
+    out = np.empty_like(a)
+    assert glm53h.lib().g53h_mtile_f8_host(out.ctypes.data, a.ctypes.data, rows, cols, inverse) == 0
+    return out
+
+
+def test_mfma_tiled_round_trip_and_operand_order():
+    """MFMA-tiled units (G53H_MAT_MTILED): the same 1 KB unit grid as the octet-tiled layout, and
+    lane 8 g + m of the unit's two 512-byte halves holds the 32 consecutive columns 32 g .. 32 g + 31
+    of row m (16 in each half): the A operand of one 16 x 128 FP8 matrix-core tile."""
+    rng = np.random.default_rng(2)
+    for rows, cols in [(8, 128), (16, 256), (40, 640)]:
+        a = rng.integers(0, 256, rows * cols, dtype=np.uint8)
+        t = mtile(a, rows, cols)
+        assert not np.array_equal(t, a)
+        assert np.array_equal(mtile(t, rows, cols, 1), a)
+    rows, cols = 16, 256
+    r = np.repeat(np.arange(rows), cols)
+    c = np.tile(np.arange(cols), rows)
+    tr = mtile(r.astype(np.uint8), rows, cols).reshape(rows // 8, cols // 128, 2, 4, 8, 16)
+    tc = mtile((c % 128).astype(np.uint8), rows, cols).reshape(rows // 8, cols // 128, 2, 4, 8, 16)
+    tb = mtile((c // 128).astype(np.uint8), rows, cols).reshape(rows // 8, cols // 128, 2, 4, 8, 16)
+    for o8 in range(rows // 8):
+        for b in range(cols // 128):
+            for g in range(4):
+                for m in range(8):
+                    lane_bytes = np.concatenate([tc[o8, b, 0, g, m], tc[o8, b, 1, g, m]])
+                    assert np.array_equal(lane_bytes, np.arange(32 * g, 32 * g + 32))
+                    assert np.all(tr[o8, b, :, g, m] == o8 * 8 + m)
+                    assert np.all(tb[o8, b, :, g, m] == b)
