@@ -197,7 +197,8 @@ def bench_grouped(a):
     T = 64 if cfg == 3 else 2048
     steps = a.steps if a.steps != 400 else (200 if cfg == 3 else 30)
     warm = a.warmup if a.warmup != 50 else 5
-    layer = S.DeviceLayer.build(sp, tiled=a.layout == "tiled")
+    lay = "tiled" if a.layout == "mfma" else a.layout      # the grouped kernels read octet-tiled experts
+    layer = S.DeviceLayer.build(sp, tiled=lay == "tiled")
     nb = 4
     xs = [S.x_host(sp, T, batch=b) for b in range(nb)]
     xd = [DevBuf.from_array(x) for x in xs]
@@ -253,7 +254,7 @@ def bench_grouped(a):
         "config": {"workload": (f"BASELINE config 3: batched decode, {T} tokens x top-8, Zipf(1.1) popularity"
                                 if cfg == 3 else f"BASELINE config 4: prefill, {T} tokens, uniform routing, + shared"),
                    "tokens": T, "token_batches_cycled": nb, "unique_routed_experts": D,
-                   "expert_layout": a.layout, "parallelism": "single GPU"},
+                   "expert_layout": lay, "parallelism": "single GPU"},
         "tokens_per_s": round(T / (ms * 1e-3), 1),
         "tflops": round(tflops, 2),
         "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
@@ -599,9 +600,10 @@ def main():
     ap.add_argument("--stack-layers", type=int, default=42,
                     help="config 5: layers in the stack (42 is BASELINE's; fewer, e.g. 24, fit every expert in the "
                          "200 GB cache, which isolates the per-layer cost from host reads)")
-    ap.add_argument("--layout", default="tiled", choices=["tiled", "rowmajor"],
-                    help="expert code layout in HBM: octet-tiled (the cache's slots; k_dec_tiled at config 2) or row-major "
-                         "(k_dec_layer at config 2)")
+    ap.add_argument("--layout", default="mfma", choices=["mfma", "tiled", "rowmajor"],
+                    help="config 2: expert code layout in HBM: MFMA-tiled (k_dec_mfma, FP8 matrix cores, outputs "
+                         "within the path's tolerance), octet-tiled (the cache's slots; k_dec_tiled, bit-exact) or "
+                         "row-major (k_dec_layer, bit-exact); configs 3-4: tiled or rowmajor")
     ap.add_argument("--experts", default="fp8", choices=["fp8", "int4"],
                     help="config 2: routed experts as the checkpoint's FP8 (the metric) or re-quantised to the "
                          "reference's int4 format (its --experts int4 mode; the row-wave kernels)")
@@ -618,9 +620,10 @@ def main():
     L = glm53h.init(0)
     sp = S.spec(2)
     i4 = a.experts == "int4"
+    mfma = a.layout == "mfma" and not i4
     tiled = a.layout == "tiled" and not i4
-    kname = "k_rows" if i4 else ("k_dec_tiled" if tiled else "k_dec_layer")
-    layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4)
+    kname = "k_rows" if i4 else ("k_dec_mfma" if mfma else ("k_dec_tiled" if tiled else "k_dec_layer"))
+    layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4, mfma=mfma)
     cp = Copies(layer)
     x = S.x_host(sp, NTOK, batch=0)
     xs = DevBuf.from_array(x)
@@ -673,8 +676,27 @@ def main():
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
-    prefill = None if (i4 or a.no_prefill) else prefill_beside(L, layer, sp)
-    batched = None if (i4 or a.no_prefill) else batched_beside(L, layer)
+    # the bit-exact decode kernel on the octet-tiled copy of the same layer, and the grouped
+    # kernels' configs 3 and 4 (they read octet-tiled or row-major experts)
+    exact, olayer = None, layer
+    if mfma:
+        olayer = S.DeviceLayer.build(sp, tiled=True)
+        ocp = Copies(olayer)
+        run_steps(L, ocp, xs, outs, sp.E, a.warmup)
+        glm53h.sync()
+        check(L.g53h_mark(), "mark")
+        run_steps(L, ocp, xs, outs, sp.E, a.steps)
+        check(L.g53h_mark(), "mark")
+        ex_us = L.g53h_elapsed_ms() * 1e3 / a.steps
+        if L.g53h_decode_errors():
+            sys.exit("the bit-exact decode kernel reported error flags")
+        ex_gbps = ((sp.K + 1) * sp.expert_bytes() + sp.NE * sp.E * 2 + sp.NE * 4) / (ex_us * 1e-6) / 1e9
+        exact = {"kernel": "k_dec_tiled", "parity": "bit-exact with the reference", "steps": a.steps,
+                 "us_per_layer": round(ex_us, 2), "achieved_GBps": round(ex_gbps, 1),
+                 "hbm_peak_frac": round(ex_gbps / HBM_PEAK_GBPS, 4)}
+        del ocp
+    prefill = None if (i4 or a.no_prefill) else prefill_beside(L, olayer, sp)
+    batched = None if (i4 or a.no_prefill) else batched_beside(L, olayer)
     traffic = None                      # HBM bytes per launch from the committed counter summary
     tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 else ''}_traffic.json")
     if os.path.exists(tp):
@@ -697,6 +719,8 @@ def main():
                                "moe_inter 2048, 288 experts resident in HBM, top-8 + 1 shared",
                    "tokens_cycled": NTOK, "router_shared_copies": NCOPY,
                    "expert_layout": "int4 row-major" if i4 else a.layout, "routed_experts": a.experts,
+                   "parity": ("routing bit-exact, outputs within 1e-2 abs + 2e-3 rel (FP8 matrix cores)" if mfma
+                              else "bit-exact with the reference"),
                    "parallelism": "single GPU"},
         "hbm_GBps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
@@ -707,6 +731,7 @@ def main():
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dom_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 2)},
         "cpu_baseline": cpu,
+        "bit_exact_config2": exact,
         "batched_config3": batched,
         "prefill_config4": prefill,
     }

@@ -318,13 +318,14 @@ static int g53_check_layer(const G53hMoeLayer *L, int T)
 }
 
 /* Octet-tiled experts are read by the single-token decode kernel k_dec_tiled (released
- * shapes) and the grouped kernels (T >= 2 where the grouped path takes the layer); the
- * per-token kernels of this file assume row-major codes, so any other case is refused. */
+ * shapes) and the grouped kernels (T >= 2 where the grouped path takes the layer), MFMA-tiled
+ * ones by k_dec_mfma only; the per-token kernels of this file assume row-major codes, so any
+ * other case is refused. */
 static int g53_tiled_refused(const char *fn, int T)
 {
-    return g53h_fail("%s: octet-tiled experts are read only by the single-token decode kernel (T = 1, hidden %d, "
+    return g53h_fail("%s: tiled experts are read only by the single-token decode kernels (T = 1, hidden %d, "
                      "inter %d, 128x128 blocks, top-k <= 15, bf16 router or given routing) and the grouped kernels "
-                     "(T >= 2, grouped path on); this call has T = %d", fn, 4096, 2048, T);
+                     "(T >= 2, grouped path on, octet-tiled only); this call has T = %d", fn, 4096, 2048, T);
 }
 
 extern "C" int g53h_moe_routed_given(float *out, const float *x, int T, const G53hMoeLayer *L,

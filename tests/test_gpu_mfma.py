@@ -149,3 +149,14 @@ def test_mfma_decode_absent_and_unusable_experts(L):
     assert L.g53h_decode_errors() == 8
     oracle_check(layer, x, out.download(np.float32).reshape(1, sp.E), idd.download(np.int32).reshape(1, sp.K),
                  wd.download(np.float32).reshape(1, sp.K), "drops", drop=(gone, bad, other))
+
+
+def test_mfma_layer_refuses_batches(L, mlayer):
+    """MFMA-tiled experts are read by the single-token kernel only: a batch is refused with an
+    error, not computed from the wrong byte order."""
+    sp = mlayer.sp
+    x = S.x_host(sp, 2, batch=3)
+    xd, out = DevBuf.from_array(x), DevBuf(2 * sp.E * 4)
+    rc = L.g53h_moe(out.ptr, xd.ptr, 2, C.byref(mlayer.layer), None, None)
+    assert rc != 0
+    assert b"tiled" in glm53h.lib().g53h_error()
