@@ -645,6 +645,8 @@ struct SynthStore {
     int hidden, inter, n_layers, n_experts, n_pool;
     uint8_t *pinned;                 /* n_pool experts: codes g, u, d, scales g, u, d */
     size_t per, off[6];
+    float *kscales = nullptr;        /* optional: per key, scales g, u, d back to back  */
+    size_t kper = 0, koff[3] = {0, 0, 0};
 };
 
 int synth_view(const G53hStore *st, int layer, int expert, Glm53fExpertQ *h)
@@ -658,7 +660,7 @@ int synth_view(const G53hStore *st, int layer, int expert, Glm53fExpertQ *h)
     for (int i = 0; i < 3; i++) {
         Glm53fMat &m = *mats[i];
         m.w = b + s->off[i];
-        m.s = (const float *)(b + s->off[3 + i]);
+        m.s = s->kscales ? s->kscales + (size_t)key * s->kper + s->koff[i] : (const float *)(b + s->off[3 + i]);
         m.dt = GLM53F_WF8;
         m.rows = rows[i]; m.cols = cols[i];
         m.br = 128; m.bc = 128;
@@ -715,10 +717,39 @@ fail:
     return -1;
 }
 
+extern "C" int g53h_store_synth_key_scales(G53hStore *st)
+{
+    SynthStore *s = st ? (SynthStore *)st->ctx : nullptr;
+    if (!s || st->view != synth_view) return g53h_fail("g53h_store_synth_key_scales: not a synthetic store");
+    if (s->kscales) return 0;
+    const int rows[3] = {s->inter, s->inter, s->hidden}, cols[3] = {s->hidden, s->hidden, s->inter};
+    size_t n[3], tot = 0;
+    for (int i = 0; i < 3; i++) {
+        n[i] = (size_t)((rows[i] + 127) / 128) * ((cols[i] + 127) / 128);
+        s->koff[i] = tot;
+        tot += n[i];
+    }
+    const size_t keys = (size_t)s->n_layers * s->n_experts;
+    float *k = (float *)g53h_host_alloc(keys * tot * sizeof(float));
+    if (!k) return g53h_fail("g53h_store_synth_key_scales: cannot allocate %zu bytes of pinned memory", keys * tot * 4);
+    for (size_t key = 0; key < keys; key++) {
+        const uint8_t *b = s->pinned + (key % (size_t)s->n_pool) * s->per;
+        const float f = 1.0f + (float)(key + 1) * (1.0f / 16384.0f);
+        for (int i = 0; i < 3; i++) {
+            const float *src = (const float *)(b + s->off[3 + i]);
+            for (size_t j = 0; j < n[i]; j++) k[key * tot + s->koff[i] + j] = src[j] * f;
+        }
+    }
+    s->kscales = k;
+    s->kper = tot;
+    return 0;
+}
+
 extern "C" void g53h_store_synth_free(G53hStore *st)
 {
     SynthStore *s = (SynthStore *)st->ctx;
     if (s) {
+        if (s->kscales) g53h_host_free(s->kscales);
         g53h_host_free(s->pinned);
         delete s;
     }

@@ -261,6 +261,7 @@ _SIGS = {
     "g53h_store_synth_init": (C.c_int, [C.POINTER(G53hStore), C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                         C.c_uint64, C.c_float]),
     "g53h_store_synth_free": (None, [C.POINTER(G53hStore)]),
+    "g53h_store_synth_key_scales": (C.c_int, [C.POINTER(G53hStore)]),
     "g53h_lru_trace": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                                  C.c_void_p]),
 }

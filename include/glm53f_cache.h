@@ -153,6 +153,11 @@ int  g53h_cache_is(const Glm53fExpertSrc *src);
 int  g53h_store_synth_init(G53hStore *st, int hidden, int inter, int n_layers, int n_experts, int n_pool,
                            uint64_t seed, float sigma);
 void g53h_store_synth_free(G53hStore *st);
+/* Gives every (layer, expert) key of a synthetic store its own block scales: the pool entry's
+ * scales times 1 + (key + 1) 2^-14, held in pinned memory (6 KB per key at the released
+ * shapes), so no two keys share a payload and a slot handed back for the wrong key changes the
+ * result. Call once, after g53h_store_synth_init. */
+int  g53h_store_synth_key_scales(G53hStore *st);
 
 /* The LRU policy alone on a scripted trace (CPU, no device): ops are
  *   1 L E        get          -> out: rc, was resident (1/0), slot

@@ -3,7 +3,8 @@ src/gpu/glm53f_gpu.c:1020-1041, copies xn to the host, runs glm53f_moe_routed th
 the result back): the drop-in takes x and out in HBM directly, so a HIP trunk calls it on its
 own buffers with no copy of either. The outputs must equal the host-pointer calls bit for bit,
 for a chunk of tokens (host-memory expert source) and for single-token decode through the HBM
-cache."""
+cache, and both must equal the oracle's glm53f_moe / glm53f_moe_routed (the CPU path the
+reference's hand-off runs) on the same inputs, bit for bit."""
 import ctypes as C
 
 import numpy as np
@@ -11,6 +12,7 @@ import pytest
 
 import glm53h
 import glm53h.synth as S
+import oracle_lib as O
 from glm53h import DevBuf, check
 from test_gpu_parity import HostSrc, cfg_struct, fmat, same, say
 
@@ -61,6 +63,8 @@ def test_device_pointers_chunk_and_decode(L):
             say("hand-off with device pointers, T", T, "routed only" if routed else "with shared")
             h, d = both_ways(L, w, cf, x, routed)
             assert same(h, d)
+            want, _, _ = O.moe(O.oracle(), x, sp, W, b, ex, None if routed else sh)
+            assert same(d, want), (T, routed)
     L.glm53f_forget_host_weights()
 
 
@@ -79,12 +83,24 @@ def test_device_pointers_cached_decode(L):
     try:
         assert L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), 40 * 25174016, 2, 0) == 0
         w = moe_w(sp, W, b, sh, cache.src)
+
+        def key_mats(e):
+            q = glm53h.Glm53fExpertQ()
+            assert store.view(C.cast(C.pointer(store), C.c_void_p), 0, e, C.byref(q)) == 0
+            return [(np.frombuffer(C.string_at(m.w, m.rows * m.cols), np.uint8).copy(),
+                     np.frombuffer(C.string_at(m.s, ((m.rows + m.br - 1) // m.br) * m.scols * 4), np.float32).copy())
+                    for m in (q.gate, q.up, q.down)]
+
         for t in range(3):
             x = np.ascontiguousarray(S.x_host(sp, 1, batch=30 + t), np.float32)
+            idx, _ = O.router(O.oracle(), x, sp, W, b)
+            mats = {int(e): key_mats(int(e)) for e in idx[0]}
             for routed in (False, True):
                 say("cached decode with device pointers, token", t, "routed only" if routed else "with shared")
                 h, d = both_ways(L, w, cf, x, routed)
                 assert same(h, d)
+                want, _, _ = O.moe(O.oracle(), x, sp, W, b, mats, None if routed else sh)
+                assert same(d, want), (t, routed)
         assert L.g53h_decode_errors() == 0
     finally:
         L.glm53f_cache_free(C.byref(cache))

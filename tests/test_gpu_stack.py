@@ -2,8 +2,10 @@
 inter 2048, 288 experts, top-8, shared expert) in single-token decode through the drop-in and
 the HBM cache (src/cache/glm53f_cache.c:128-306 is the reference's), with the calibrated
 Zipf(1.1) routing and correlated inputs of the bench and a budget of 40 slots for 2,304
-experts, so reads, evictions and prefetch reads all happen. Sampled outputs equal the oracle's
-bit for bit; every output equals the one from a cache large enough to never evict, without
+experts, so reads, evictions and prefetch reads all happen. Every (layer, expert) key has its
+own payload (the pinned store's codes come from a pool of 24, its block scales are the key's
+own), so a slot handed back for the wrong key changes the output. Every output equals the
+oracle's bit for bit, and equals the one from a cache large enough to never evict, without
 prefetch (the cache decides what is resident when, never what a layer returns)."""
 import ctypes as C
 
@@ -48,6 +50,7 @@ def test_stack_through_cache_with_misses(L):
     say("building the pinned store of", NP, "experts")
     check(L.g53h_store_synth_init(C.byref(store), sp.E, sp.I, NL + 1, sp.NE, NP, sp.seed, C.c_float(sp.expert_sigma)),
           "store")
+    check(L.g53h_store_synth_key_scales(C.byref(store)), "key scales")
 
     def run(slots, n_io, pf):
         cache = glm53h.Glm53fCache()
@@ -91,18 +94,30 @@ def test_stack_through_cache_with_misses(L):
         want, st2 = run(300, 0, 0)
         assert st2["evictions"] == 0
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-        pool = {}
-        for t, l in ((0, 0), (STEPS - 1, NL - 1), (2, 3)):
-            say("oracle check: token", t, "layer", l)
-            idx, _ = O.router(O.oracle(), X[t, l:l + 1], sps[l], W[l], B[l])
-            mats = {}
-            for e in idx[0]:
-                p = (l * sp.NE + int(e)) % NP
-                if p not in pool:
-                    pool[p] = S.expert_host(S.spec(2), p)
-                mats[int(e)] = pool[p]
-            o, oi, _ = O.moe(O.oracle(), X[t, l:l + 1], sps[l], W[l], B[l], mats, sh)
-            assert np.array_equal(oi, idx) and same(got[t, l], o[0])
+        # every output against the oracle, with each key's experts as the store hands them out
+        def key_mats(l, e):
+            q = glm53h.Glm53fExpertQ()
+            assert store.view(C.cast(C.pointer(store), C.c_void_p), l, e, C.byref(q)) == 0
+            out = []
+            for m in (q.gate, q.up, q.down):
+                nsc = ((m.rows + m.br - 1) // m.br) * m.scols
+                w = np.frombuffer(C.string_at(m.w, m.rows * m.cols), np.uint8).copy()
+                sc = np.frombuffer(C.string_at(m.s, nsc * 4), np.float32).copy()
+                out.append((w, sc))
+            return out
+
+        distinct = set()
+        for t in range(STEPS):
+            for l in range(NL):
+                idx, _ = O.router(O.oracle(), X[t, l:l + 1], sps[l], W[l], B[l])
+                mats = {int(e): key_mats(l, int(e)) for e in idx[0]}
+                for e, mm in mats.items():
+                    distinct.add((l, e, float(mm[0][1][0])))
+                o, oi, _ = O.moe(O.oracle(), X[t, l:l + 1], sps[l], W[l], B[l], mats, sh)
+                assert np.array_equal(oi, idx) and same(got[t, l], o[0]), (t, l)
+        say("oracle: all", STEPS * NL, "outputs equal;", len(distinct), "distinct (layer, expert) keys used")
+        # no two keys share a first gate scale, so no two payloads are alike
+        assert len({d[2] for d in distinct}) == len(distinct)
     finally:
         L.g53h_store_synth_free(C.byref(store))
         L.glm53f_forget_host_weights()
