@@ -51,8 +51,8 @@
 #define G53_DM_MAXDO 4
 #define G53_DM_DTAB 24576
 #define G53_DM_ROT 16
-#ifndef G53_DM_QUIET
-#define G53_DM_QUIET 0
+#ifndef G53_DM_PIN
+#define G53_DM_PIN 2                /* blocks between two pins of the block arithmetic     */
 #endif
 #ifndef G53_DM_NPX
 #define G53_DM_NPX 3                /* E4M3 planes of x                                   */
@@ -163,16 +163,20 @@ __device__ __forceinline__ g53_m8i g53_dm_ld(g53_mgv4 *q)
 
 /* One block on the matrix cores: A (the lane's 32 code bytes), B and its scale from LDS; the
  * result times the lane's block scale s added to acc. */
-__device__ __forceinline__ void g53_dm_block(g53_m4f &acc, const g53_m8i &a, const uint8_t *bq, int bscale, float s)
+__device__ __forceinline__ void g53_dm_block(g53_m4f &acc, const g53_m8i &a, const uint8_t *bq, const uint8_t *bs,
+                                             bool bl, float s)
 {
-    const g53_m8i b = *(const g53_m8i *)bq;
+    /* only the lanes of columns 0-2 hold planes: the others pass zeros without reading LDS */
+    g53_m8i b = {0, 0, 0, 0, 0, 0, 0, 0};
+    int bscale = 127;
+    if (bl) {
+        b = *(const g53_m8i *)bq;
+        bscale = *bs;
+    }
     g53_m4f c = {0.0f, 0.0f, 0.0f, 0.0f};
     c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, bscale);
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(c[i], s, acc[i]);
-    /* pin the block's arithmetic here: the compiler would otherwise hoist every block's LDS
-     * operand and sink the matrix work past the loads, keeping all operands live at once */
-    asm volatile("" : "+v"(acc));
 }
 
 /* The sums of the three planes into the lanes of column 0 (lanes 16 g): rows 4 g .. 4 g + 3. */
@@ -212,7 +216,7 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
     __shared__ int sidx[16], ebuf[64];
     __shared__ uint32_t kbuf[64];
     __shared__ uint64_t etab[32];
-    __shared__ int qctr, ndone, routed, nrouted, inited, xready, sready, seen;
+    __shared__ int qctr, ndone, routed, nrouted, inited, xready, sready;
 
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, grp = lane >> 4;
@@ -227,7 +231,7 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
     const int n_setup = G53_DM_NW - 1 - nR;
 
     G53_MTRACE(0);
-    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; nrouted = 0; inited = 0; xready = 0; sready = 0; seen = 0; }
+    if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; nrouted = 0; inited = 0; xready = 0; sready = 0; }
     __syncthreads();
     if (w < nR || w == G53_DM_NW - 1) __builtin_amdgcn_s_setprio(3);
     if (w < nR) {
@@ -305,18 +309,10 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
         G53_MTRACE(160 + w);
     }
     if (w != G53_DM_NW - 1 && !g53_wait_lds(&sready, n_setup) && lane == 0) g53_flag_err(a.err, 1);
-#if G53_DM_QUIET
-    /* no code streams until the routing wave has every score: its reads then meet an idle
-     * memory system */
-    if (w != G53_DM_NW - 1 && !a.idx_in && !g53_wait_lds(&seen, 1) && lane == 0) g53_flag_err(a.err, 1);
-#endif
 
     /* the routing: top-k, weights (reference :945-976), bit for bit */
     if (w == G53_DM_NW - 1) {
-        if (!a.idx_in)
-            for (int e = lane; e < a.NE; e += 64) biasl[e] = a.bias[e];
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
+
         g53_u64 t_seen = 0, t_tau = 0, t_rank = 0;
         int n_polls = 0;
         bool ok = true;
@@ -326,11 +322,11 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
             __builtin_amdgcn_wave_barrier();
         } else if (a.NE <= 64 * 5)
             ok = g53_route_wave<5>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx, sw, kbuf, ebuf,
-                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted, &seen);
+                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted, nullptr, a.bias);
         else
             ok = g53_route_wave<G53_DEC_MAXNE / 64>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch,
                                                     sidx, sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank,
-                                                    a.spin, &nrouted, &seen);
+                                                    a.spin, &nrouted, nullptr, a.bias);
         if (!ok) {
             if (lane == 0) g53_flag_err(a.err, 1);
             if (lane < K) { sidx[lane] = -1; sw[lane] = 0.0f; }
@@ -342,7 +338,6 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
         if (lane == 0) {
             const int have = g53_lds_ld(&nrouted);
             if (have < K) (void)g53_lds_add(&nrouted, K - have);
-            if (g53_lds_ld(&seen) == 0) (void)g53_lds_add(&seen, 1);
         }
         G53_CBAR();
         if (lane == 0) g53_lds_add(&routed, 1);
@@ -441,7 +436,11 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
                     const float sg = __int_as_float(__builtin_amdgcn_readlane(sbits, kb));
                     const float su = __int_as_float(__builtin_amdgcn_readlane(sbits, 16 + kb));
                     /* the result's rows 0-7 (gate) sit in lanes 0-31, rows 8-15 (up) in 32-63 */
-                    g53_dm_block(acc, r[j], bq0 + kb * G53_DM_BB, (int)bs0[kb * 64], grp < 2 ? sg : su);
+                    g53_dm_block(acc, r[j], bq0 + kb * G53_DM_BB, bs0 + kb * 64, m < 3, grp < 2 ? sg : su);
+                    /* pin the arithmetic every G53_DM_PIN blocks: the compiler would otherwise
+                     * hoist every block's LDS operand and sink the matrix work past the loads,
+                     * keeping all operands live at once */
+                    if ((j % G53_DM_PIN) == G53_DM_PIN - 1) asm volatile("" : "+v"(acc));
                     if (k0 + PB < NB) r[j] = g53_dm_ld(q + 64 * (kb + PB));
                 }
             }
@@ -540,7 +539,8 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
 #pragma unroll
             for (int kb = 0; kb < NB; kb++) {
                 const float sd = __int_as_float(__builtin_amdgcn_readlane(sbits, kb));
-                g53_dm_block(acc, r[kb], bq0 + kb * G53_DM_BB, (int)bs0[kb * 64], sd);
+                g53_dm_block(acc, r[kb], bq0 + kb * G53_DM_BB, bs0 + kb * 64, m < 3, sd);
+                if ((kb % G53_DM_PIN) == G53_DM_PIN - 1) asm volatile("" : "+v"(acc));
             }
             v = g53_dm_planesum(acc);
         }

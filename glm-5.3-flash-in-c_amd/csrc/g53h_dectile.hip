@@ -365,10 +365,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
 
     /* the routing: top-k, weights, the chosen descriptors (reference :945-976) */
     if (w == G53_DT_NW - 1) {
-        if (!a.idx_in)
-            for (int e = lane; e < a.NE; e += 64) biasl[e] = a.bias[e];
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
+
         g53_u64 t_seen = 0, t_tau = 0, t_rank = 0;
         int n_polls = 0;
         bool ok = true;
@@ -378,10 +375,10 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
             __builtin_amdgcn_wave_barrier();
         } else if (a.NE <= 64 * 5)
             ok = g53_route_wave<5>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch, sidx, sw, kbuf, ebuf,
-                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted);
+                                   a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted, nullptr, a.bias);
         else
             ok = g53_route_wave<G53_DEC_MAXNE / 64>(a.score, biasl, a.NE, K, a.norm_topk, a.routed_scale, a.epoch,
-                                                    sidx, sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted);
+                                                    sidx, sw, kbuf, ebuf, a.err, lane, t_seen, n_polls, t_tau, t_rank, a.spin, &nrouted, nullptr, a.bias);
         if (!ok) {                                    /* scores missing: no routed slots */
             if (lane == 0) g53_flag_err(a.err, 1);
             if (lane < K) { sidx[lane] = -1; sw[lane] = 0.0f; }

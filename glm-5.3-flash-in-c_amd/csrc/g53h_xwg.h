@@ -129,23 +129,32 @@ extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
  * flags is then set). Returns false when the scores did not all arrive in time. With nrouted
  * (an LDS counter), slot j is handed over as soon as its round ends: the counter reaches j + 1
  * once sidx[j] (and its pre-normalisation score in sw[j]) is written, and K at the end; the
- * normalised weights are final only when the function returns. */
+ * normalised weights are final only when the function returns. With gbias, the selection's
+ * code runs once on dummy values before anything is read (the instruction cache is warm when
+ * the scores arrive), then the bias is copied from gbias into bias (LDS) and the scores read. */
 template <int NV>
 __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float *bias, int NE, int K, int norm_topk,
                                                float routed_scale, unsigned epoch, int *sidx, float *sw,
                                                uint32_t *kbuf, int *ebuf, int *err, int lane, g53_u64 &t_seen,
                                                int &n_polls, g53_u64 &t_tau, g53_u64 &t_rank, int limit,
-                                               int *nrouted = nullptr, int *seenf = nullptr)
+                                               int *nrouted = nullptr, int *seenf = nullptr,
+                                               const float *gbias = nullptr)
 {
     const __amdgpu_buffer_rsrc_t rs = g53_rsrc(score);
     float scv[NV];
-    uint32_t pend = 0;
+    uint32_t pend = (1u << NV) - 1;
+    if (!gbias) {                                /* the first read: stale scores for pass 0 */
+        pend = 0;
 #pragma unroll
-    for (int v = 0; v < NV; v++) {
-        const int e = min(lane + 64 * v, NE - 1);
-        const g53_u64 t = g53_ld_coh64(rs, 8 * e);
-        scv[v] = __uint_as_float((uint32_t)t);
-        if ((unsigned)(t >> 32) != epoch) pend |= 1u << v;
+        for (int v = 0; v < NV; v++) {
+            const int e = min(lane + 64 * v, NE - 1);
+            const g53_u64 t = g53_ld_coh64(rs, 8 * e);
+            scv[v] = __uint_as_float((uint32_t)t);
+            if ((unsigned)(t >> 32) != epoch) pend |= 1u << v;
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < NV; v++) scv[v] = 0.0f;
     }
     int spins = 0;
     int pos = 0;
@@ -155,6 +164,13 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
 #pragma clang loop unroll(disable)
     for (int pass = 0; pass < 2; pass++) {
     if (pass == 1) {
+    if (gbias) {
+        /* pass 0 ran first thing, on zeros and whatever the bias array held (only to bring the
+         * selection's code into the instruction cache); now the bias, then the scores */
+        for (int e = lane; e < NE; e += 64) ((float *)bias)[e] = gbias[e];
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+    }
     /* two reads of the scores in flight at a time, issued a short sleep apart: a score that
      * lands is seen one memory latency later, not up to two */
     g53_u64 ta[NV], tb[NV];
