@@ -503,8 +503,10 @@ struct G53GrpArgs {
     uint64_t *trace;               /* optional: [grid][8] timestamps of each workgroup    */
 };
 
-/* Diagnostics: 100 MHz timestamps of workgroup phases into a.trace when it is set. */
-#define G53_GTRACE(k, v) do { if (a.trace && threadIdx.x == 0) a.trace[(size_t)blockIdx.x * 8 + (k)] = (v); } while (0)
+/* Diagnostics: 100 MHz timestamps of an item's phases into a.trace[item * 8 + k] when it is set
+ * (gti: the item's number). */
+#define G53_GTRACE(k, v) do { if (a.trace && threadIdx.x == 0) a.trace[(size_t)gti * 32 + (k)] = (v); } while (0)
+#define G53_GTRACE_W(k, v) do { if (a.trace && (threadIdx.x & 63) == 0) a.trace[(size_t)gti * 32 + (k)] = (v); } while (0)
 
 /* Item loc of the workgroup's group: the dispatcher deals workgroups round-robin over the 8
  * XCDs, so the workgroups of XCD x (blockIdx.x % 8 == x) share the items blo .. bhi - 1 (a
@@ -535,15 +537,28 @@ __device__ __forceinline__ int g53_grp_claim(int *ctr)
 /* Gate/up + SwiGLU for (tile, block mb of 16*NW intermediate rows). Wave w: A rows 0-15 = gate
  * rows mb*16*NW + w*16 + 0..15, rows 16-31 = the up rows of the same indices, so C registers r
  * and r + 8 of a lane are gate and up of one intermediate row and one position. */
+/* The clamped SwiGLU of src/core/glm53f_ops.c:486-494 (gate clamped from above, up both ways)
+ * with the hardware exponential: the result is rounded to two E4M3 planes (about 8 significant
+ * bits) right after, so the reference's expf to the last bit buys nothing here, and the exact
+ * table method's LDS lookups queue behind the K loop's operand reads of the other waves (about
+ * 3 us per 32 positions). Infinities and NaN follow the reference: sigmoid(-inf) = 0. */
+__device__ __forceinline__ float g53_grp_swiglu(float g, float u, float limit)
+{
+    const float gi = g > limit ? limit : g;
+    const float ui = u > limit ? limit : (u < -limit ? -limit : u);
+    return gi * __frcp_rn(1.0f + __expf(-gi)) * ui;
+}
+
 template <int NW, int NKB>
 __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs a)
 {
     __shared__ __attribute__((aligned(16))) uint8_t xs[G53_GRP_NS * G53_GRP_NPX * G53_GRP_NT * G53_GRP_XST];
-    __shared__ uint64_t etab[32];                        /* the exponential's table (LDS) */
+    __shared__ __attribute__((aligned(16))) uint8_t ao[G53_GRP_NPA * G53_GRP_NT * 128];   /* the item's planes */
+    __shared__ float xil[G53_GRP_NT];                    /* the tile's token scales          */
     __shared__ int flags[2 * G53_GRP_NS];
     __shared__ int claim[2];
+    static_assert(16 * NW == 128, "an item is one 128-row scale block");
     int *ctr = a.ctr + (blockIdx.x & 7);
-    if (threadIdx.x < 32) etab[threadIdx.x] = g53_exp2_tab_dev[threadIdx.x];
     if (threadIdx.x == 0) claim[0] = g53_grp_claim(ctr);
     if (blockIdx.x == 0 && threadIdx.x < 8) a.ctr[8 + threadIdx.x] = 0;   /* the down kernel's */
     const int blo = a.meta[G53_GRP_BGU + (blockIdx.x & 7)], bhi = a.meta[G53_GRP_BGU + (blockIdx.x & 7) + 1];
@@ -551,11 +566,14 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
         __syncthreads();                     /* claim[] written; the previous item is done with LDS */
         int4 tl;
         int mb;
-        G53_GTRACE(0, __builtin_amdgcn_s_memrealtime());
+        const uint64_t t_item = __builtin_amdgcn_s_memrealtime();
         if (!g53_grp_item(a.tiles, blo, bhi, a.I / (16 * NW), claim[kk & 1], tl, mb)) break;
+        const int gti = blo + claim[kk & 1];
+        G53_GTRACE(0, t_item);
         int nxt = 0;
         if (threadIdx.x == 0) nxt = g53_grp_claim(ctr);
         G53_GTRACE(4, (uint64_t)__smid() << 32 | (uint32_t)(tl.y << 8 | tl.z));
+        G53_GTRACE(5, (uint64_t)blockIdx.x << 32 | (uint32_t)(tl.x << 8 | mb));
         const G53hExpert *ex = tl.x < a.NE ? &a.experts[tl.x] : a.shared;
         const bool usable = ex && ex->gate.w != nullptr && g53_grp_desc_ok(*ex, a.E, a.I, a.tiled);
         if (!usable) {                                       /* absent expert: down writes zeros */
@@ -584,14 +602,16 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
         const float *s0 = (const float *)ex->gate.s + (size_t)(r0 / 128) * ex->gate.scols;
         const float *s1 = (const float *)ex->up.s + (size_t)(r0 / 128) * ex->up.scols;
         g53_v16f acc[G53_GRP_NH] = {};
-        /* the token scales of this lane's positions, loaded before the weights stream */
-        float xi[G53_GRP_NH];
-#pragma unroll
-        for (int h = 0; h < G53_GRP_NH; h++) xi[h] = a.xinv[a.tok_of[pos0 + (h * 32 + i < n ? h * 32 + i : 0)]];
+        /* the token scales of the tile's positions into LDS before the weights stream (read in
+         * registers at the end, the compiler would load them there, behind the weights) */
+        if (tid < n) xil[tid] = a.xinv[a.tok_of[pos0 + tid]];
         G53_GTRACE(1, __builtin_amdgcn_s_memrealtime());
         if (threadIdx.x < 2 * G53_GRP_NS) flags[threadIdx.x] = 0;
         if (threadIdx.x == 0) claim[(kk + 1) & 1] = nxt;
         __syncthreads();
+        float xi[G53_GRP_NH];                                /* this lane's positions' scales */
+#pragma unroll
+        for (int h = 0; h < G53_GRP_NH; h++) xi[h] = xil[h * 32 + i];
         int spin_err = 0;
         switch ((n + 31) >> 5) {
         case 1: g53_grp_kloop<NW, G53_GRP_NPX, NKB, 1>(acc, arow, kst, s0, s1, ld, xps, xs, flags, spin_err, lane); break;
@@ -601,28 +621,50 @@ __global__ void __launch_bounds__(64 * NW, G53_GRP_WPC) k_grp_gateup(G53GrpArgs 
         }
         if (spin_err && lane == 0) atomicOr(&a.meta_w[1], G53_GRP_ESPIN);
         G53_GTRACE(2, __builtin_amdgcn_s_memrealtime());
-        /* epilogue: SwiGLU and the activation planes */
+        G53_GTRACE_W(8 + w, __builtin_amdgcn_s_memrealtime());
+        /* epilogue: SwiGLU; the activation planes of the item's 128 rows go to LDS in their final
+         * byte order (the tiled order within the 128-column block when the pass is tiled), then
+         * leave as whole 16-byte pieces: a lane's own bytes are scattered over 64 positions, and
+         * storing them one by one from each lane costs the address unit about 3 us per 32
+         * positions */
 #pragma unroll
         for (int h = 0; h < G53_GRP_NH; h++) {
             const int j = h * 32 + i;
             if (j >= n) continue;
-            const int pos = pos0 + j;
+            uint32_t pk[2][G53_GRP_NPA];
 #pragma unroll
             for (int q = 0; q < 2; q++) {
                 float v[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const int r = q * 4 + k;
-                    v[k] = g53_swiglu1_tab(acc[h][r] * xi[h], acc[h][r + 8] * xi[h], a.limit, etab) * a.aq_scale;
+                    v[k] = g53_grp_swiglu(acc[h][r] * xi[h], acc[h][r + 8] * xi[h], a.limit) * a.aq_scale;
                 }
-                uint32_t pk[G53_GRP_NPA];
-                g53_split_planes<G53_GRP_NPA>(v, pk);
-                const int row = r0 + q * 8 + g * 4;
+                g53_split_planes<G53_GRP_NPA>(v, pk[q]);
+            }
+            /* C register q * 4 + k holds local row w * 16 + q * 8 + g * 4 + k of the block */
 #pragma unroll
-                for (int p = 0; p < G53_GRP_NPA; p++) g53_grp_st4(a.aq + ((size_t)p * a.P + pos) * a.I, row, pk[p], a.tiled);
+            for (int p = 0; p < G53_GRP_NPA; p++) {
+                uint8_t *d = ao + (p * G53_GRP_NT + j) * 128;
+                if (a.tiled) {          /* rows of q = 0 and 1 are neighbouring bytes of one run */
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+                        *(uint16_t *)(d + (g53_grp_tpos(g * 4 + k) & ~15) + 2 * w) =
+                            (uint16_t)(((pk[0][p] >> (8 * k)) & 0xffu) | (((pk[1][p] >> (8 * k)) & 0xffu) << 8));
+                } else {
+                    *(uint32_t *)(d + w * 16 + g * 4) = pk[0][p];
+                    *(uint32_t *)(d + w * 16 + 8 + g * 4) = pk[1][p];
+                }
             }
         }
+        __syncthreads();
+        for (int c = tid; c < n * G53_GRP_NPA * 8; c += 64 * NW) {
+            const int p = c / (n * 8), jq = c - p * n * 8, j = jq >> 3, piece = jq & 7;
+            *(g53_v4i *)(a.aq + ((size_t)p * a.P + pos0 + j) * a.I + mb * 128 + piece * 16) =
+                *(const g53_v4i *)(ao + (p * G53_GRP_NT + j) * 128 + piece * 16);
+        }
         G53_GTRACE(3, __builtin_amdgcn_s_memrealtime());
+        G53_GTRACE_W(16 + w, __builtin_amdgcn_s_memrealtime());
     }
 }
 
@@ -741,8 +783,8 @@ k_grp_combine(float *__restrict__ out, const float *__restrict__ contrib, const 
 static int g_grp_mode = 1;           /* 1: T >= 2 takes this path when the shapes fit */
 static uint64_t *g_grp_trace = nullptr;
 
-/* Diagnostics: with dev_buf != NULL (device, >= gate/up grid x 8 uint64), the gate/up kernel's
- * workgroups record timestamps (100 MHz) of their phases and their CU; NULL turns it off. */
+/* Diagnostics: with dev_buf != NULL (device, >= gate/up items x 8 uint64), the gate/up kernel
+ * records timestamps (100 MHz) of each item's phases, its CU and workgroup; NULL turns it off. */
 extern "C" int g53h_set_grouped_trace(void *dev_buf)
 {
     g_grp_trace = (uint64_t *)dev_buf;

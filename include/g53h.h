@@ -222,8 +222,8 @@ int g53h_grouped_end(float *out_d, const float *w_d);
 int g53h_set_grouped(int on);
 int g53h_grouped_ok(const G53hMoeLayer *L);
 int g53h_grouped_errors(void);
-/* Diagnostics: with dev_buf != NULL (device, at least gate/up grid x 8 uint64), the grouped
- * gate/up kernel's workgroups record 100 MHz timestamps of their phases; NULL turns it off. */
+/* Diagnostics: with dev_buf != NULL (device, at least (gate/up items) x 8 uint64), the grouped
+ * gate/up kernel records 100 MHz timestamps of each item's phases; NULL turns it off. */
 int g53h_set_grouped_trace(void *dev_buf);
 
 /* Single-token decode runs as one persistent launch when the layer has the released shapes
