@@ -527,12 +527,43 @@ def bench_stack(a):
         step(s_)
     check(L.glm53f_cache_sync(C.byref(cache)), "cache sync")
     L.glm53f_cache_reset_stats(C.byref(cache))
+    spec = (C.c_int64 * 3)()
+    L.g53h_speculate_counts(spec)
+    hprof = (C.c_double * 16)()
+    if hasattr(L, "g53h_host_prof"):             # a build with the drop-in's host timers
+        L.g53h_host_prof.argtypes = [C.c_void_p]
+        L.g53h_host_prof(hprof)
     glm53h.sync()
     t0 = time.perf_counter()
     for s_ in range(steps):
         step(warm + s_)
     glm53h.sync()
     dt = time.perf_counter() - t0
+    L.g53h_speculate_counts(spec)
+    ktrace = None
+    if a.decode_trace:          # one more step with the decode kernel's timestamps, per layer call
+        tb = DevBuf(1024 * 192 * 8)                       # up to 1024 workgroups
+        spans, routed = [], []
+        for l in range(NL):
+            tb.zero()
+            L.g53h_set_tiled_decode_trace(tb.ptr)
+            fn(optr, xptr[warm + steps - 1][l], wref[l], cref, 1, None)
+            L.g53h_set_tiled_decode_trace(None)
+            glm53h.sync()
+            t = tb.download(np.uint64).reshape(-1, 192).astype(np.int64)
+            t = t[t[:, 0] > 0]
+            if len(t):
+                end = t[:, :16].max(1)
+                spans.append((end.max() - t[:, 0].min()) / 100.0)
+                routed.append((np.median(t[t[:, 1] > 0, 1]) - t[:, 0].min()) / 100.0 if (t[:, 1] > 0).any() else -1)
+        if spans:
+            ktrace = {"layers": len(spans), "kernel_us_mean": round(float(np.mean(spans)), 2),
+                      "kernel_us_min": round(float(np.min(spans)), 2), "kernel_us_max": round(float(np.max(spans)), 2),
+                      "routing_done_us_median": round(float(np.median(routed)), 2)}
+    if hasattr(L, "g53h_host_prof"):
+        L.g53h_host_prof(hprof)
+        print("[bench] host timers (us per layer call):", " ".join(f"{i}:{hprof[i]:.1f}" for i in range(16)),
+              file=sys.stderr, flush=True)
     us_layer = dt * 1e6 / (steps * NL)
     hits, misses, bg_reads, bg_used = cache.hits, cache.misses, cache.bg_reads, cache.bg_used
     h2d = cache.bytes_read + cache.bg_bytes
@@ -572,6 +603,8 @@ def bench_stack(a):
         "miss_rate": round(misses / max(hits + misses, 1), 4),
         "misses_per_token": round(misses / steps, 2),
         "requests": int(hits + misses), "misses": int(misses),
+        "decode_kernel_trace": ktrace,
+        "speculative_layers": {"done": int(spec[0]), "run_again": int(spec[1]), "not_speculative": int(spec[2])},
         "prefetch_reads": int(bg_reads), "prefetch_used": int(bg_used),
         "h2d_GB": round(h2d / 1e9, 3), "h2d_GBps_avg": round(h2d / dt / 1e9, 2), "h2d_link_GBps": round(link, 2),
         "hbm_GBps_experts": round((K + 1) * eb / (us_layer * 1e-6) / 1e9, 1),
@@ -600,6 +633,9 @@ def main():
     ap.add_argument("--stack-layers", type=int, default=42,
                     help="config 5: layers in the stack (42 is BASELINE's; fewer, e.g. 24, fit every expert in the "
                          "200 GB cache, which isolates the per-layer cost from host reads)")
+    ap.add_argument("--decode-trace", action="store_true",
+                    help="config 5: after the timed steps, one step with the one-launch decode's timestamps "
+                         "(kernel span and routing time per layer call; diagnostic)")
     ap.add_argument("--layout", default="mfma", choices=["mfma", "tiled", "rowmajor"],
                     help="config 2: expert code layout in HBM: MFMA-tiled (k_dec_mfma, FP8 matrix cores, outputs "
                          "within the path's tolerance), octet-tiled (the cache's slots; k_dec_tiled, bit-exact) or "

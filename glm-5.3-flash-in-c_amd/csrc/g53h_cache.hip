@@ -77,6 +77,14 @@ struct Impl {
     uint8_t *stage_demand = nullptr, *stage_prefetch = nullptr;
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
+    /* tiled slots: the descriptor of every key whose read has been seen complete, per layer in
+     * pinned host memory (zero where the key holds no landed slot) and its device copy, which is
+     * uploaded on the compute stream when the layer's entries have changed; a one-launch decode
+     * that routes by itself reads its chosen experts from it */
+    G53hExpert *tab_h = nullptr, *tab_d = nullptr;
+    std::vector<unsigned char> tab_dirty;   /* per layer: tab_h differs from tab_d       */
+    std::vector<int> tab_key;               /* per slot: the key whose entry names it, -1  */
+    std::vector<int> pend;                  /* per layer: reads issued, not yet seen complete */
     std::mutex mu;
     ~Impl()
     {
@@ -133,6 +141,38 @@ void unuse(Impl *m, int slot)
     if (--m->used_refs[u] == 0 && u != m->cur_used) m->used_free.push_back(u);
 }
 
+void view_of(const Glm53fCache *c, const Impl *m, int slot, Glm53fExpertQ *q);
+
+/* The descriptor table: slot's entry (its key's) cleared before the slot is read into again, and
+ * set once its read has been seen complete. */
+void table_clear(Glm53fCache *c, Impl *m, int slot)
+{
+    if (!m->tab_h || m->tab_key[slot] < 0) return;
+    const int key = m->tab_key[slot];
+    memset(&m->tab_h[key], 0, sizeof(G53hExpert));
+    m->tab_dirty[key / c->n_experts] = 1;
+    m->tab_key[slot] = -1;
+}
+
+void table_set(Glm53fCache *c, Impl *m, int slot, int layer, int expert)
+{
+    if (!m->tab_h) return;
+    table_clear(c, m, slot);
+    Glm53fExpertQ q;
+    view_of(c, m, slot, &q);
+    const int key = layer * c->n_experts + expert;
+    G53hExpert &e = m->tab_h[key];
+    G53hMat *d[3] = {&e.gate, &e.up, &e.down};
+    const Glm53fMat *v[3] = {&q.gate, &q.up, &q.down};
+    for (int i = 0; i < 3; i++) {
+        d[i]->w = (const uint8_t *)v[i]->w; d[i]->s = v[i]->s;
+        d[i]->rows = v[i]->rows; d[i]->cols = v[i]->cols; d[i]->br = v[i]->br; d[i]->bc = v[i]->bc;
+        d[i]->scols = v[i]->scols; d[i]->flags = G53H_MAT_TILED;
+    }
+    m->tab_key[slot] = key;
+    m->tab_dirty[layer] = 1;
+}
+
 /* Copies seen complete hand their host bytes back to the store, and the slot they filled no
  * longer needs its landed event waited on. */
 void poll(Glm53fCache *c, Impl *m)
@@ -142,7 +182,11 @@ void poll(Glm53fCache *c, Impl *m)
         Copy &cp = m->inflight[i];
         if (hipEventQuery(cp.ev) == hipSuccess) {
             store_done(m, cp.layer, cp.expert);
-            if (m->gen[cp.slot] == cp.gen) m->landed_ok[cp.slot] = 0;
+            if (m->gen[cp.slot] == cp.gen) {
+                m->landed_ok[cp.slot] = 0;
+                table_set(c, m, cp.slot, cp.layer, cp.expert);
+            }
+            if (m->tab_h) m->pend[cp.layer]--;
             m->pool.push_back(cp.ev);
         } else {
             m->inflight[k++] = cp;
@@ -174,6 +218,7 @@ int issue(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStream_t 
     else if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return 0;
     if (hipEventRecord(ev, s) != hipSuccess) return 0;
     m->inflight.push_back(Copy{ev, layer, expert, background, slot, m->gen[slot]});
+    if (m->tab_h) m->pend[layer]++;
     return 1;
 }
 
@@ -198,6 +243,7 @@ int issue_reads(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStr
             return 0;
         }
     uint8_t *base = m->arena + (size_t)slot * (size_t)c->slot_bytes;
+    table_clear(c, m, slot);
     if (m->used[slot] >= 0) {
         if (hipStreamWaitEvent(s, m->used_ev[m->used[slot]], 0) != hipSuccess) return 0;
         unuse(m, slot);
@@ -407,6 +453,27 @@ void cache_hint(Glm53fExpertSrc *self, int layer, const int *ids, int n)
 
 extern "C" int g53h_cache_is(const Glm53fExpertSrc *src) { return src && src->get == cache_get; }
 
+extern "C" int g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **table_d,
+                                      const G53hExpert **table_h)
+{
+    if (!g53h_cache_is(src)) return -1;
+    Glm53fCache *c = (Glm53fCache *)src;
+    Impl *m = impl_of(c);
+    if (!m || !m->tab_h || layer < 0 || layer >= c->n_layers) return -1;
+    std::lock_guard<std::mutex> g(m->mu);
+    poll(c, m);
+    if (m->pend[layer] > 0) return m->pend[layer];
+    const size_t nb = (size_t)c->n_experts * sizeof(G53hExpert);
+    G53hExpert *h = m->tab_h + (size_t)layer * c->n_experts, *d = m->tab_d + (size_t)layer * c->n_experts;
+    if (m->tab_dirty[layer]) {
+        if (hipMemcpyAsync(d, h, nb, hipMemcpyHostToDevice, g53h_stream()) != hipSuccess) return -1;
+        m->tab_dirty[layer] = 0;
+    }
+    *table_d = d;
+    *table_h = h;
+    return 0;
+}
+
 /* Common set-up once the store is known (m->store or m->ckpt). */
 static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t budget_bytes, int n_io, int i4)
 {
@@ -516,6 +583,16 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
         m->stage_prefetch = (uint8_t *)g53h_alloc(sb);
         ok = m->stage_demand && m->stage_prefetch;
     }
+    if (ok && m->tiled) {
+        const size_t tb = (size_t)c->n_layers * (size_t)c->n_experts * sizeof(G53hExpert);
+        m->tab_h = (G53hExpert *)g53h_host_alloc(tb);
+        m->tab_d = (G53hExpert *)g53h_alloc(tb);
+        ok = m->tab_h && m->tab_d && !g53h_memset(m->tab_d, 0, tb);
+        if (m->tab_h) memset(m->tab_h, 0, tb);
+        m->tab_dirty.assign(c->n_layers, 0);
+        m->tab_key.assign(c->nslot, -1);
+        m->pend.assign(c->n_layers, 0);
+    }
     c->stage = (unsigned char **)(void *)m;
     if (!ok) {
         fprintf(stderr, "glm53f_cache: cannot create the copy events and streams\n");
@@ -600,6 +677,8 @@ extern "C" void glm53f_cache_free(Glm53fCache *c)
         if (m->arena) g53h_free(m->arena);
         g53h_free(m->stage_demand);
         g53h_free(m->stage_prefetch);
+        g53h_free(m->tab_d);
+        g53h_host_free(m->tab_h);
         g53_lru_free(&m->lru);
         delete m;
     }

@@ -94,6 +94,9 @@ struct G53TiledArgs {
     float routed_scale, limit;
     int spin;                      /* polls before a wait on another workgroup gives up */
     g53_u64 *trace;                /* optional: [grid][32] timestamps                    */
+    const uint16_t *nrouter;       /* optional: the next layer's bf16 router [NE][E] and bias, */
+    const float *nbias;            /* whose scores (choice = score + bias) spare waves write */
+    float *nscore, *nchoice;       /* to nscore / nchoice [NE] (the prediction's input)      */
 };
 
 /* A descriptor this kernel can stream: the released shapes, 128 x 128 blocks, every matrix
@@ -290,13 +293,14 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
     const int ng = 2 * n_go, nd = (n_do + 1) >> 1, nslot = hs + K;
     int n_task = 0;
     const int nR = a.idx_in ? 0 : (a.NE > b ? (a.NE - 1 - b) / G + 1 : 0);
+    const int nN = a.nrouter ? (a.NE > b ? (a.NE - 1 - b) / G + 1 : 0) : 0;   /* next-layer rows */
     const int words = (int)(sizeof(G53hExpert) / 4);
 #ifdef G53_DT_NOSTAGE
     const bool dstage = false;
 #else
     const bool dstage = a.NE * (int)sizeof(G53hExpert) <= G53_DT_DTAB;
 #endif
-    const int n_setup = G53_DT_NW - 1 - nR;        /* waves that set up the workgroup's LDS */
+    const int n_setup = G53_DT_NW - 1 - nR - nN;   /* waves that set up the workgroup's LDS */
 
     G53_TTRACE(0);
     if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; nrouted = 0; inited = 0; }
@@ -316,10 +320,23 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
         if (lane == 0) g53_st_tag(a.score + b + w * G, g53_tag(a.epoch, g53_sigmoidf_tab((float)d, g53_exp2_tab_dev)));
         if (w == 0) G53_TTRACE(2);
         __builtin_amdgcn_s_setprio(0);
+    } else if (w < nR + nN) {
+        /* the next layer's router row b + (w - nR) G on the same x: its score and choice for the
+         * prediction (the arithmetic of k_router_scores, bit for bit) */
+        const int e = b + (w - nR) * G;
+        g53_gv4t *q = (g53_gv4t *)(a.nrouter + (size_t)e * G53_DEC_E + lane * 64);
+#pragma unroll
+        for (int k = 0; k < 8; k++) cr[k] = q[k];
+        const double d = g53_router_row(cr, a.x, lane);
+        if (lane == 0) {
+            const float sc = g53_sigmoidf_tab((float)d, g53_exp2_tab_dev);
+            a.nscore[e] = sc;
+            a.nchoice[e] = sc + a.nbias[e];
+        }
     } else if (w < G53_DT_NW - 1) {
         /* the set-up, by the waves between the router rows and the routing wave: every load
          * is issued before the first store into LDS; all waves start once it is done */
-        const int ti = threadIdx.x - 64 * nR, nt = (G53_DT_NW - 1 - nR) * 64;
+        const int ti = threadIdx.x - 64 * (nR + nN), nt = (G53_DT_NW - 1 - nR - nN) * 64;
         constexpr int XPER = 8;                             /* nt >= 128 */
         float4 xv[XPER];
         /* the expert table too, so that the routing picks the chosen descriptors from LDS */
@@ -649,6 +666,17 @@ static void dt_launch(float *out, const float *x, const G53hMoeLayer *L, int *id
     e.err = g53h_errblock() + 1; e.idx_out = idx_out; e.w_out = w_out; e.idx_in = idx_in; e.w_in = w_in;
     e.NE = L->n_experts; e.K = L->topk; e.norm_topk = L->norm_topk; e.epoch = epoch;
     e.spin = g53h_spin_limit(); e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dt_trace;
+    e.nrouter = nullptr; e.nbias = nullptr; e.nscore = e.nchoice = nullptr;
+    G53NextReq *nq = g53h_next_req();
+    const int rows = (L->n_experts + g_dt_grid - 1) / g_dt_grid;
+    /* the next layer's scores by spare waves: a bf16 router on this x, and at least two set-up
+     * waves left (router rows + next rows + the routing wave + 2 <= the workgroup's waves) */
+    if (nq->armed && nq->dt == 1 && nq->x == x && nq->NE == L->n_experts && nq->E == G53_DEC_E &&
+        (idx_in ? 0 : rows) + rows + 3 <= G53_DT_NW) {
+        float *nb = g53h_next_buf();
+        e.nrouter = (const uint16_t *)nq->gate; e.nbias = nq->bias; e.nchoice = nb; e.nscore = nb + 1024;
+        nq->armed = 0;
+    }
     g53h_prof_mark(G53_PROF_START);
     hipLaunchKernelGGL(k_dec_tiled, dim3(g_dt_grid), dim3(G53_DT_NT), 0, g53h_stream(), e);
     g53h_prof_mark(G53_PROF_FUSED);

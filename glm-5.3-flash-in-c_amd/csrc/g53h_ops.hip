@@ -748,3 +748,87 @@ extern "C" int g53h_route_decode(int *idx, float *w, int *nan_flag, int *pred, i
     G53_LAUNCHED("k_route_decode");
     return 0;
 }
+
+/* ------------------------------------------------- speculative decode: next scores, publish ---- */
+static float *g_next = nullptr;          /* [2][1024]: choice (score + bias), then score */
+static G53NextReq g_next_req;
+
+float *g53h_next_buf(void)
+{
+    if (!g_next) g_next = (float *)g53h_alloc(2 * 1024 * sizeof(float));
+    return g_next;
+}
+G53NextReq *g53h_next_req(void) { return &g_next_req; }
+
+extern "C" int g53h_decode_next(const float *x, const void *next_gate, int next_dt, const float *next_bias, int NE,
+                                int E)
+{
+    if (g53h_ready()) return -1;
+    if (NE < 1 || NE > 1024 || !x || !next_gate || !next_bias)
+        return g53h_fail("g53h_decode_next: %d experts (max 1024)", NE);
+    if (!g53h_next_buf()) return -1;
+    g_next_req = G53NextReq{1, x, next_gate, next_dt, next_bias, NE, E};
+    return 0;
+}
+
+extern "C" int g53h_route_next(const float *x, const void *next_gate, int next_dt, const float *next_bias, int NE,
+                               int E)
+{
+    if (g53h_ready()) return -1;
+    if (NE < 1 || NE > 1024) return g53h_fail("g53h_route_next: %d experts (max 1024)", NE);
+    if (!g53h_next_buf()) return -1;
+    hipLaunchKernelGGL(k_router_scores, dim3(NE, 1), dim3(64), 0, g53h_stream(), g_next + 1024, g_next, x, 1,
+                       next_gate, next_dt, next_bias, NE, E);
+    G53_LAUNCHED("k_router_scores");
+    return 0;
+}
+
+/* Wave 0 takes the next layer's top-n (the selection of k_route_decode, src/core/glm53f_ops.c:
+ * 1021-1042), then the workgroup writes the host's copy: idx [K], the NaN flag, pred [n] at
+ * route_off_w; the error words and the output at out_off_w; then the sequence word. */
+__global__ void __launch_bounds__(256) k_dec_publish(unsigned *__restrict__ mb, int slot, unsigned seq,
+                                                     int route_off_w, const int *__restrict__ idx, int K,
+                                                     int *__restrict__ pred, int n, const float *__restrict__ choice,
+                                                     const float *__restrict__ score, int NE, int out_off_w,
+                                                     const uint32_t *__restrict__ out, int nw,
+                                                     const int *__restrict__ errs)
+{
+    if (threadIdx.x < 64 && n > 0) g53_topn_token(0, (int)threadIdx.x, pred, n, choice, NE, score, nullptr);
+    __threadfence_block();
+    __syncthreads();
+    unsigned *r = mb + route_off_w;
+    const int nan = ((errs[0] | errs[1]) & 2) ? 1 : 0;
+    for (int i = threadIdx.x; i < K + 1 + n; i += 256)
+        r[i] = (unsigned)(i < K ? idx[i] : i == K ? nan : pred[i - K - 1]);
+    uint32_t *d = mb + out_off_w;
+    for (int i = threadIdx.x; i < G53H_NERR; i += 256) d[i] = (uint32_t)errs[i];
+    for (int i = threadIdx.x; i < nw; i += 256) d[G53H_NERR + i] = out[i];
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(mb + slot, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+extern "C" int g53h_decode_publish(int slot, unsigned seq, size_t route_off, const int *idx_d, int K, int *pred_d,
+                                   int n, int NE, size_t out_off, const void *out_d, size_t out_bytes)
+{
+    if (g53h_ready()) return -1;
+    if (K < 1 || K > GLM53F_MAX_TOPK_DEV || n < 0 || n > NE || NE < 1 || NE > 1024 || (n > 0 && (!g_next || !pred_d)))
+        return g53h_fail("g53h_decode_publish: topk %d, n %d of %d experts (g53h_route_next first)", K, n, NE);
+    if (g_next_req.armed) {          /* requested, and no decode launch computed them */
+        g_next_req.armed = 0;
+        if (g_next_req.NE != NE ||
+            g53h_route_next(g_next_req.x, g_next_req.gate, g_next_req.dt, g_next_req.bias, g_next_req.NE, g_next_req.E))
+            return g53h_fail("g53h_decode_publish: the next layer's scores (%d experts) cannot be computed", NE);
+    }
+    if (slot < 0 || slot >= G53H_MBOX_SLOTS || route_off % 4 || out_off % 4 || out_bytes % 4 ||
+        route_off < G53H_MBOX_SLOTS * 4 || out_off < G53H_MBOX_SLOTS * 4 ||
+        route_off + 4 * (size_t)(K + 1 + n) > G53H_MBOX_BYTES || out_off + 4 * G53H_NERR + out_bytes > G53H_MBOX_BYTES ||
+        (route_off < out_off + 4 * G53H_NERR + out_bytes && out_off < route_off + 4 * (size_t)(K + 1 + n)))
+        return g53h_fail("g53h_decode_publish: slot %d, routing at %zu, %zu bytes at %zu", slot, route_off, out_bytes,
+                         out_off);
+    hipLaunchKernelGGL(k_dec_publish, dim3(1), dim3(256), 0, g53h_stream(), g53h_mailbox_dev(), slot, seq,
+                       (int)(route_off / 4), idx_d, K, pred_d, n, g_next, g_next + 1024, NE, (int)(out_off / 4),
+                       (const uint32_t *)out_d, (int)(out_bytes / 4), g53h_errblock());
+    G53_LAUNCHED("k_dec_publish");
+    return 0;
+}

@@ -39,6 +39,20 @@ int        *g53h_counters(void);
 /* The layer kernels' error flags, one int each ([0] k_dec_layer, [1] k_dec_tiled, [2] the
  * grouped path), zero at init; g53h_errors_async copies and clears them. */
 int        *g53h_errblock(void);
+/* The next layer's router scores of a decode token (g53h_route_next / g53h_decode_next): the
+ * buffer [2][1024] (choice = score + bias, then score), and the request armed by
+ * g53h_decode_next, which the tiled decode launch takes (its spare waves compute them) or
+ * g53h_decode_publish serves with a launch of its own. */
+struct G53NextReq {
+    int armed;
+    const float *x;
+    const void *gate;
+    int dt;
+    const float *bias;
+    int NE, E;
+};
+float      *g53h_next_buf(void);
+G53NextReq *g53h_next_req(void);
 /* Polls before a wait on another workgroup gives up (g53h_set_spin_limit). */
 int         g53h_spin_limit(void);
 

@@ -22,6 +22,8 @@ static int        *g_counters = nullptr;
 static int        *g_errs = nullptr;   /* [0] k_dec_layer, [1] k_dec_tiled, [2] grouped path   */
 static unsigned   *g_mbox = nullptr;   /* host mailbox: pinned, mapped, written by kernels      */
 static unsigned   *g_mbox_d = nullptr; /* its device address                                    */
+static uint8_t    *g_inbox = nullptr;  /* host inbox: pinned, mapped, read by kernels           */
+static uint8_t    *g_inbox_d = nullptr;
 
 extern "C" int g53h_fail(const char *fmt, ...)
 {
@@ -73,6 +75,9 @@ extern "C" int g53h_init(int device)
     G53_TRY(hipHostMalloc((void **)&g_mbox, G53H_MBOX_BYTES, hipHostMallocMapped | hipHostMallocCoherent));
     memset(g_mbox, 0, G53H_MBOX_BYTES);
     G53_TRY(hipHostGetDevicePointer((void **)&g_mbox_d, g_mbox, 0));
+    G53_TRY(hipHostMalloc((void **)&g_inbox, G53H_INBOX_BYTES, hipHostMallocMapped | hipHostMallocCoherent));
+    memset(g_inbox, 0, G53H_INBOX_BYTES);
+    G53_TRY(hipHostGetDevicePointer((void **)&g_inbox_d, g_inbox, 0));
     G53_TRY(hipDeviceSynchronize());
     if (g53_noalloc_setup(device)) return -1;
     g_device = device;
@@ -91,6 +96,27 @@ int *g53h_errblock(void) { return g_errs; }
 unsigned *g53h_mailbox_dev(void) { return g_mbox_d; }
 
 extern "C" void *g53h_mailbox(void) { return g53h_ready() ? nullptr : (void *)g_mbox; }
+extern "C" void *g53h_inbox(void) { return g53h_ready() ? nullptr : (void *)g_inbox; }
+
+/* 16 bytes per thread from the mapped host inbox into device memory. */
+__global__ void __launch_bounds__(256) k_inbox_fetch(uint4 *__restrict__ dst, const uint4 *__restrict__ src, int n16)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n16) dst[i] = src[i];
+}
+
+extern "C" int g53h_inbox_fetch(void *dst_d, size_t off, size_t bytes)
+{
+    if (g53h_ready()) return -1;
+    if (off % 16 || bytes % 16 || off + bytes > G53H_INBOX_BYTES || ((uintptr_t)dst_d & 15))
+        return g53h_fail("g53h_inbox_fetch: %zu bytes at %zu", bytes, off);
+    if (!bytes) return 0;
+    const int n16 = (int)(bytes / 16);
+    hipLaunchKernelGGL(k_inbox_fetch, dim3((n16 + 255) / 256), dim3(256), 0, g_stream, (uint4 *)dst_d,
+                       (const uint4 *)(g_inbox_d + off), n16);
+    G53_LAUNCHED("k_inbox_fetch");
+    return 0;
+}
 
 extern "C" int g53h_mailbox_wait(int slot, unsigned seq)
 {

@@ -204,6 +204,12 @@ _SIGS = {
     "g53h_mailbox": (C.c_void_p, []),
     "g53h_mailbox_wait": (C.c_int, [C.c_int, C.c_uint]),
     "g53h_publish": (C.c_int, [C.c_int, C.c_uint, C.c_size_t, C.c_void_p, C.c_size_t]),
+    "g53h_inbox": (C.c_void_p, []),
+    "g53h_inbox_fetch": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t]),
+    "g53h_route_next": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int]),
+    "g53h_decode_next": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_int]),
+    "g53h_decode_publish": (C.c_int, [C.c_int, C.c_uint, C.c_size_t, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                                      C.c_int, C.c_size_t, C.c_void_p, C.c_size_t]),
     "g53h_d2h_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "g53h_moe_decode_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(G53hMoeLayer), C.c_void_p, C.c_void_p]),
     "g53h_set_tiled_decode_trace": (C.c_int, [C.c_void_p]),
@@ -250,6 +256,10 @@ _SIGS = {
     "glm53f_cache_report": (None, [C.POINTER(Glm53fCache), C.c_char_p]),
     "glm53f_cache_sync": (C.c_int, [C.POINTER(Glm53fCache)]),
     "g53h_cache_is": (C.c_int, [C.POINTER(Glm53fExpertSrc)]),
+    "g53h_set_speculate": (C.c_int, [C.c_int]),
+    "g53h_speculate_counts": (None, [C.c_void_p]),
+    "g53h_cache_layer_table": (C.c_int, [C.POINTER(Glm53fExpertSrc), C.c_int, C.POINTER(C.c_void_p),
+                                         C.POINTER(C.c_void_p)]),
     "g53h_cache_init_store": (C.c_int, [C.POINTER(Glm53fCache), C.POINTER(G53hStore), C.POINTER(Glm53fCfg),
                                         C.c_int64, C.c_int, C.c_int]),
     "g53h_st_open": (C.c_int, [C.POINTER(Glm53fSt), C.c_char_p, C.c_int]),

@@ -622,6 +622,55 @@ static int shared_tileable(const Glm53fMoeW *w)
     return 1;
 }
 
+/* G53H_NO_SPECULATE (set at the first call) turns the speculative cached layer off: every layer
+ * then routes first and fetches before it computes (a switch of this library, for comparisons). */
+static int g_spec = -1;
+static int spec_enabled(void)
+{
+    if (g_spec < 0) g_spec = getenv("G53H_NO_SPECULATE") ? 0 : 1;
+    return g_spec;
+}
+static int64_t g_spec_n[3];     /* layers: speculative and done, speculative and run again, not */
+/* The last 16 speculative layers' outcomes (bit set: finished by the speculative launch). A
+ * layer speculates while at least half of them finished, and every 16th layer regardless, so
+ * that a cache that misses most of the time (a small budget) pays for few wasted launches. */
+static unsigned g_spec_hist = 0xffffu, g_spec_tick = 0;
+static int spec_worth(void)
+{
+    return __builtin_popcount(g_spec_hist & 0xffffu) >= 8 || (++g_spec_tick & 15) == 0;
+}
+static void spec_outcome(int done) { g_spec_hist = (g_spec_hist << 1) | (done ? 1u : 0u); }
+void g53h_speculate_counts(int64_t *out)
+{
+    for (int i = 0; i < 3; i++) { out[i] = g_spec_n[i]; g_spec_n[i] = 0; }
+}
+int g53h_set_speculate(int on)
+{
+    const int prev = spec_enabled();
+    g_spec = on ? 1 : 0;
+    return prev;
+}
+
+/* The shared expert's descriptor in HBM (octet-tiled, resident), one per layer, uploaded when
+ * it changes. */
+static G53hExpert g_shh[GLM53F_MAX_LAYERS + 1];
+static G53Buf g_shd;
+static const G53hExpert *shared_desc(const Glm53fMoeW *w)
+{
+    const int l = w->layer >= 0 && w->layer <= GLM53F_MAX_LAYERS ? w->layer : GLM53F_MAX_LAYERS;
+    G53hExpert *d = (G53hExpert *)buf_get(&g_shd, (size_t)(GLM53F_MAX_LAYERS + 1) * sizeof(G53hExpert));
+    G53hExpert e;
+    memset(&e, 0, sizeof e);
+    e.gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
+    e.up = dev_mat_resident_tiled(&w->sh_up, "shared up");
+    e.down = dev_mat_resident_tiled(&w->sh_down, "shared down");
+    if (memcmp(&e, &g_shh[l], sizeof e)) {
+        g_shh[l] = e;
+        if (g53h_h2d_async(d + l, &g_shh[l], sizeof e)) g53_die("glm53f_moe");
+    }
+    return d + l;
+}
+
 static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int with_shared)
 {
     const int E = c->hidden, K = c->topk, NE = c->n_experts;
@@ -632,10 +681,18 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
 #endif
     float *xd = (float *)x;
     if (!g53h_is_device_ptr(x)) {                   /* x up without a wait */
-        float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, (size_t)E * sizeof(float));
-        memcpy(xp, x, (size_t)E * sizeof(float));
-        xd = (float *)buf_get(&g_xin, (size_t)E * sizeof(float));
-        if (g53h_h2d_async(xd, xp, (size_t)E * sizeof(float))) g53_die("glm53f_moe");
+        const size_t xb = (size_t)E * sizeof(float);
+        xd = (float *)buf_get(&g_xin, xb);
+        if (xb <= G53H_INBOX_BYTES && xb % 16 == 0) {
+            /* through the mapped inbox, read by a kernel on the compute stream (the previous
+             * call's fetch has run: its output was waited for) */
+            memcpy(g53h_inbox(), x, xb);
+            if (g53h_inbox_fetch(xd, 0, xb)) g53_die("glm53f_moe");
+        } else {
+            float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, xb);
+            memcpy(xp, x, xb);
+            if (g53h_h2d_async(xd, xp, xb)) g53_die("glm53f_moe");
+        }
     }
     HP(8);
     const int per_max = 2 * GLM53F_MAX_TOPK;
@@ -660,22 +717,64 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         nbias = (const float *)resident(w->next_bias, (size_t)NE * sizeof(float));
     }
     HP(9);
-    /* routing, NaN flag and the next layer's prediction: two launches, and the kernel writes the
-     * host's copy into the mailbox, which the host polls */
-    const unsigned seq_r = next_seq();
-    if (g53h_route_decode(idx_d, w_d, flag_d, pred_d, per, xd, gate, dt, bias, ngate, ndt, nbias, NE, E, K,
-                          c->norm_topk, c->routed_scale, G53_MB_ROUTE, seq_r, G53_MB_ROUTE_OFF))
-        g53_die("glm53f_router");
-    HP(0);
-    if (g53h_mailbox_wait(G53_MB_ROUTE, seq_r)) g53_die("glm53f_moe routing");
-    const int *back = (const int *)((const char *)g53h_mailbox() + G53_MB_ROUTE_OFF);
-    HP(1);
+    const int odev = g53h_is_device_ptr(out);
+    float *od = odev ? out : (float *)buf_get(&g_out, (size_t)E * sizeof(float));
+    const size_t ob = odev ? 0 : (size_t)E * sizeof(float);
+    /* Speculative layer: with the HBM cache's octet-tiled slots, the one-launch decode routes by
+     * itself over the table of this layer's landed slots, the next layer's prediction and the
+     * mailbox copy follow, and the host waits once. The reference's calls (hints, gets, releases)
+     * are then made in its order on the routing that came back; if a chosen expert had no landed
+     * slot at the launch (its contribution was left out) or a get fails, the layer is run again
+     * below on the experts the gets returned. No cache call happens while the kernel runs, so
+     * no slot it reads is refilled under it. */
+    const G53hExpert *stab_d = NULL, *stab_h = NULL;
+    int spec = spec_enabled() && spec_worth() && dt == 1 && K <= 15 && NE <= 1024 && E == 4096 && c->moe_inter == 2048 &&
+               G53_MB_OUT_OFF + 4 * G53H_NERR + ob <= G53H_MBOX_BYTES &&
+               (!with_shared || shared_tileable(w)) && g53h_cache_layer_table(src, w->layer, &stab_d, &stab_h) == 0;
+    const int *back;
+    const int spec_launched = spec;
+    if (spec) {
+        G53hMoeLayer SL;
+        memset(&SL, 0, sizeof SL);
+        SL.hidden = E; SL.inter = c->moe_inter; SL.topk = K; SL.norm_topk = c->norm_topk;
+        SL.routed_scale = c->routed_scale; SL.swiglu_limit = c->swiglu_limit;
+        SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = 1;
+        SL.n_experts = NE; SL.experts = stab_d;
+        SL.shared = with_shared ? shared_desc(w) : NULL;
+        if (per > 0 && g53h_decode_next(xd, ngate, ndt, nbias, NE, E)) g53_die("glm53f_router");
+        if (g53h_moe(od, xd, 1, &SL, idx_d, w_d)) g53_die("glm53f_moe");
+        const unsigned seq_s = next_seq();
+        if (g53h_decode_publish(G53_MB_OUT, seq_s, G53_MB_ROUTE_OFF, idx_d, K, pred_d, per, NE, G53_MB_OUT_OFF, od, ob))
+            g53_die("glm53f_moe");
+        HP(0);
+        if (g53h_mailbox_wait(G53_MB_OUT, seq_s)) g53_die("glm53f_moe");
+        HP(1);
+        back = (const int *)((const char *)g53h_mailbox() + G53_MB_ROUTE_OFF);
+    } else {
+        /* routing, NaN flag and the next layer's prediction: two launches, and the kernel writes
+         * the host's copy into the mailbox, which the host polls */
+        const unsigned seq_r = next_seq();
+        if (g53h_route_decode(idx_d, w_d, flag_d, pred_d, per, xd, gate, dt, bias, ngate, ndt, nbias, NE, E, K,
+                              c->norm_topk, c->routed_scale, G53_MB_ROUTE, seq_r, G53_MB_ROUTE_OFF))
+            g53_die("glm53f_router");
+        HP(0);
+        if (g53h_mailbox_wait(G53_MB_ROUTE, seq_r)) g53_die("glm53f_moe routing");
+        back = (const int *)((const char *)g53h_mailbox() + G53_MB_ROUTE_OFF);
+        HP(1);
+    }
     if (back[K]) {
         fprintf(stderr, "glm53f: FATAL, router selection (NaN scores) is below %d, above the limit of %d.\n", K, K);
         abort();
     }
     int ids[GLM53F_MAX_TOPK];
     memcpy(ids, back, (size_t)K * sizeof(int));
+    if (spec) {
+        /* the layer's flags (the routing's NaN case is handled above, as the reference's) */
+        errors_check((const int *)((const char *)g53h_mailbox() + G53_MB_OUT_OFF), w->layer, K);
+        /* the table is as it was at the launch: no cache call since */
+        for (int j = 0; j < K; j++)
+            if (ids[j] < 0 || ids[j] >= NE || !stab_h[ids[j]].gate.w) spec = 0;
+    }
     route_top16(w->layer, xd, w, c);
     if (prefetch) {
         src->hint(src, w->layer, ids, K);
@@ -690,6 +789,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         Glm53fExpertQ q;
         memset(&q, 0, sizeof q);
         if (src->get(src, w->layer, ids[j], &q) != 0) {
+            spec = 0;                              /* the speculative output included it */
             glm53f_expert_drops++;
             fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this output is CORRUPT\n", w->layer,
                     ids[j]);
@@ -706,6 +806,16 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     }
     if (!nh) i4r = 0;
     HP(3);
+    if (spec) {                  /* every chosen expert was in the kernel's table: the output is done */
+        g_spec_n[0]++;
+        spec_outcome(1);
+        for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
+        if (ob) memcpy(out, (const char *)g53h_mailbox() + G53_MB_OUT_OFF + 4 * G53H_NERR, ob);
+        HP(6);
+        return;
+    }
+    g_spec_n[spec_launched ? 1 : 2]++;
+    if (spec_launched) spec_outcome(0);
     if (with_shared) {
         /* the shared expert resident in the layout of the routed slots */
         /* (int4 routed experts: the row-wave kernel's fast FP8 path reads it octet-tiled too) */
@@ -734,8 +844,6 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
             L.block_c = 0;
     }
     G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
-    const int odev = g53h_is_device_ptr(out);
-    float *od = odev ? out : (float *)buf_get(&g_out, (size_t)E * sizeof(float));
     if (tiled) {
         /* compact table: slot j holds the j-th chosen expert (the kernel is told indices 0 .. K-1),
          * slot K the shared expert */
@@ -768,7 +876,6 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     /* the HBM cache orders each slot's reuse after the kernels launched so far */
     for (int i = 0; i < nh; i++) src->release(src, w->layer, held[i]);
     /* the error flags and the output come back together through the mailbox, one wait */
-    const size_t ob = odev ? 0 : (size_t)E * sizeof(float);
     const unsigned seq_o = next_seq();
     if (G53_MB_OUT_OFF + 4 * G53H_NERR + ob <= G53H_MBOX_BYTES) {
         if (g53h_publish(G53_MB_OUT, seq_o, G53_MB_OUT_OFF, od, ob)) g53_die("glm53f_moe");

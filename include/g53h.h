@@ -268,7 +268,34 @@ int g53h_errors_peek_async(int *host);
 #define G53H_MBOX_SLOTS 16
 void *g53h_mailbox(void);
 int   g53h_mailbox_wait(int slot, unsigned seq);
+/* The inbox, the other direction: G53H_INBOX_BYTES of pinned, mapped host memory that kernels
+ * read. g53h_inbox_fetch enqueues on the compute stream a kernel that copies bytes (a multiple
+ * of 16, at a multiple of 16) of it into device memory, so that small inputs reach the stream
+ * without the copy engine. The host must not rewrite those bytes before the stream has passed
+ * the fetch (a later wait on it). */
+#define G53H_INBOX_BYTES (1 << 16)
+void *g53h_inbox(void);
+int   g53h_inbox_fetch(void *dst_d, size_t off, size_t bytes);
 int   g53h_publish(int slot, unsigned seq, size_t off, const void *src_d, size_t bytes);
+
+/* The next layer's router scores for one decode token (the scores of
+ * src/core/glm53f_ops.c:1190-1228's prediction: sigmoid of next_gate . x, plus next_bias for the
+ * choice), kept in a library buffer for g53h_decode_publish. n_experts <= 1024. */
+int   g53h_route_next(const float *x_d, const void *next_gate_d, int next_dt, const float *next_bias_d,
+                      int n_experts, int hidden);
+/* The same scores requested of the next single-token decode launch: the octet-tiled one-launch
+ * decode computes them with its spare waves when the router is bf16 and they fit (n_experts <=
+ * 2 x its grid), else g53h_decode_publish launches g53h_route_next itself. x_d must stay
+ * unchanged until then. */
+int   g53h_decode_next(const float *x_d, const void *next_gate_d, int next_dt, const float *next_bias_d,
+                       int n_experts, int hidden);
+/* One launch after a decode layer: the next layer's top-n from the last g53h_route_next (n = 0:
+ * none; into pred_d [n]), then into the mailbox idx_d [topk], the NaN flag (bit 2 of the decode
+ * error words) and pred [n] as 32-bit words at route_off, the G53H_NERR error words and
+ * out_bytes of out_d at out_off, and seq into sequence word `slot` (g53h_route_decode and
+ * g53h_publish in one, after a layer kernel that routed by itself). */
+int   g53h_decode_publish(int slot, unsigned seq, size_t route_off, const int *idx_d, int topk, int *pred_d,
+                          int n, int n_experts, size_t out_off, const void *out_d, size_t out_bytes);
 
 /* Test hook: the number of polls after which a wait on another workgroup of the one-launch
  * decode kernels gives up (and sets bit 1 of their error flags); 0 restores the default.

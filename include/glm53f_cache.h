@@ -39,6 +39,7 @@
 
 #include "glm53f.h"
 #include "glm53f_st.h"
+#include "g53h.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -144,6 +145,24 @@ int  glm53f_cache_sync(Glm53fCache *c);
 /* 1 when src is the expert source of a cache made by glm53f_cache_init (its views are HBM and
  * its release is ordered on the device), else 0. */
 int  g53h_cache_is(const Glm53fExpertSrc *src);
+/* The device table of layer's experts whose reads have landed (no counterpart in the
+ * reference): table_d [n_experts] of octet-tiled descriptors (gate.w NULL where the expert holds
+ * no landed slot) on the compute stream's timeline, and table_h its host copy. It is current as
+ * of this call; any later cache call may evict or fill slots, so a kernel that reads it must
+ * complete before the next cache call. Returns 0, a positive count of this layer's reads still
+ * in flight (no table then), or -1 when src is not a cache with octet-tiled slots. */
+int  g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **table_d,
+                            const G53hExpert **table_h);
+/* The drop-in's speculative cached decode (no counterpart in the reference): with a cache of
+ * octet-tiled slots, glm53f_moe at T = 1 runs the one-launch decode over the layer's table
+ * before the reference's hint/get/release calls, which it then makes in the reference's order,
+ * and runs the layer again only when a chosen expert had no landed slot. on = 0 makes every
+ * layer route first and fetch before it computes. The environment variable G53H_NO_SPECULATE
+ * sets the default to 0. Returns the previous setting. */
+int  g53h_set_speculate(int on);
+/* Counts of cached single-token layers since the last call: out[0] finished by the speculative
+ * launch, out[1] speculative and run again, out[2] not speculative. Resets them. */
+void g53h_speculate_counts(int64_t *out);
 
 /* A store of experts in pinned host memory built by the library: n_pool distinct experts
  * generated from the seeded synthetic distribution (FP8 E4M3, N(0, sigma^2) absmax-quantised

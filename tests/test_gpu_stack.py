@@ -6,7 +6,10 @@ experts, so reads, evictions and prefetch reads all happen. Every (layer, expert
 own payload (the pinned store's codes come from a pool of 24, its block scales are the key's
 own), so a slot handed back for the wrong key changes the output. Every output equals the
 oracle's bit for bit, and equals the one from a cache large enough to never evict, without
-prefetch (the cache decides what is resident when, never what a layer returns)."""
+prefetch (the cache decides what is resident when, never what a layer returns). The same run
+with the drop-in's speculative layer turned off (route, fetch, then compute) returns the same
+outputs (what the cache reads ahead, and when, depends on when copies are seen complete, in
+the reference as here, so its counts may differ)."""
 import ctypes as C
 
 import numpy as np
@@ -84,15 +87,34 @@ def test_stack_through_cache_with_misses(L):
             L.glm53f_cache_free(C.byref(cache))
         return outs, stats
 
+    def counts():
+        n = (C.c_int64 * 3)()
+        L.g53h_speculate_counts(n)
+        return list(n)
+
     try:
+        counts()
         say("stack: 40 slots, prefetch 4 in flight, prefetch_n 6")
         got, st = run(40, 4, 6)
-        say("stack stats", st)
+        sc = counts()
+        say("stack stats", st, "layers speculative done / again / not", sc)
+        assert sum(sc) == STEPS * NL
+        prev = L.g53h_set_speculate(0)
+        try:
+            say("stack: the same without speculation")
+            got0, st0 = run(40, 4, 6)
+        finally:
+            L.g53h_set_speculate(prev)
+        assert counts()[:2] == [0, 0]
+        say("without speculation", st0)
+        assert np.array_equal(got.view(np.uint32), got0.view(np.uint32))
         assert st["misses"] > 0 and st["evictions"] > 0 and st["bg_reads"] > 0
         assert st["hits"] + st["misses"] == STEPS * NL * sp.K
         say("stack: 300 slots, no prefetch")
         want, st2 = run(300, 0, 0)
-        assert st2["evictions"] == 0
+        sc2 = counts()
+        say("layers speculative done / again / not", sc2)
+        assert st2["evictions"] == 0 and sc2[0] > 0
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         # every output against the oracle, with each key's experts as the store hands them out
         def key_mats(l, e):
