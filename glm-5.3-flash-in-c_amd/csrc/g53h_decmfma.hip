@@ -42,7 +42,9 @@
 #include "g53h_xwg.h"
 
 #define G53_DM_NW 8                 /* waves per workgroup                                */
+#ifndef G53_DM_P
 #define G53_DM_P 16                 /* G tasks: 1 KB half-tiles in flight per wave        */
+#endif
 #define G53_DM_NT (64 * G53_DM_NW)
 #define G53_DM_BB 512               /* LDS bytes of one block's B operand (4 groups x 4 x 32) */
 #define G53_DM_NGO (G53_DEC_I / 8)
@@ -51,6 +53,12 @@
 #define G53_DM_MAXDO 4
 #define G53_DM_DTAB 24576
 #define G53_DM_ROT 16
+#ifndef G53_DM_BPIPE
+#define G53_DM_BPIPE 1              /* B operands read by every lane, one block ahead          */
+#endif
+#ifndef G53_DM_RING1
+#define G53_DM_RING1 1              /* G tasks: PB + 1 register slots, requests one block early */
+#endif
 #ifndef G53_DM_PIN
 #define G53_DM_PIN 2                /* blocks between two pins of the block arithmetic     */
 #endif
@@ -173,6 +181,16 @@ __device__ __forceinline__ void g53_dm_block(g53_m4f &acc, const g53_m8i &a, con
         b = *(const g53_m8i *)bq;
         bscale = *bs;
     }
+    g53_m4f c = {0.0f, 0.0f, 0.0f, 0.0f};
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, bscale);
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = __builtin_fmaf(c[i], s, acc[i]);
+}
+
+/* The same with B and its scale already in registers (read a block ahead by every lane: the
+ * lanes of columns 3-15 read the zero slot of their group and the scale 0x7f). */
+__device__ __forceinline__ void g53_dm_mma(g53_m4f &acc, const g53_m8i &a, const g53_m8i &b, int bscale, float s)
+{
     g53_m4f c = {0.0f, 0.0f, 0.0f, 0.0f};
     c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, bscale);
 #pragma unroll
@@ -350,6 +368,7 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
         if (a.trace && lane == 0) {
             a.trace[(size_t)blockIdx.x * 192 + 12] = t_seen;
             a.trace[(size_t)blockIdx.x * 192 + 13] = t_tau;
+            a.trace[(size_t)blockIdx.x * 192 + 14] = t_rank;
         }
     }
     const bool shared_ok = hs && st[K].gate.w && g53_desc_mtiled(st[K]);
@@ -417,7 +436,11 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
             __builtin_amdgcn_sched_barrier(0);
             g53_mgv4 *q = (g53_mgv4 *)pl;
             constexpr int NB = G53_DEC_NBE / 2, PB = G53_DM_P / 2;
+#if G53_DM_RING1
+            g53_m8i r[PB + 1];
+#else
             g53_m8i r[PB];
+#endif
 #pragma unroll
             for (int j = 0; j < PB; j++) r[j] = g53_dm_ld(q + 64 * j);
             if (!xr) {                            /* x as planes: the first multiply needs them */
@@ -428,6 +451,32 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
             const int sbits = __float_as_int(scv);
             const uint8_t *bq0 = xq + 16 * h * G53_DM_BB + grp * 128 + min(m, 3) * 32;
             const uint8_t *bs0 = xsc + 16 * h * 64 + lane;
+#if G53_DM_RING1
+            /* a ring of PB + 1: block kb + PB is requested before block kb is multiplied, so
+             * the multiply's operand reads never delay the next request */
+#if G53_DM_BPIPE
+            g53_m8i bn = *(const g53_m8i *)bq0;
+            int sn = bs0[0];
+#endif
+#pragma unroll
+            for (int kb = 0; kb < NB; kb++) {
+                if (kb + PB < NB) r[(kb + PB) % (PB + 1)] = g53_dm_ld(q + 64 * (kb + PB));
+                const float sg = __int_as_float(__builtin_amdgcn_readlane(sbits, kb));
+                const float su = __int_as_float(__builtin_amdgcn_readlane(sbits, 16 + kb));
+#if G53_DM_BPIPE
+                const g53_m8i bc = bn;
+                const int sc = sn;
+                if (kb + 1 < NB) {
+                    bn = *(const g53_m8i *)(bq0 + (kb + 1) * G53_DM_BB);
+                    sn = bs0[(kb + 1) * 64];
+                }
+                g53_dm_mma(acc, r[kb % (PB + 1)], bc, sc, grp < 2 ? sg : su);
+#else
+                g53_dm_block(acc, r[kb % (PB + 1)], bq0 + kb * G53_DM_BB, bs0 + kb * 64, m < 3, grp < 2 ? sg : su);
+#endif
+                if ((kb % G53_DM_PIN) == G53_DM_PIN - 1) asm volatile("" : "+v"(acc));
+            }
+#else
 #pragma unroll 1
             for (int k0 = 0; k0 < NB; k0 += PB) {
 #pragma unroll
@@ -444,6 +493,7 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
                     if (k0 + PB < NB) r[j] = g53_dm_ld(q + 64 * (kb + PB));
                 }
             }
+#endif
             const g53_m4f v = g53_dm_planesum(acc);
             if (m == 0)
 #pragma unroll
@@ -536,10 +586,24 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
             const int sbits = __float_as_int(scv);
             const uint8_t *bq0 = myaq + grp * 128 + min(m, 3) * 32;
             const uint8_t *bs0 = myasc + lane;
+#if G53_DM_BPIPE
+            g53_m8i bn = *(const g53_m8i *)bq0;
+            int sn = bs0[0];
+#endif
 #pragma unroll
             for (int kb = 0; kb < NB; kb++) {
                 const float sd = __int_as_float(__builtin_amdgcn_readlane(sbits, kb));
+#if G53_DM_BPIPE
+                const g53_m8i bc = bn;
+                const int sc = sn;
+                if (kb + 1 < NB) {
+                    bn = *(const g53_m8i *)(bq0 + (kb + 1) * G53_DM_BB);
+                    sn = bs0[(kb + 1) * 64];
+                }
+                g53_dm_mma(acc, r[kb], bc, sc, sd);
+#else
                 g53_dm_block(acc, r[kb], bq0 + kb * G53_DM_BB, bs0 + kb * 64, m < 3, sd);
+#endif
                 if ((kb % G53_DM_PIN) == G53_DM_PIN - 1) asm volatile("" : "+v"(acc));
             }
             v = g53_dm_planesum(acc);

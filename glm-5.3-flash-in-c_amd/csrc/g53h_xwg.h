@@ -114,6 +114,9 @@ __device__ __forceinline__ double g53_router_row(const g53_u4 (&c)[8], const flo
 
 
 extern "C" __device__ unsigned __ockl_wfred_max_u32(unsigned);
+#ifndef G53_RW_BREG
+#define G53_RW_BREG 1
+#endif
 
 /* ------------------------------------------------------------------ routing ---- */
 #ifndef G53_POLL_GAP
@@ -158,18 +161,30 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
     }
     int spins = 0;
     int pos = 0;
+    float bre[NV];                              /* the bias in registers (G53_RW_BREG) */
+#pragma unroll
+    for (int v = 0; v < NV; v++) bre[v] = 0.0f;
     /* two passes of the selection: the first on whatever the first read returned, while the
      * scores are still being computed (it runs the selection's code once, so that its
      * instructions are cached when the real pass runs), the second once every score is current */
+#ifndef G53_RW_PASSES
+#define G53_RW_PASSES 2
+#endif
+    constexpr int LAST = G53_RW_PASSES - 1;
 #pragma clang loop unroll(disable)
-    for (int pass = 0; pass < 2; pass++) {
+    for (int pass = 0; pass < G53_RW_PASSES; pass++) {
     if (pass == 1) {
     if (gbias) {
         /* pass 0 ran first thing, on zeros and whatever the bias array held (only to bring the
          * selection's code into the instruction cache); now the bias, then the scores */
+#if G53_RW_BREG
+#pragma unroll
+        for (int v = 0; v < NV; v++) bre[v] = gbias[min(lane + 64 * v, NE - 1)];
+#else
         for (int e = lane; e < NE; e += 64) ((float *)bias)[e] = gbias[e];
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_wave_barrier();
+#endif
     }
     /* two reads of the scores in flight at a time, issued a short sleep apart: a score that
      * lands is seen one memory latency later, not up to two */
@@ -207,7 +222,11 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
 #pragma unroll
     for (int v = 0; v < NV; v++) {
         const int e = lane + 64 * v;
+#if G53_RW_BREG
+        const float ch = e < NE ? scv[v] + (gbias ? bre[v] : bias[e]) : -INFINITY;
+#else
         const float ch = e < NE ? scv[v] + bias[e] : -INFINITY;
+#endif
         key[v] = (ch > -INFINITY) ? g53_fkey(ch) : 0u;    /* 0: never chosen */
     }
     /* K rounds of arg-max. Each lane first sorts its keys, largest first and, among equal keys,
@@ -230,6 +249,7 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
             vid[q] = sw_ ? i1 : i0; vid[q + 1] = sw_ ? i0 : i1;
             vsc[q] = sw_ ? s1 : s0; vsc[q + 1] = sw_ ? s0 : s1;
         }
+    if (pass == LAST) t_rank = __builtin_amdgcn_s_memrealtime();
     /* the lane's head: its first key not yet taken (index hp into the sorted list) */
     int hp = 0;
     uint32_t hk = key[0];
@@ -246,7 +266,7 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
         const int e = __builtin_amdgcn_readlane(hv, win);
         const float wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(hs), win));
         if (lane == 0) { sidx[j] = e; sw[j] = wsc; }
-        if (pass == 1 && nrouted && lane == 0) {    /* slot j is known: its tasks may start */
+        if (pass == LAST && nrouted && lane == 0) { /* slot j is known: its tasks may start */
             G53_CBAR();
             (void)g53_lds_add(nrouted, 1);
         }
@@ -267,7 +287,6 @@ __device__ __forceinline__ bool g53_route_wave(const g53_u64 *score, const float
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    t_rank = __builtin_amdgcn_s_memrealtime();
     /* the weights: every lane forms the sum in slot order, lane j divides weight j */
     float wj = 0.0f;
     if (lane < K) wj = sw[lane];
