@@ -33,6 +33,7 @@
  * bounded; one that runs out sets an error flag and the wave goes on, so the grid drains. */
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <type_traits>
 
 #include "g53h.h"
 #include "g53h_core.h"
@@ -71,8 +72,10 @@
 #endif
 #if defined(__HIP_DEVICE_COMPILE__)
 typedef __attribute__((address_space(1))) const g53_u4 g53_gv4t;
+typedef __attribute__((address_space(1))) const float4 g53_gf4;
 #else
 typedef const g53_u4 g53_gv4t;
+typedef const float4 g53_gf4;
 #endif
 
 struct G53TiledArgs {
@@ -262,9 +265,155 @@ __device__ __forceinline__ void g53_oct_stream2(const uint8_t *pa, const uint8_t
     acc_b = r1 ? acc : other;
 }
 
+/* ----------------------------------------------------------- int4 experts ---- */
+/* A descriptor of int4 codes in the int4-tiled layout (include/g53h.h, G53H_MAT_I4T) with the
+ * released shapes and one step per row and 64 columns. */
+__device__ __forceinline__ bool g53_desc_i4t(const G53hExpert &e)
+{
+    const G53hMat *m[3] = {&e.gate, &e.up, &e.down};
+    const int rows[3] = {G53_DEC_I, G53_DEC_I, G53_DEC_E}, cols[3] = {G53_DEC_E, G53_DEC_E, G53_DEC_I};
+    bool ok = true;
+    for (int i = 0; i < 3; i++)
+        ok = ok && m[i]->w && m[i]->s && (m[i]->flags & G53H_MAT_I4) && (m[i]->flags & G53H_MAT_I4T) &&
+             m[i]->rows == rows[i] && m[i]->cols == cols[i] && m[i]->bc == 64 && m[i]->scols == cols[i] / 64;
+    return ok;
+}
+
+/* One lane's accumulator of one 64-column group: its 8 levels (nibbles of d, the low one first)
+ * times the 8 matching inputs in column order, a = fmaf((float)(level - 8), x, a) (reference
+ * src/core/glm53f_ops.c:270-276). level - 8 is the 4-bit two's complement of level ^ 8. */
+__device__ __forceinline__ float g53_i4_acc(uint32_t d, const float4 &x0, const float4 &x1)
+{
+    const uint32_t s = d ^ 0x88888888u;
+    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) a = __builtin_fmaf((float)((int)(s << (28 - 4 * i)) >> 28), xv[i], a);
+    return a;
+}
+
+/* The inputs of group g (0..3) of 256-column unit u for this lane: block 2 u + g / 2 of the
+ * vector tiled in LDS (run of 16 at xv, VBLK floats per block), half g % 2 of the run. */
+template <int VBLK>
+__device__ __forceinline__ void g53_i4_x(const float *xv, int u, int g, float4 &x0, float4 &x1)
+{
+    const float4 *r = (const float4 *)(xv + (2 * u + (g >> 1)) * VBLK + 8 * (g & 1));
+    x0 = r[0];
+    x1 = r[1];
+}
+
+#ifndef G53_DT_P4
+#define G53_DT_P4 8                /* int4 G tasks: units in flight per wave               */
+#endif
+
+/* Stream one int4 row octet's NU units (pu: its first unit; this lane's 16 bytes at + 16 lane),
+ * unit u's four groups against blocks 2 u, 2 u + 1 of the vector; the row's double sum over its
+ * groups in order (reference :246-292), the same in every lane of the row's octet. srow: this
+ * lane's row of steps (float4 u = unit u's four). */
+template <int NU, int VBLK, class Ready>
+__device__ __forceinline__ double g53_i4_stream(const uint8_t *pu, const float *srow, const float *xv, int lane,
+                                                const Ready &ready)
+{
+    constexpr int P = G53_DT_P4 < NU ? G53_DT_P4 : NU;
+    static_assert(NU % P == 0, "units in flight");
+    g53_gv4t *q = (g53_gv4t *)(g53_uniform_ptr(pu) + 16 * lane);
+    const float4 *sq = (const float4 *)srow;
+    g53_u4 r[P];
+    float4 st[P];
+#pragma unroll
+    for (int j = 0; j < P; j++) { r[j] = G53_DT_LD(q + 64 * j); st[j] = *(const g53_gf4 *)(sq + j); }
+    ready();
+    const int pr = lane & 7;
+    const bool r1 = ((pr ^ (pr >> 2)) & 1) != 0;
+    double acc = 0.0;
+    auto unit = [&](int u, int j, bool refill) {
+        const uint32_t d[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+        const float sv[4] = {st[j].x, st[j].y, st[j].z, st[j].w};
+        float f[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float4 x0, x1;
+            g53_i4_x<VBLK>(xv, u, g, x0, x1);
+            f[g] = g53_i4_acc(d[g], x0, x1);
+        }
+        if (refill) {
+            r[j] = G53_DT_LD(q + 64 * (u + P));
+            st[j] = *(const g53_gf4 *)(sq + u + P);
+        }
+        /* groups (0, 1) and (2, 3) through one tree each; then each lane takes the other role's
+         * sum from its neighbour, and the row adds the four in order */
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const double t = g53_oct_tree2(f[2 * h], f[2 * h + 1], r1);
+            const double o = g53_dpp64<0xB1>(t);
+            const double ta = r1 ? o : t, tb = r1 ? t : o;
+            acc = acc + ta * (double)sv[2 * h];
+            acc = acc + tb * (double)sv[2 * h + 1];
+        }
+        /* one unit at a time: the compiler would otherwise hoist every unit's input reads */
+        asm volatile("" : "+v"(acc));
+    };
+#pragma unroll 1
+    for (int u0 = 0; u0 < NU - P; u0 += P) {
+#pragma unroll
+        for (int j = 0; j < P; j++) unit(u0 + j, j, true);
+    }
+#pragma unroll
+    for (int j = 0; j < P; j++) unit(NU - P + j, j, false);
+    return acc;
+}
+
+/* Two int4 row octets at once (pa, pb): group g of unit u of both through one tree; lanes of role
+ * 0 keep octet a's sums, role 1 octet b's (srow: this lane's row of steps in its role's octet).
+ * All 2 NU units are in flight before ready() runs. */
+template <int NU, int VBLK, class Ready>
+__device__ __forceinline__ void g53_i4_stream2(const uint8_t *pa, const uint8_t *pb, const float *srow, const float *xv,
+                                               int lane, const Ready &ready, double &acc_a, double &acc_b)
+{
+    g53_gv4t *qa = (g53_gv4t *)(g53_uniform_ptr(pa) + 16 * lane);
+    g53_gv4t *qb = (g53_gv4t *)(g53_uniform_ptr(pb) + 16 * lane);
+    const float4 *sq = (const float4 *)srow;
+    constexpr int SR = 3;                                /* units of steps in flight */
+    g53_u4 ra[NU], rb[NU];
+    float4 st[SR];
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        ra[u] = G53_DT_LD(qa + 64 * u);
+        rb[u] = G53_DT_LD(qb + 64 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < SR - 1; u++) st[u] = *(const g53_gf4 *)(sq + u);
+    ready();
+    const int pr = lane & 7;
+    const bool r1 = ((pr ^ (pr >> 2)) & 1) != 0;
+    double acc = 0.0;
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        if (u + SR - 1 < NU) st[(u + SR - 1) % SR] = *(const g53_gf4 *)(sq + u + SR - 1);
+        const uint32_t da[4] = {ra[u].x, ra[u].y, ra[u].z, ra[u].w};
+        const uint32_t db[4] = {rb[u].x, rb[u].y, rb[u].z, rb[u].w};
+        const float sv[4] = {st[u % SR].x, st[u % SR].y, st[u % SR].z, st[u % SR].w};
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float4 x0, x1;
+            g53_i4_x<VBLK>(xv, u, g, x0, x1);
+            const float fa = g53_i4_acc(da[g], x0, x1), fb = g53_i4_acc(db[g], x0, x1);
+            const double t = g53_oct_tree2(fa, fb, r1);
+            acc = acc + t * (double)sv[g];
+        }
+        asm volatile("" : "+v"(acc));            /* one unit at a time (see g53_i4_stream) */
+    }
+    const double other = g53_dpp64<0xB1>(acc);          /* the neighbour has the other role */
+    acc_a = r1 ? other : acc;
+    acc_b = r1 ? acc : other;
+}
+
 #define G53_TTRACE(k) do { if (a.trace && lane == 0) \
     a.trace[(size_t)blockIdx.x * 192 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 
+/* I4: the routed experts are int4, int4-tiled (G53H_MAT_I4T; the reference's --experts int4),
+ * streamed by g53_i4_stream / g53_i4_stream2; the shared expert stays FP8 octet-tiled. */
+template <bool I4>
 __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
 {
     __shared__ __attribute__((aligned(16))) float xs[G53_DEC_NBE * G53_DT_BLK];          /* x, tiled  */
@@ -433,11 +582,11 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
     const int n_dall = nslot * nd;
     float *myact = actw[w];
     g53_u64 tg = 0, twait = 0, td = 0;
-    for (;;) {
-        int t = 0;
-        if (lane == 0) t = g53_lds_add(&qctr, 1);
-        t = __builtin_amdgcn_readfirstlane(t);
-        if (t >= n_task) break;
+    /* one task (t: its number in the order); RT: a routed slot of the int4 kernel (int4 code
+     * paths), else the FP8 paths. The int4 kernel runs the shared expert's tasks, then the
+     * routed ones, in two loops, so that the two kinds of down task never share registers */
+    auto task = [&](int t, auto rt_tag) {
+        constexpr bool RT = decltype(rt_tag)::value;
         if (t < 32) G53_TTRACE(64 + 2 * t);
         /* the order: the shared expert's G tasks, its D tasks (its activations are complete
          * while the routing is still being decided), the routed slots' G tasks slot by slot,
@@ -463,18 +612,25 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
             const int e = sidx[s];
             if (e >= 0 && e < a.NE) ex = dstage ? ((const G53hExpert *)dtab)[e] : a.experts[e];
             else ex.gate.w = nullptr;
-            usable = ex.gate.w != nullptr && g53_desc_tiled(ex);
+            usable = ex.gate.w != nullptr && (RT ? g53_desc_i4t(ex) : g53_desc_tiled(ex));
             if (ex.gate.w && !usable && lane == 0) g53_flag_err(a.err, 8);
         }
         const bool present = __builtin_amdgcn_readfirstlane((int)usable) != 0;
         if (is_g) {
-            if (!present) continue;                   /* its activations are never read */
+            if (!present) return;                     /* its activations are never read */
             const int ogl = idx >> 1, og = go_lo + ogl, m = idx & 1;
             const G53hMat &mat = m ? ex.up : ex.gate;
-            const uint8_t *pu = mat.w + (size_t)og * (G53_DEC_NBE * 1024);
-            const float *sp = mat.s + (size_t)(og >> 4) * mat.scols + (lane & 31);
             const g53_u64 t0 = a.trace ? __builtin_amdgcn_s_memrealtime() : 0;
-            const double acc = g53_oct_stream<G53_DEC_NBE, G53_DT_BLK>(pu, sp, xs + p * G53_DT_PAD, lane, G53NoWait());
+            double acc;
+            if constexpr (RT) {
+                const uint8_t *pu = mat.w + (size_t)og * (G53_DEC_E / 256 * 1024);
+                const float *srow = mat.s + (size_t)(og * 8 + o) * mat.scols;
+                acc = g53_i4_stream<G53_DEC_E / 256, G53_DT_BLK>(pu, srow, xs + p * G53_DT_PAD, lane, G53NoWait());
+            } else {
+                const uint8_t *pu = mat.w + (size_t)og * (G53_DEC_NBE * 1024);
+                const float *sp = mat.s + (size_t)(og >> 4) * mat.scols + (lane & 31);
+                acc = g53_oct_stream<G53_DEC_NBE, G53_DT_BLK>(pu, sp, xs + p * G53_DT_PAD, lane, G53NoWait());
+            }
             if (a.trace) tg += __builtin_amdgcn_s_memrealtime() - t0;
             /* gate and up of an octet meet in LDS; the second of the two computes the SwiGLU
              * and publishes the octet's activations */
@@ -492,7 +648,7 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
                 }
             }
             if (t < 32) G53_TTRACE(65 + 2 * t);
-            continue;
+            return;
         }
         const int oa = do_lo + 2 * idx, ob = oa + 1 < do_lo + n_do ? oa + 1 : oa;
         float va = 0.0f, vb = 0.0f;
@@ -569,7 +725,15 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
                 if (a.trace) t1 = __builtin_amdgcn_s_memrealtime();
             };
             double da, db;
-            g53_oct_stream2<G53_DEC_NBI, G53_DT_ABLK>(pa, pb, sp, myact + p * G53_DT_APAD, lane, ready, da, db);
+            if constexpr (RT) {
+                const uint8_t *qa = ex.down.w + (size_t)oa * (G53_DEC_I / 256 * 1024);
+                const uint8_t *qb = ex.down.w + (size_t)ob * (G53_DEC_I / 256 * 1024);
+                const bool r1 = ((p ^ (p >> 2)) & 1) != 0;      /* this lane's octet in the shared trees */
+                const float *srow = ex.down.s + (size_t)((r1 ? ob : oa) * 8 + o) * ex.down.scols;
+                g53_i4_stream2<G53_DEC_I / 256, G53_DT_ABLK>(qa, qb, srow, myact + p * G53_DT_APAD, lane, ready, da, db);
+            } else {
+                g53_oct_stream2<G53_DEC_NBI, G53_DT_ABLK>(pa, pb, sp, myact + p * G53_DT_APAD, lane, ready, da, db);
+            }
             va = (float)da;
             vb = (float)db;
             if (a.trace) {
@@ -602,6 +766,18 @@ __global__ void __launch_bounds__(G53_DT_NT, 1) k_dec_tiled(G53TiledArgs a)
             }
             G53_TTRACE(3);
         }
+    };
+    auto claim = [&]() {
+        int t = 0;
+        if (lane == 0) t = g53_lds_add(&qctr, 1);
+        return __builtin_amdgcn_readfirstlane(t);
+    };
+    {
+        const int i_rg = hs * (ng + nd);                /* the first routed task */
+        int t = claim();
+        for (; t < n_task && (!I4 || t < i_rg); t = claim()) task(t, std::integral_constant<bool, false>());
+        if constexpr (I4)
+            for (; t < n_task; t = claim()) task(t, std::integral_constant<bool, true>());
     }
     G53_TTRACE(4 + (w & 7));
     if (a.trace && lane == 0 && w < 16) {
@@ -628,7 +804,7 @@ int g53h_decode_tiled_grid(void) { return g_dt_grid; }
 
 static int dt_takes(const G53hMoeLayer *L, const int *idx_in)
 {
-    return L->tiled && L->block_c == 128 && L->hidden == G53_DEC_E && L->inter == G53_DEC_I &&
+    return (L->tiled == 1 || L->tiled == 3) && L->block_c == 128 && L->hidden == G53_DEC_E && L->inter == G53_DEC_I &&
            (idx_in || (L->router_dt == 1 && L->router)) && L->topk >= 1 && L->topk <= G53_DEC_MAXK &&
            L->n_experts >= 1 && L->n_experts <= G53_DEC_MAXNE;
 }
@@ -639,9 +815,13 @@ static int dt_size_grid(void)
         const int cus = g53h_num_cus();
         int per = 0;
         g_dt_grid = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_dec_tiled, G53_DT_NT, 0) != hipSuccess) {
+        int per4 = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_dec_tiled<false>, G53_DT_NT, 0) !=
+                hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per4, (const void *)k_dec_tiled<true>, G53_DT_NT, 0) !=
+                hipSuccess) {
             (void)hipGetLastError();
-        } else if (per >= 1 && cus >= 128 && cus <= 512) {
+        } else if (per >= 1 && per4 >= 1 && cus >= 128 && cus <= 512) {
             g_dt_grid = cus;
         }
     }
@@ -678,7 +858,10 @@ static void dt_launch(float *out, const float *x, const G53hMoeLayer *L, int *id
         nq->armed = 0;
     }
     g53h_prof_mark(G53_PROF_START);
-    hipLaunchKernelGGL(k_dec_tiled, dim3(g_dt_grid), dim3(G53_DT_NT), 0, g53h_stream(), e);
+    if (L->tiled == 3)                 /* int4-tiled routed experts */
+        hipLaunchKernelGGL(k_dec_tiled<true>, dim3(g_dt_grid), dim3(G53_DT_NT), 0, g53h_stream(), e);
+    else
+        hipLaunchKernelGGL(k_dec_tiled<false>, dim3(g_dt_grid), dim3(G53_DT_NT), 0, g53h_stream(), e);
     g53h_prof_mark(G53_PROF_FUSED);
 }
 
@@ -748,7 +931,7 @@ extern "C" int g53h_moe_decode_noalloc(float *out_d, const float *x_d, const G53
                          G53_DEC_MAXNE);
     if (L->topk < 1 || L->topk > G53_DEC_MAXK)
         return g53h_fail("g53h_moe_decode_noalloc: top-k %d, above the limit of %d", L->topk, G53_DEC_MAXK);
-    if (!dt_takes(L, nullptr))
+    if (L->tiled != 1 || !dt_takes(L, nullptr))
         return g53h_fail("g53h_moe_decode_noalloc: the layer must be octet-tiled with hidden %d, inter %d, "
                          "128-column blocks and a bf16 router", G53_DEC_E, G53_DEC_I);
     if (!dt_size_grid()) return g53h_fail("g53h_moe_decode_noalloc: the decode kernel does not fit this device");

@@ -816,7 +816,7 @@ static int g53_grp_shapes_ok(const G53hMoeLayer *L)
 extern "C" int g53h_grouped_ok(const G53hMoeLayer *L)
 {
     /* the grouped kernels read row-major or octet-tiled experts, not MFMA-tiled ones */
-    return L && L->router && L->bias && L->tiled != 2 && g53_grp_shapes_ok(L);
+    return L && L->router && L->bias && (L->tiled == 0 || L->tiled == 1) && g53_grp_shapes_ok(L);
 }
 
 int g53h_grouped_use(const G53hMoeLayer *L, int T) { return g_grp_mode && T >= 2 && g53h_grouped_ok(L); }

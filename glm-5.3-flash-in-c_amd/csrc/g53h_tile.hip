@@ -132,7 +132,99 @@ __global__ void __launch_bounds__(256) k_mtile_f8(uint8_t *__restrict__ dst, con
     else *tl = *rm;
 }
 
+/* Dword q of an int4-tiled matrix (G53H_MAT_I4T): unit u = q / 256 (row octet u / nb, 256-column
+ * block u % nb), row m = (q % 256) / 32 of the octet, lane run p = (q % 32) / 4 (accumulator
+ * g53h_tile_acc(p)), group g = q % 4 of the block. Its nibble i (low nibble first) is the level of
+ * column block * 256 + 64 g + acc + 8 i. */
+__host__ __device__ inline void g53_i4tile_dword(long q, int nb, int &row, int &col0)
+{
+    const long u = q >> 8;
+    const int l = (int)(q & 255), m = l >> 5, p = (l >> 2) & 7, g = l & 3;
+    row = (int)(u / nb) * 8 + m;
+    col0 = (int)(u % nb) * 256 + 64 * g + (((p & 1) << 2) | (p & 2) | (p >> 2));
+}
+
+/* The level of column c of a row-major int4 row (low nibble = even column). */
+__host__ __device__ inline unsigned g53_i4_get(const uint8_t *row, int c) { return (row[c >> 1] >> (4 * (c & 1))) & 15u; }
+
+__global__ void __launch_bounds__(256) k_tile_i4(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src,
+                                                 int cols, long ndw, int inverse)
+{
+    const long q = (long)blockIdx.x * 256 + threadIdx.x;
+    if (q >= ndw) return;
+    int row, c0;
+    g53_i4tile_dword(q, cols / 256, row, c0);
+    if (!inverse) {
+        const uint8_t *r = src + (size_t)row * (cols / 2);
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) w |= g53_i4_get(r, c0 + 8 * i) << (4 * i);
+        ((uint32_t *)dst)[q] = w;
+    } else {
+        /* column c0 + 8 i has the parity of c0: the eight levels are all low or all high nibbles of
+         * eight bytes four apart, which this thread alone writes half of; the other half belongs to
+         * the run of the neighbouring accumulator (c0 ^ 1), so the byte is assembled from both */
+        const uint32_t w = ((const uint32_t *)src)[q];
+        const long q2 = q ^ 16;                      /* run p ^ 4: accumulator c0 ^ 1, same group */
+        const uint32_t w2 = ((const uint32_t *)src)[q2];
+        if (c0 & 1) return;                          /* the even-column thread writes both nibbles */
+        uint8_t *r = dst + (size_t)row * (cols / 2);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            r[(c0 + 8 * i) >> 1] = (uint8_t)(((w >> (4 * i)) & 15u) | (((w2 >> (4 * i)) & 15u) << 4));
+    }
+}
+
 } /* namespace */
+
+static int g53_i4tile_shape(int rows, int cols)
+{
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 256)
+        return g53h_fail("g53h_tile_i4: a %d x %d matrix cannot be int4-tiled (rows a multiple of 8, columns of 256)",
+                         rows, cols);
+    return 0;
+}
+
+int g53h_tile_i4_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse, hipStream_t s)
+{
+    if (g53h_ready() || g53_i4tile_shape(rows, cols)) return -1;
+    if (dst_d == src_d) return g53h_fail("g53h_tile_i4: in-place conversion is not supported");
+    const long ndw = (long)rows * cols / 8;
+    hipLaunchKernelGGL(k_tile_i4, dim3((unsigned)((ndw + 255) / 256)), dim3(256), 0, s, dst_d, src_d, cols, ndw,
+                       inverse);
+    G53_LAUNCHED("k_tile_i4");
+    return 0;
+}
+
+extern "C" int g53h_tile_i4(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse)
+{
+    if (g53h_ready()) return -1;
+    return g53h_tile_i4_on(dst_d, src_d, rows, cols, inverse, g53h_stream());
+}
+
+extern "C" int g53h_tile_i4_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse)
+{
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 256 || dst == src) return -1;
+    const long ndw = (long)rows * cols / 8;
+    if (inverse) memset(dst, 0, (size_t)rows * cols / 2);
+    for (long q = 0; q < ndw; q++) {
+        int row, c0;
+        g53_i4tile_dword(q, cols / 256, row, c0);
+        uint8_t *r = (uint8_t *)(inverse ? dst : src) + (size_t)row * (cols / 2);
+        uint32_t *t = (uint32_t *)(inverse ? src : dst) + q;
+        if (!inverse) {
+            uint32_t w = 0;
+            for (int i = 0; i < 8; i++) w |= g53_i4_get(r, c0 + 8 * i) << (4 * i);
+            *t = w;
+        } else {
+            for (int i = 0; i < 8; i++) {
+                const int c = c0 + 8 * i;
+                r[c >> 1] |= (uint8_t)(((*t >> (4 * i)) & 15u) << (4 * (c & 1)));
+            }
+        }
+    }
+    return 0;
+}
 
 int g53h_mtile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse, hipStream_t s)
 {

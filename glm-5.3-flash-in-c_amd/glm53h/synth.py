@@ -138,6 +138,7 @@ class DeviceLayer:
     tiled: bool = False
     i4: bool = False
     mfma: bool = False
+    i4t: bool = False
 
     @classmethod
     def build(cls, sp: LayerSpec, n_experts_present=None, tiled=False, i4=False, mfma=False):
@@ -146,9 +147,14 @@ class DeviceLayer:
         mfma: MFMA-tiled instead (G53H_MAT_MTILED), the layout of k_dec_mfma.
         i4: re-quantise every routed expert on the device into the reference's int4 format
         (G53H_MAT_I4: levels, and one step per row and 64 columns; the reference's
-        --experts int4), the shared expert staying FP8; the layer then has block_c 0."""
-        assert not (tiled and i4) and not (mfma and (tiled or i4))
+        --experts int4), the shared expert staying FP8; the layer then has block_c 0.
+        i4 and tiled: the int4 levels int4-tiled (G53H_MAT_I4T), the layout of the one-launch
+        int4 decode, and the shared expert octet-tiled; the layer has tiled 3, block_c 128."""
+        assert not (mfma and (tiled or i4))
         self = cls(sp)
+        self.i4t = bool(tiled and i4)
+        if self.i4t:
+            tiled = False
         self.mfma = bool(mfma)
         tiled = tiled or mfma
         self.tiled = bool(tiled)
@@ -172,6 +178,7 @@ class DeviceLayer:
             s_stage = _align(max(r * c for r, c in shapes))
             stage = DevBuf(s_stage + max(((r + sp.br - 1) // sp.br) * ((c + sp.bc - 1) // sp.bc) * 4
                                          for r, c in shapes))
+            stage4 = DevBuf(max(r * c // 2 for r, c in shapes)) if self.i4t else None
         for i in range(nslots):
             base = self.arena.ptr + i * self.slot_bytes
             mats = []
@@ -186,13 +193,18 @@ class DeviceLayer:
                     off4 = _align(off4 + r * c // 2)
                     st = base + off4
                     off4 = _align(off4 + r * (c // 64) * 4)
-                    check(L.g53h_i4_from_f8(q, st, C.byref(f)), "g53h_i4_from_f8")
-                    mats.append(G53hMat(q, st, r, c, 1, 64, c // 64, 4))
+                    if self.i4t:                 # quantised row-major into staging, then tiled
+                        check(L.g53h_i4_from_f8(stage4.ptr, st, C.byref(f)), "g53h_i4_from_f8")
+                        check(L.g53h_tile_i4(q, stage4.ptr, r, c, 0), "g53h_tile_i4")
+                    else:
+                        check(L.g53h_i4_from_f8(q, st, C.byref(f)), "g53h_i4_from_f8")
+                    mats.append(G53hMat(q, st, r, c, 1, 64, c // 64, 4 | (16 if self.i4t else 0)))
                 descs[i] = G53hExpert(*mats)
                 continue
             # an int4 layer keeps its FP8 shared expert octet-tiled where the shapes allow (the
             # row-wave kernel's fast FP8 path), as the drop-in does
             tile = self.tiled or (self.i4 and sp.bc == 128 and all(r % 8 == 0 and c % 128 == 0 for r, c in shapes))
+            assert tile or not self.i4t, "the int4-tiled layer needs an octet-tiled shared expert"
             for m, (r, c) in enumerate(shapes):
                 strm = stream(K_SHARED, sp.layer, m) if i == NE else stream(K_EXPERT, sp.layer, i * 3 + m)
                 w, s = base + code_off[m], base + sc_off[m]
@@ -218,7 +230,8 @@ class DeviceLayer:
             routed_scale=sp.routed_scale, swiglu_limit=sp.limit, router=self.router.ptr, router_dt=1,
             bias=self.bias.ptr, experts=self.table.ptr,
             shared=(self.table.ptr + NE * C.sizeof(G53hExpert)) if sp.shared else None,
-            block_c=0 if self.i4 else sp.bc, tiled=(2 if self.mfma else 1) if self.tiled else 0)
+            block_c=sp.bc if self.i4t else (0 if self.i4 else sp.bc),
+            tiled=3 if self.i4t else ((2 if self.mfma else 1) if self.tiled else 0))
         check(L.g53h_sync(), "g53h_sync")
         del stage
         return self
@@ -233,6 +246,10 @@ class DeviceLayer:
                 s = np.empty(m.rows * m.scols, np.float32)
                 check(lib().g53h_d2h(w.ctypes.data, m.w, w.nbytes), "d2h")
                 check(lib().g53h_d2h(s.ctypes.data, m.s, s.nbytes), "d2h")
+                if m.flags & 16:                  # int4-tiled in HBM: the row-major levels
+                    rm = np.zeros_like(w)
+                    assert lib().g53h_tile_i4_host(rm.ctypes.data, w.ctypes.data, m.rows, m.cols, 1) == 0
+                    w = rm
                 out.append((w, s))
                 continue
             w = np.empty(m.rows * m.cols, np.uint8)

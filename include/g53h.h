@@ -78,6 +78,14 @@ int         g53h_mem_info(size_t *free_b, size_t *total_b);
  * column in the low nibble, minus 8), s one fp32 step per row and group of bc columns,
  * [rows][scols]; br is ignored (one step row per matrix row). cols must be even. */
 #define G53H_MAT_I4      4
+/* Int4 codes (with G53H_MAT_I4) in the int4-tiled layout the one-launch int4 decode streams:
+ * units of 8 rows x 256 columns (1 KB), unit (r / 8, c / 256) at ((r / 8) (cols / 256) + c / 256)
+ * KB; inside a unit row m holds 128 bytes at 128 m, as 8 runs of 16: run p holds accumulator
+ * g53h_tile_acc(p) of each of the block's four 64-column groups, group g in the run's bytes
+ * 4 g .. 4 g + 3, level i (column 64 g + acc + 8 i) in nibble i (the low nibble first). The steps
+ * stay [rows][cols / 64]. One 64-lane load of 16 bytes per lane reads a unit and leaves in each
+ * lane exactly the 8 levels of one of the reference's eight fp32 accumulators of four groups. */
+#define G53H_MAT_I4T     16
 typedef struct {
     const uint8_t *w;
     const float   *s;
@@ -161,7 +169,10 @@ typedef struct {
                                        tiled kernels; any other value the generic ones)     */
     int               tiled;        /* 1: every expert matrix (routed and shared) is in the
                                        octet-tiled layout (G53H_MAT_TILED), 2: MFMA-tiled
-                                       (G53H_MAT_MTILED), 0: row-major                       */
+                                       (G53H_MAT_MTILED), 3: routed experts int4, int4-tiled
+                                       (G53H_MAT_I4 | G53H_MAT_I4T), the shared expert FP8
+                                       octet-tiled (single-token decode only; block_c 128),
+                                       0: row-major                                          */
     /* Experts in the int4 format (G53H_MAT_I4, per matrix) need block_c = 0 and tiled = 0: the
        row-wave kernels then take them (and any FP8 matrix, such as the shared expert, in the
        same layer; an octet-tiled one streams fastest), exactly as glm53f_mm on a GLM53F_WI4
@@ -320,6 +331,10 @@ int g53h_tile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int 
 /* The same for the MFMA-tiled layout (G53H_MAT_MTILED); inverse != 0 converts back. */
 int g53h_mtile_f8(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse);
 int g53h_mtile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse);
+/* Int4 levels [rows][cols / 2] (row-major, the reference's GLM53F_WI4) to the int4-tiled layout
+ * (G53H_MAT_I4T); inverse != 0 converts back. rows a multiple of 8, cols of 256. */
+int g53h_tile_i4(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse);
+int g53h_tile_i4_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse);
 
 /* -------------------------------------------------------- checks and inputs ---- */
 /* y[i] = expf(x[i]) by the device restatement of glibc's expf (for exhaustive checks). */

@@ -92,3 +92,56 @@ def test_mfma_tiled_round_trip_and_operand_order():
                     assert np.array_equal(lane_bytes, np.arange(32 * g, 32 * g + 32))
                     assert np.all(tr[o8, b, :, g, m] == o8 * 8 + m)
                     assert np.all(tb[o8, b, :, g, m] == b)
+
+
+def i4tile(a, rows, cols, inverse=0):
+    out = np.zeros_like(a)
+    assert glm53h.lib().g53h_tile_i4_host(out.ctypes.data, a.ctypes.data, rows, cols, inverse) == 0
+    return out
+
+
+def levels(packed, rows, cols):
+    """Row-major int4 (the reference's GLM53F_WI4: low nibble = even column) to [rows][cols]."""
+    b = packed.reshape(rows, cols // 2)
+    out = np.empty((rows, cols), np.uint8)
+    out[:, 0::2] = b & 15
+    out[:, 1::2] = b >> 4
+    return out
+
+
+def test_int4_tiled_round_trip_and_accumulator_order():
+    """Int4-tiled units (G53H_MAT_I4T): 8 rows x 256 columns per KB; run p of a unit row holds,
+    for each of the block's four 64-column groups, the 8 levels of the reference's accumulator
+    g53h_tile_acc(p) (columns acc + 8 i, i = 0..7, the order of matmul_i4's lane l,
+    src/core/glm53f_ops.c:270-276), low nibble first."""
+    rng = np.random.default_rng(4)
+    for rows, cols in [(8, 256), (16, 512), (24, 768)]:
+        a = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+        t = i4tile(a, rows, cols)
+        assert not np.array_equal(t, a)
+        assert np.array_equal(i4tile(t, rows, cols, 1), a)
+        L = levels(a, rows, cols)
+        w = t.view(np.uint32).reshape(rows // 8, cols // 256, 8, 8, 4)     # octet, block, row, run, group
+        for o8 in range(rows // 8):
+            for blk in range(cols // 256):
+                for m in range(8):
+                    for p in range(8):
+                        acc = glm53h_tile_acc(p)
+                        for g in range(4):
+                            got = [(int(w[o8, blk, m, p, g]) >> (4 * i)) & 15 for i in range(8)]
+                            want = L[o8 * 8 + m, blk * 256 + 64 * g + acc + 8 * np.arange(8)]
+                            assert got == list(want)
+    # every (row, group) holds the same 64 levels, so a group's dot product is unchanged
+    rows, cols = 8, 256
+    a = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+    L = levels(a, rows, cols).astype(np.int64) - 8
+    t = i4tile(a, rows, cols).view(np.uint32).reshape(8, 8, 4)
+    x = rng.integers(-50, 50, cols)
+    for m in range(8):
+        for g in range(4):
+            s = 0
+            for p in range(8):
+                acc = glm53h_tile_acc(p)
+                for i in range(8):
+                    s += (((int(t[m, p, g]) >> (4 * i)) & 15) - 8) * int(x[64 * g + acc + 8 * i])
+            assert s == int(L[m, 64 * g:64 * g + 64] @ x[64 * g:64 * g + 64])
