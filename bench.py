@@ -642,7 +642,8 @@ def main():
                          "row-major (k_dec_layer, bit-exact); configs 3-4: tiled or rowmajor")
     ap.add_argument("--experts", default="fp8", choices=["fp8", "int4"],
                     help="config 2: routed experts as the checkpoint's FP8 (the metric) or re-quantised to the "
-                         "reference's int4 format (its --experts int4 mode; the row-wave kernels)")
+                         "reference's int4 format (its --experts int4 mode): one launch over int4-tiled slots, or "
+                         "with --layout rowmajor the five-launch row-wave kernels")
     a = ap.parse_args()
     if a.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (expert-parallel "
@@ -656,10 +657,12 @@ def main():
     L = glm53h.init(0)
     sp = S.spec(2)
     i4 = a.experts == "int4"
-    mfma = a.layout == "mfma" and not i4
-    tiled = a.layout == "tiled" and not i4
-    kname = "k_rows" if i4 else ("k_dec_mfma" if mfma else ("k_dec_tiled" if tiled else "k_dec_layer"))
-    layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4, mfma=mfma)
+    i4t = i4 and a.layout != "rowmajor"                 # int4: one launch over int4-tiled slots
+    i4 = i4 and not i4t                                  # (rowmajor: the five-launch row kernels)
+    mfma = a.layout == "mfma" and not (i4 or i4t)
+    tiled = (a.layout == "tiled" and not i4) or i4t
+    kname = "k_rows" if i4 else ("k_dec_tiled_i4" if i4t else ("k_dec_mfma" if mfma else ("k_dec_tiled" if tiled else "k_dec_layer")))
+    layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4 or i4t, mfma=mfma)
     cp = Copies(layer)
     x = S.x_host(sp, NTOK, batch=0)
     xs = DevBuf.from_array(x)
@@ -709,6 +712,9 @@ def main():
         # expert) with the SwiGLU between them, timed together by the profiled run's events
         dom_bytes = sp.K * sp.expert_i4_bytes() + eb
         dom_us = per["row_kernels_us"]
+    elif i4t:
+        # int4 in one launch: the router, 8 int4 experts and the FP8 shared expert
+        dom_bytes = sp.K * sp.expert_i4_bytes() + eb + router_bytes
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(layer, x, idx_all, a.cpu_seconds)
@@ -731,10 +737,10 @@ def main():
                  "us_per_layer": round(ex_us, 2), "achieved_GBps": round(ex_gbps, 1),
                  "hbm_peak_frac": round(ex_gbps / HBM_PEAK_GBPS, 4)}
         del ocp
-    prefill = None if (i4 or a.no_prefill) else prefill_beside(L, olayer, sp)
-    batched = None if (i4 or a.no_prefill) else batched_beside(L, olayer)
+    prefill = None if (i4 or i4t or a.no_prefill) else prefill_beside(L, olayer, sp)
+    batched = None if (i4 or i4t or a.no_prefill) else batched_beside(L, olayer)
     traffic = None                      # HBM bytes per launch from the committed counter summary
-    tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 else ''}_traffic.json")
+    tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 or i4t else ''}_traffic.json")
     if os.path.exists(tp):
         with open(tp) as f:
             traffic = json.load(f).get("traffic_bytes")
@@ -754,7 +760,8 @@ def main():
         "config": {"workload": "BASELINE config 2: single-token decode of one MoE layer, hidden 4096, "
                                "moe_inter 2048, 288 experts resident in HBM, top-8 + 1 shared",
                    "tokens_cycled": NTOK, "router_shared_copies": NCOPY,
-                   "expert_layout": "int4 row-major" if i4 else a.layout, "routed_experts": a.experts,
+                   "expert_layout": "int4 row-major" if i4 else ("int4-tiled" if i4t else a.layout),
+                   "routed_experts": a.experts,
                    "parity": ("routing bit-exact, outputs within 1e-2 abs + 2e-3 rel (FP8 matrix cores)" if mfma
                               else "bit-exact with the reference"),
                    "parallelism": "single GPU"},
