@@ -648,6 +648,8 @@ int g53h_set_speculate(int on)
 {
     const int prev = spec_enabled();
     g_spec = on ? 1 : 0;
+    g_spec_hist = 0xffffu;          /* a fresh history: the next layers speculate */
+    g_spec_tick = 0;
     return prev;
 }
 

@@ -158,7 +158,8 @@ int  g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **
  * before the reference's hint/get/release calls, which it then makes in the reference's order,
  * and runs the layer again only when a chosen expert had no landed slot. on = 0 makes every
  * layer route first and fetch before it computes. The environment variable G53H_NO_SPECULATE
- * sets the default to 0. Returns the previous setting. */
+ * sets the default to 0. It also clears the record of recent outcomes by which a layer decides
+ * whether to speculate. Returns the previous setting. */
 int  g53h_set_speculate(int on);
 /* Counts of cached single-token layers since the last call: out[0] finished by the speculative
  * launch, out[1] speculative and run again, out[2] not speculative. Resets them. */
