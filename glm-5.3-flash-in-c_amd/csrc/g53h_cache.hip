@@ -375,7 +375,11 @@ void cache_release(Glm53fExpertSrc *self, int layer, int expert)
     const int32_t key = layer * c->n_experts + expert;
     std::lock_guard<std::mutex> g(m->mu);
     const int slot = m->lru.slot_of[key];
-    if (slot >= 0 && m->lru.pins[slot] > 0) {
+    if (slot >= 0 && m->lru.pins[slot] > 0 && g53h_quiet()) {
+        /* every kernel launched so far has completed: a refill of the slot waits for nothing */
+        unuse(m, slot);
+        g53_lru_release(&m->lru, key);
+    } else if (slot >= 0 && m->lru.pins[slot] > 0) {
         /* one event for all releases between two get() calls: the caller launched the kernels
          * that read these slots before releasing any of them */
         if (m->cur_used < 0) {

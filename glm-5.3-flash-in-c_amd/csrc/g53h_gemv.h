@@ -194,4 +194,67 @@ __device__ __forceinline__ uint32_t g53_fkey(float f)
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+/* The maximum (or minimum) of v over the wave, in every lane, without leaving the vector
+ * unit: four DPP steps within each row of 16 lanes (lane xor 1, xor 2, the half-row mirror,
+ * the row mirror), then the gfx950 row-pair and half-wave swaps. The whole wave must be
+ * active. */
+template <bool MAX>
+__device__ __forceinline__ uint32_t g53_wall(uint32_t v)
+{
+    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true));   /* quad_perm 1,0,3,2 */
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true));   /* quad_perm 2,3,0,1 */
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, true));  /* row_half_mirror */
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, true));  /* row_mirror */
+    const auto p16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = op(p16[0], p16[1]);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return op(p32[0], p32[1]);
+}
+
+#ifndef G53_SEL_PER_LANE
+#define G53_SEL_PER_LANE 16   /* up to 1024 experts per wave */
+#endif
+/* route_topn (src/core/glm53f_ops.c:1021-1042): the scan starts from expert 0, so a NaN at
+ * index 0 wins the round (the taken expert is then -inf) and NaN elsewhere is skipped. */
+__device__ __forceinline__ void g53_topn_token(int t, int lane, int *__restrict__ idx, int n,
+                                               const float *__restrict__ choice, int NE,
+                                               const float *__restrict__ score, float *__restrict__ score_out)
+{
+    choice += (size_t)t * NE;
+    idx += (size_t)t * n;
+    float c[G53_SEL_PER_LANE];
+    for (int k = 0; k < G53_SEL_PER_LANE; k++) {
+        const int e = lane + 64 * k;
+        c[k] = e < NE ? choice[e] : NAN;
+    }
+    /* a round: each lane's first strictly greater (its lowest expert among equal values), then
+     * the wave's largest as a total-order key (+0 and -0 equal, 0 for no candidate) and the
+     * lowest expert holding it, both reduced in every lane (the whole wave runs this) */
+    for (int j = 0; j < n; j++) {
+        int best;
+        /* expert 0's value: a NaN there wins the round (and is -inf after it) */
+        if (__builtin_isnan(__uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(c[0]))))) {
+            best = 0;
+        } else {
+            float bv = -INFINITY;
+            int bi = -1;
+            for (int k = 0; k < G53_SEL_PER_LANE; k++) {
+                const int e = lane + 64 * k;
+                if (e < NE && c[k] == c[k] && (bi < 0 || c[k] > bv)) { bv = c[k]; bi = e; }
+            }
+            const uint32_t kb = bi < 0 ? 0u : g53_fkey(bv);
+            const uint32_t m = g53_wall<true>(kb);
+            const uint32_t lo = g53_wall<false>(kb == m && m != 0u ? (uint32_t)bi : 0xffffffffu);
+            best = lo == 0xffffffffu ? 0 : (int)lo;
+        }
+        for (int k = 0; k < G53_SEL_PER_LANE; k++)
+            if (lane + 64 * k == best) c[k] = -INFINITY;
+        if (lane == 0) {
+            idx[j] = best;
+            if (score_out) score_out[(size_t)t * n + j] = score[(size_t)t * NE + best];
+        }
+    }
+}
+
 #endif /* G53H_GEMV_H */

@@ -533,7 +533,6 @@ extern "C" int g53h_router(int *idx, float *w, const float *x, int T, const void
                             nan_flag, ws, nullptr, nullptr, nullptr);
 }
 
-#define G53_SEL_PER_LANE 16   /* up to 1024 experts per wave */
 
 /* Wave-wide argmax with the reference's rule: strictly greater wins, so the lowest index among
  * equal maxima; an empty candidate (index < 0) never wins. */
@@ -541,47 +540,6 @@ __device__ inline void g53_argmax_merge(float &bv, int &bi, float ov, int oi)
 {
     if (oi < 0) return;
     if (bi < 0 || ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-}
-
-/* route_topn (src/core/glm53f_ops.c:1021-1042): the scan starts from expert 0, so a NaN at
- * index 0 wins every round and NaN elsewhere is skipped. */
-__device__ __forceinline__ void g53_topn_token(int t, int lane, int *__restrict__ idx, int n,
-                                               const float *__restrict__ choice, int NE,
-                                               const float *__restrict__ score, float *__restrict__ score_out)
-{
-    choice += (size_t)t * NE;
-    idx += (size_t)t * n;
-    float c[G53_SEL_PER_LANE];
-    for (int k = 0; k < G53_SEL_PER_LANE; k++) {
-        const int e = lane + 64 * k;
-        c[k] = e < NE ? choice[e] : NAN;
-    }
-    for (int j = 0; j < n; j++) {
-        const float c0 = __shfl(c[0], 0);
-        int best;
-        if (c0 != c0) {
-            best = 0;
-        } else {
-            float bv = -INFINITY;
-            int bi = -1;
-            for (int k = 0; k < G53_SEL_PER_LANE; k++) {
-                const int e = lane + 64 * k;
-                if (e < NE && c[k] == c[k] && (bi < 0 || c[k] > bv)) { bv = c[k]; bi = e; }
-            }
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int oi = __shfl_xor(bi, o);
-                g53_argmax_merge(bv, bi, ov, oi);
-            }
-            best = bi < 0 ? 0 : bi;
-        }
-        for (int k = 0; k < G53_SEL_PER_LANE; k++)
-            if (lane + 64 * k == best) c[k] = -INFINITY;
-        if (lane == 0) {
-            idx[j] = best;
-            if (score_out) score_out[(size_t)t * n + j] = score[(size_t)t * NE + best];
-        }
-    }
 }
 
 __global__ void __launch_bounds__(64) k_route_topn(int *__restrict__ idx, int n,
@@ -746,6 +704,7 @@ extern "C" int g53h_route_decode(int *idx, float *w, int *nan_flag, int *pred, i
         hipLaunchKernelGGL(k_route_decode<16>, dim3(1), dim3(128), 0, g53h_stream(), idx, w, nan_flag, sc0, ch0, bias,
                            NE, K, norm_topk, routed_scale, pred, n, sc1, ch1, mb, mb_slot, off_w, seq);
     G53_LAUNCHED("k_route_decode");
+    if (mb) g53h_note_publish(mb_slot, seq);
     return 0;
 }
 
@@ -759,6 +718,7 @@ float *g53h_next_buf(void)
     return g_next;
 }
 G53NextReq *g53h_next_req(void) { return &g_next_req; }
+
 
 extern "C" int g53h_decode_next(const float *x, const void *next_gate, int next_dt, const float *next_bias, int NE,
                                 int E)
@@ -802,10 +762,19 @@ __global__ void __launch_bounds__(256) k_dec_publish(unsigned *__restrict__ mb, 
         r[i] = (unsigned)(i < K ? idx[i] : i == K ? nan : pred[i - K - 1]);
     uint32_t *d = mb + out_off_w;
     for (int i = threadIdx.x; i < G53H_NERR; i += 256) d[i] = (uint32_t)errs[i];
-    for (int i = threadIdx.x; i < nw; i += 256) d[G53H_NERR + i] = out[i];
+    g53_copy_words(d + G53H_NERR, out, nw, (int)threadIdx.x, 256);
     __threadfence_system();
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(mb + slot, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+/* The mailbox areas of a publication: in range, word-aligned, not overlapping. */
+static int pub_areas_bad(int slot, size_t route_off, int K, int n, size_t out_off, size_t out_bytes)
+{
+    return slot < 0 || slot >= G53H_MBOX_SLOTS || route_off % 4 || out_off % 4 || out_bytes % 4 ||
+           route_off < G53H_MBOX_SLOTS * 4 || out_off < G53H_MBOX_SLOTS * 4 ||
+           route_off + 4 * (size_t)(K + 1 + n) > G53H_MBOX_BYTES || out_off + 4 * G53H_NERR + out_bytes > G53H_MBOX_BYTES ||
+           (route_off < out_off + 4 * G53H_NERR + out_bytes && out_off < route_off + 4 * (size_t)(K + 1 + n));
 }
 
 extern "C" int g53h_decode_publish(int slot, unsigned seq, size_t route_off, const int *idx_d, int K, int *pred_d,
@@ -820,15 +789,13 @@ extern "C" int g53h_decode_publish(int slot, unsigned seq, size_t route_off, con
             g53h_route_next(g_next_req.x, g_next_req.gate, g_next_req.dt, g_next_req.bias, g_next_req.NE, g_next_req.E))
             return g53h_fail("g53h_decode_publish: the next layer's scores (%d experts) cannot be computed", NE);
     }
-    if (slot < 0 || slot >= G53H_MBOX_SLOTS || route_off % 4 || out_off % 4 || out_bytes % 4 ||
-        route_off < G53H_MBOX_SLOTS * 4 || out_off < G53H_MBOX_SLOTS * 4 ||
-        route_off + 4 * (size_t)(K + 1 + n) > G53H_MBOX_BYTES || out_off + 4 * G53H_NERR + out_bytes > G53H_MBOX_BYTES ||
-        (route_off < out_off + 4 * G53H_NERR + out_bytes && out_off < route_off + 4 * (size_t)(K + 1 + n)))
+    if (pub_areas_bad(slot, route_off, K, n, out_off, out_bytes))
         return g53h_fail("g53h_decode_publish: slot %d, routing at %zu, %zu bytes at %zu", slot, route_off, out_bytes,
                          out_off);
     hipLaunchKernelGGL(k_dec_publish, dim3(1), dim3(256), 0, g53h_stream(), g53h_mailbox_dev(), slot, seq,
                        (int)(route_off / 4), idx_d, K, pred_d, n, g_next, g_next + 1024, NE, (int)(out_off / 4),
                        (const uint32_t *)out_d, (int)(out_bytes / 4), g53h_errblock());
     G53_LAUNCHED("k_dec_publish");
+    g53h_note_publish(slot, seq);
     return 0;
 }

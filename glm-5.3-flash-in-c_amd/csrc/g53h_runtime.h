@@ -22,7 +22,12 @@ int  g53h_num_cus(void);
 unsigned *g53h_mailbox_dev(void);    /* device address of the host mailbox             */
 int g53h_current_device(void);        /* the device g53h_init bound, -1 before it      */
 int g53_noalloc_setup(int device);    /* scratch address of the no-alloc decode (init)  */
-hipStream_t g53h_stream(void);        /* compute stream (initialises on first use)      */
+hipStream_t g53h_stream(void);        /* compute stream; each call counts as an enqueue on it */
+/* After enqueuing a kernel that writes sequence word `slot` of the mailbox last. */
+void g53h_note_publish(int slot, unsigned seq);
+/* 1 while the compute stream is quiet: a mailbox wait saw the last publication's sequence word
+ * and nothing has been enqueued on the stream since. */
+int g53h_quiet(void);
 hipStream_t g53h_copy_stream(void);   /* side stream for host-to-HBM expert copies     */
 /* g53h_tile_f8 on stream s (the expert cache tiles on its copy streams). */
 int g53h_tile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, hipStream_t s);
@@ -62,5 +67,18 @@ int         g53h_spin_limit(void);
 enum { G53_PROF_START = 0, G53_PROF_ROUTER = 1, G53_PROF_GATEUP = 2, G53_PROF_DOWN = 3,
        G53_PROF_GENERIC = 4, G53_PROF_GROUPED = 5, G53_PROF_COMBINE = 6, G53_PROF_FUSED = 7, G53_PROF_NTAGS = 8 };
 void        g53h_prof_mark(int tag);
+
+/* nw words from src to d by nt threads: 16 bytes a store where both are 16-byte aligned
+ * (stores into host memory cross the link, and fewer, larger writes go faster), else 4. */
+__device__ __forceinline__ void g53_copy_words(uint32_t *d, const uint32_t *src, int nw, int tid, int nt)
+{
+    if ((((uintptr_t)d | (uintptr_t)src) & 15) == 0) {
+        const int n4 = nw >> 2;
+        for (int i = tid; i < n4; i += nt) ((uint4 *)d)[i] = ((const uint4 *)src)[i];
+        for (int i = 4 * n4 + tid; i < nw; i += nt) d[i] = src[i];
+    } else {
+        for (int i = tid; i < nw; i += nt) d[i] = src[i];
+    }
+}
 
 #endif /* G53H_RUNTIME_H */

@@ -89,7 +89,26 @@ int g53h_current_device(void) { return g_ready ? g_device : -1; }
 
 extern "C" int g53h_ready(void) { return g_ready ? 0 : g53h_init(0); }
 extern "C" int g53h_num_cus(void) { return g_cus; }
-hipStream_t g53h_stream(void) { return g_stream; }
+/* Operations enqueued on the compute stream (every use of it through g53h_stream or enq counts
+ * as one), and the last mailbox publication: when a wait sees that publication's sequence word
+ * and nothing was enqueued after it, the stream is quiet (every kernel before it has completed). */
+static unsigned long g_enq = 0, g_pub_enq = 0;
+static int g_pub_slot = -1, g_quiet = 0;
+static unsigned g_pub_seq = 0;
+static hipStream_t enq(void)
+{
+    g_enq++;
+    g_quiet = 0;
+    return g_stream;
+}
+hipStream_t g53h_stream(void) { return enq(); }
+void g53h_note_publish(int slot, unsigned seq)
+{
+    g_pub_enq = g_enq;
+    g_pub_slot = slot;
+    g_pub_seq = seq;
+}
+int g53h_quiet(void) { return g_quiet; }
 hipStream_t g53h_copy_stream(void) { return g_copy; }
 int *g53h_counters(void) { return g_counters; }
 int *g53h_errblock(void) { return g_errs; }
@@ -112,7 +131,7 @@ extern "C" int g53h_inbox_fetch(void *dst_d, size_t off, size_t bytes)
         return g53h_fail("g53h_inbox_fetch: %zu bytes at %zu", bytes, off);
     if (!bytes) return 0;
     const int n16 = (int)(bytes / 16);
-    hipLaunchKernelGGL(k_inbox_fetch, dim3((n16 + 255) / 256), dim3(256), 0, g_stream, (uint4 *)dst_d,
+    hipLaunchKernelGGL(k_inbox_fetch, dim3((n16 + 255) / 256), dim3(256), 0, enq(), (uint4 *)dst_d,
                        (const uint4 *)(g_inbox_d + off), n16);
     G53_LAUNCHED("k_inbox_fetch");
     return 0;
@@ -125,10 +144,17 @@ extern "C" int g53h_mailbox_wait(int slot, unsigned seq)
     const volatile unsigned *w = g_mbox + slot;
     /* spin while the stream works; after ~1e6 polls fall back to a blocking wait, which also
      * reports an error the stream hit (then the word never arrives) */
+    const int last = slot == g_pub_slot && seq == g_pub_seq && g_enq == g_pub_enq;
     for (long i = 0; i < (1L << 20); i++)
-        if (__atomic_load_n(w, __ATOMIC_ACQUIRE) == seq) return 0;
+        if (__atomic_load_n(w, __ATOMIC_ACQUIRE) == seq) {
+            if (last) g_quiet = 1;
+            return 0;
+        }
     G53_TRY(hipStreamSynchronize(g_stream));
-    if (__atomic_load_n(w, __ATOMIC_ACQUIRE) == seq) return 0;
+    if (__atomic_load_n(w, __ATOMIC_ACQUIRE) == seq) {
+        if (last) g_quiet = 1;
+        return 0;
+    }
     return g53h_fail("g53h_mailbox_wait: slot %d never reached %u", slot, seq);
 }
 
@@ -139,7 +165,7 @@ __global__ void __launch_bounds__(256) k_publish(unsigned *__restrict__ mb, cons
 {
     uint32_t *d = mb + off_w;
     for (int i = threadIdx.x; i < G53H_NERR; i += 256) d[i] = (uint32_t)errs[i];
-    for (int i = threadIdx.x; i < nw; i += 256) d[G53H_NERR + i] = src[i];
+    g53_copy_words(d + G53H_NERR, src, nw, (int)threadIdx.x, 256);
     __threadfence_system();
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(mb + slot, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -151,9 +177,10 @@ extern "C" int g53h_publish(int slot, unsigned seq, size_t off, const void *src_
     if (slot < 0 || slot >= G53H_MBOX_SLOTS || off % 4 || bytes % 4 || off < G53H_MBOX_SLOTS * 4 ||
         off + (G53H_NERR * 4) + bytes > G53H_MBOX_BYTES)
         return g53h_fail("g53h_publish: slot %d, %zu bytes at %zu", slot, bytes, off);
-    hipLaunchKernelGGL(k_publish, dim3(1), dim3(256), 0, g_stream, g_mbox_d, (const uint32_t *)src_d, (int)(bytes / 4),
+    hipLaunchKernelGGL(k_publish, dim3(1), dim3(256), 0, enq(), g_mbox_d, (const uint32_t *)src_d, (int)(bytes / 4),
                        g_errs, (int)(off / 4), slot, seq);
     G53_LAUNCHED("k_publish");
+    g53h_note_publish(slot, seq);
     return 0;
 }
 
@@ -180,7 +207,7 @@ extern "C" int g53h_inject_errors(int word, int bits)
 {
     if (g53h_ready()) return -1;
     if (word < 0 || word >= G53H_NERR) return g53h_fail("g53h_inject_errors: word %d of %d", word, G53H_NERR);
-    hipLaunchKernelGGL(k_errs_or, dim3(1), dim3(64), 0, g_stream, g_errs, word, bits);
+    hipLaunchKernelGGL(k_errs_or, dim3(1), dim3(64), 0, enq(), g_errs, word, bits);
     G53_LAUNCHED("k_errs_or");
     return 0;
 }
@@ -188,15 +215,15 @@ extern "C" int g53h_inject_errors(int word, int bits)
 extern "C" int g53h_errors_peek_async(int *host)
 {
     if (g53h_ready()) return -1;
-    G53_TRY(hipMemcpyAsync(host, g_errs, G53H_NERR * sizeof(int), hipMemcpyDeviceToHost, g_stream));
+    G53_TRY(hipMemcpyAsync(host, g_errs, G53H_NERR * sizeof(int), hipMemcpyDeviceToHost, enq()));
     return 0;
 }
 
 extern "C" int g53h_errors_async(int *host)
 {
     if (g53h_ready()) return -1;
-    G53_TRY(hipMemcpyAsync(host, g_errs, G53H_NERR * sizeof(int), hipMemcpyDeviceToHost, g_stream));
-    hipLaunchKernelGGL(k_errs_clear, dim3(1), dim3(64), 0, g_stream, g_errs);
+    G53_TRY(hipMemcpyAsync(host, g_errs, G53H_NERR * sizeof(int), hipMemcpyDeviceToHost, enq()));
+    hipLaunchKernelGGL(k_errs_clear, dim3(1), dim3(64), 0, enq(), g_errs);
     G53_LAUNCHED("k_errs_clear");
     return 0;
 }
@@ -245,7 +272,7 @@ extern "C" int g53h_h2d(void *dst, const void *src, size_t n)
 {
     if (g53h_ready()) return -1;
     if (!n) return 0;
-    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_stream));
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, enq()));
     G53_TRY(hipStreamSynchronize(g_stream));
     return 0;
 }
@@ -254,7 +281,7 @@ extern "C" int g53h_h2d_async(void *dst, const void *src, size_t n)
 {
     if (g53h_ready()) return -1;
     if (!n) return 0;
-    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_stream));
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, enq()));
     return 0;
 }
 
@@ -262,7 +289,7 @@ extern "C" int g53h_d2h(void *dst, const void *src, size_t n)
 {
     if (g53h_ready()) return -1;
     if (!n) return 0;
-    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_stream));
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, enq()));
     G53_TRY(hipStreamSynchronize(g_stream));
     return 0;
 }
@@ -271,7 +298,7 @@ extern "C" int g53h_d2h_async(void *dst, const void *src, size_t n)
 {
     if (g53h_ready()) return -1;
     if (!n) return 0;
-    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_stream));
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, enq()));
     return 0;
 }
 
@@ -279,7 +306,7 @@ extern "C" int g53h_d2d(void *dst, const void *src, size_t n)
 {
     if (g53h_ready()) return -1;
     if (!n) return 0;
-    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, g_stream));
+    G53_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, enq()));
     return 0;
 }
 
@@ -287,7 +314,7 @@ extern "C" int g53h_memset(void *dst, int v, size_t n)
 {
     if (g53h_ready()) return -1;
     if (!n) return 0;
-    G53_TRY(hipMemsetAsync(dst, v, n, g_stream));
+    G53_TRY(hipMemsetAsync(dst, v, n, enq()));
     return 0;
 }
 
@@ -305,7 +332,7 @@ extern "C" int g53h_is_device_ptr(const void *p)
 extern "C" int g53h_mark(void)
 {
     if (g53h_ready()) return -1;
-    G53_TRY(hipEventRecord(g_ev[g_ev_next], g_stream));
+    G53_TRY(hipEventRecord(g_ev[g_ev_next], enq()));
     g_ev_next ^= 1;
     return 0;
 }
@@ -369,7 +396,7 @@ extern "C" int g53h_prof_enable(int on)
 void g53h_prof_mark(int tag)
 {
     if (!g_prof_on || g_prof_n >= G53_PROF_EVENTS) return;
-    if (hipEventRecord(g_prof_ev[g_prof_n], g_stream) != hipSuccess) return;
+    if (hipEventRecord(g_prof_ev[g_prof_n], enq()) != hipSuccess) return;
     g_prof_tag[g_prof_n++] = tag;
 }
 

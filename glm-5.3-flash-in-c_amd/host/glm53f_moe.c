@@ -594,7 +594,7 @@ static G53Buf g_ident;
 #define G53_MB_ROUTE 0
 #define G53_MB_ROUTE_OFF 1024
 #define G53_MB_OUT 1
-#define G53_MB_OUT_OFF 4096
+#define G53_MB_OUT_OFF 4100                 /* the output after the 3 error words: 16-byte aligned */
 static unsigned g_seq;
 static unsigned next_seq(void)
 {
@@ -743,8 +743,11 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = 1;
         SL.n_experts = NE; SL.experts = stab_d;
         SL.shared = with_shared ? shared_desc(w) : NULL;
+        HP(7);
         if (per > 0 && g53h_decode_next(xd, ngate, ndt, nbias, NE, E)) g53_die("glm53f_router");
+        HP(14);
         if (g53h_moe(od, xd, 1, &SL, idx_d, w_d)) g53_die("glm53f_moe");
+        HP(15);
         const unsigned seq_s = next_seq();
         if (g53h_decode_publish(G53_MB_OUT, seq_s, G53_MB_ROUTE_OFF, idx_d, K, pred_d, per, NE, G53_MB_OUT_OFF, od, ob))
             g53_die("glm53f_moe");

@@ -88,7 +88,7 @@ def test_route_topn_scores_are_the_sigmoid(L):
 
 def test_route_topn_ties_and_nan(L):
     """All-equal choices pick the lowest indices in order; a NaN at index 0 is taken first, a
-    NaN elsewhere never (the strict > of the reference's scan)."""
+    NaN elsewhere never (the strict > of the reference's scan); -inf choices come last."""
     E, NE = 64, 40
     x = np.ones((1, E), np.float32)
     W = np.zeros((NE, E), np.float32)
@@ -97,6 +97,11 @@ def test_route_topn_ties_and_nan(L):
         bb = np.linspace(0, 1, NE).astype(np.float32)
         bb[bad] = np.nan
         cases.append(bb)
+    # -inf choices: taken last, lowest index first; once every value is -inf (taken experts are
+    # -inf too) the scan returns expert 0 again
+    bb = np.linspace(0, 1, NE).astype(np.float32)
+    bb[[3, 9, 30]] = -np.inf
+    cases.append(bb)
     for b in cases:
         for n in (1, 7, 40):
             assert np.array_equal(topn_gpu(L, x, W, b, n), topn_oracle(x, W, b, n)), (b, n)

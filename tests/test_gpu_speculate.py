@@ -42,7 +42,7 @@ def mailbox_words(L, off, n, dtype):
     return np.frombuffer(C.string_at(base + off, 4 * n), dtype).copy()
 
 
-def publish_round(L, layer, x, Wn, bn, n, seq):
+def publish_round(L, layer, x, Wn, bn, n, seq, out_off=OUT_OFF):
     sp = layer.sp
     xd = DevBuf.from_array(np.ascontiguousarray(x[0]))
     gate = DevBuf.from_array((np.ascontiguousarray(Wn, np.float32).view(np.uint32) >> 16).astype(np.uint16))
@@ -50,12 +50,12 @@ def publish_round(L, layer, x, Wn, bn, n, seq):
     out, idx, w, pred = DevBuf(sp.E * 4), DevBuf(sp.K * 4), DevBuf(sp.K * 4), DevBuf(max(n, 1) * 4)
     check(L.g53h_decode_next(xd.ptr, gate.ptr, 1, bd.ptr, sp.NE, sp.E), "g53h_decode_next")
     layer.forward(out, xd, 1, idx, w)
-    check(L.g53h_decode_publish(SLOT, seq, ROUTE_OFF, idx.ptr, sp.K, pred.ptr, n, sp.NE, OUT_OFF, out.ptr, sp.E * 4),
+    check(L.g53h_decode_publish(SLOT, seq, ROUTE_OFF, idx.ptr, sp.K, pred.ptr, n, sp.NE, out_off, out.ptr, sp.E * 4),
           "g53h_decode_publish")
     check(L.g53h_mailbox_wait(SLOT, seq), "mailbox wait")
     r = mailbox_words(L, ROUTE_OFF, sp.K + 1 + n, np.int32)
-    errs = mailbox_words(L, OUT_OFF, NERR, np.int32)
-    o = mailbox_words(L, OUT_OFF + 4 * NERR, sp.E, np.float32)
+    errs = mailbox_words(L, out_off, NERR, np.int32)
+    o = mailbox_words(L, out_off + 4 * NERR, sp.E, np.float32)
     glm53h.sync()
     assert np.array_equal(o.view(np.uint32), out.download(np.float32).view(np.uint32))
     assert np.array_equal(r[:sp.K], idx.download(np.int32))
@@ -73,7 +73,9 @@ def test_next_scores_in_the_tiled_decode(L, tiled):
     x = S.x_host(sp, 3, batch=4)
     for t in range(3):
         say("tiled decode + next scores + publish, token", t)
-        ids, nan, pred, errs, out, w = publish_round(L, tiled, x[t:t + 1], Wn, bn, 6, 900 + t)
+        # the output 16-byte aligned in the mailbox (16-byte stores) on the last token
+        ids, nan, pred, errs, out, w = publish_round(L, tiled, x[t:t + 1], Wn, bn, 6, 900 + t,
+                                                     OUT_OFF + 4 if t == 2 else OUT_OFF)
         assert nan == 0 and not errs[:3].any()
         assert np.array_equal(pred, topn_oracle(x[t:t + 1], Wn, bn, 6)[0])
         mats = {int(e): tiled.fetch_expert(int(e)) for e in ids}
