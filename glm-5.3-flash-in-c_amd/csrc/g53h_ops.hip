@@ -753,16 +753,20 @@ __global__ void __launch_bounds__(256) k_dec_publish(unsigned *__restrict__ mb, 
                                                      const uint32_t *__restrict__ out, int nw,
                                                      const int *__restrict__ errs)
 {
-    if (threadIdx.x < 64 && n > 0) g53_topn_token(0, (int)threadIdx.x, pred, n, choice, NE, score, nullptr);
+    /* wave 0 the top-n while the other waves copy the error words and the output */
+    if (threadIdx.x < 64) {
+        if (n > 0) g53_topn_token(0, (int)threadIdx.x, pred, n, choice, NE, score, nullptr);
+    } else {
+        uint32_t *d = mb + out_off_w;
+        for (int i = threadIdx.x - 64; i < G53H_NERR; i += 192) d[i] = (uint32_t)errs[i];
+        g53_copy_words(d + G53H_NERR, out, nw, (int)threadIdx.x - 64, 192);
+    }
     __threadfence_block();
     __syncthreads();
     unsigned *r = mb + route_off_w;
     const int nan = ((errs[0] | errs[1]) & 2) ? 1 : 0;
     for (int i = threadIdx.x; i < K + 1 + n; i += 256)
         r[i] = (unsigned)(i < K ? idx[i] : i == K ? nan : pred[i - K - 1]);
-    uint32_t *d = mb + out_off_w;
-    for (int i = threadIdx.x; i < G53H_NERR; i += 256) d[i] = (uint32_t)errs[i];
-    g53_copy_words(d + G53H_NERR, out, nw, (int)threadIdx.x, 256);
     __threadfence_system();
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(mb + slot, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);

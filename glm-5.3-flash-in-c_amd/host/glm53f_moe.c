@@ -673,6 +673,22 @@ static const G53hExpert *shared_desc(const Glm53fMoeW *w)
     return d + l;
 }
 
+/* x (host memory) into xd without a wait: through the mapped inbox, read by a kernel on the
+ * compute stream (the previous call's fetch has run: its output was waited for), or a copy from
+ * pinned staging when it does not fit the inbox. */
+static void upload_x(float *xd, const float *x, int E)
+{
+    const size_t xb = (size_t)E * sizeof(float);
+    if (xb <= G53H_INBOX_BYTES && xb % 16 == 0) {
+        memcpy(g53h_inbox(), x, xb);
+        if (g53h_inbox_fetch(xd, 0, xb)) g53_die("glm53f_moe");
+    } else {
+        float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, xb);
+        memcpy(xp, x, xb);
+        if (g53h_h2d_async(xd, xp, xb)) g53_die("glm53f_moe");
+    }
+}
+
 static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const Glm53fCfg *c, int with_shared)
 {
     const int E = c->hidden, K = c->topk, NE = c->n_experts;
@@ -681,21 +697,11 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     double hp_t = hp_now();
     g_hp_n++;
 #endif
+    /* x goes up right before the first launch that reads it (upload_x below), after the host's
+     * preparation, so that the layer kernel's launch follows the fetch closely */
     float *xd = (float *)x;
-    if (!g53h_is_device_ptr(x)) {                   /* x up without a wait */
-        const size_t xb = (size_t)E * sizeof(float);
-        xd = (float *)buf_get(&g_xin, xb);
-        if (xb <= G53H_INBOX_BYTES && xb % 16 == 0) {
-            /* through the mapped inbox, read by a kernel on the compute stream (the previous
-             * call's fetch has run: its output was waited for) */
-            memcpy(g53h_inbox(), x, xb);
-            if (g53h_inbox_fetch(xd, 0, xb)) g53_die("glm53f_moe");
-        } else {
-            float *xp = (float *)pinned(&g_pin_x, &g_pin_x_n, xb);
-            memcpy(xp, x, xb);
-            if (g53h_h2d_async(xd, xp, xb)) g53_die("glm53f_moe");
-        }
-    }
+    const int x_host = !g53h_is_device_ptr(x);
+    if (x_host) xd = (float *)buf_get(&g_xin, (size_t)E * sizeof(float));
     HP(8);
     const int per_max = 2 * GLM53F_MAX_TOPK;
     int *rd = (int *)buf_get(&g_idx, (size_t)(K + 1 + per_max) * sizeof(int));
@@ -744,6 +750,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         SL.n_experts = NE; SL.experts = stab_d;
         SL.shared = with_shared ? shared_desc(w) : NULL;
         HP(7);
+        if (x_host) upload_x(xd, x, E);
         if (per > 0 && g53h_decode_next(xd, ngate, ndt, nbias, NE, E)) g53_die("glm53f_router");
         HP(14);
         if (g53h_moe(od, xd, 1, &SL, idx_d, w_d)) g53_die("glm53f_moe");
@@ -759,6 +766,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         /* routing, NaN flag and the next layer's prediction: two launches, and the kernel writes
          * the host's copy into the mailbox, which the host polls */
         const unsigned seq_r = next_seq();
+        if (x_host) upload_x(xd, x, E);
         if (g53h_route_decode(idx_d, w_d, flag_d, pred_d, per, xd, gate, dt, bias, ngate, ndt, nbias, NE, E, K,
                               c->norm_topk, c->routed_scale, G53_MB_ROUTE, seq_r, G53_MB_ROUTE_OFF))
             g53_die("glm53f_router");
