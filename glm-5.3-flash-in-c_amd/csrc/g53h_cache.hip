@@ -21,6 +21,8 @@
  *     slot's GLM53F_WI4 levels and steps from there on the same stream (the reference
  *     quantises on its I/O threads, src/cache/glm53f_cache.c:114-127); the slot layout is the
  *     reference's (src/io/glm53f_load.c:141-163), so a budget holds the same number of slots.
+ *     In int4 mode 2 the levels are quantised into staging and int4-tiled into the slot (the
+ *     same bytes per slot), for the one-launch int4 decode.
  * Every entry point takes one mutex, as the reference's. */
 #include <hip/hip_runtime.h>
 
@@ -74,7 +76,10 @@ struct Impl {
      * are tiled into the slot by a kernel on the same stream, so one buffer per stream suffices */
     bool tiled = false;
     bool i4 = false;                /* int4 slots: FP8 staged, quantised into the slot      */
+    bool i4t = false;               /* int4 mode 2: the levels quantised into staging, then
+                                       int4-tiled into the slot (the steps straight in)     */
     uint8_t *stage_demand = nullptr, *stage_prefetch = nullptr;
+    size_t stage_lv = 0;            /* int4 mode 2: the levels' offset in a staging buffer  */
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
     /* tiled slots: the descriptor of every key whose read has been seen complete, per layer in
@@ -167,7 +172,7 @@ void table_set(Glm53fCache *c, Impl *m, int slot, int layer, int expert)
     for (int i = 0; i < 3; i++) {
         d[i]->w = (const uint8_t *)v[i]->w; d[i]->s = v[i]->s;
         d[i]->rows = v[i]->rows; d[i]->cols = v[i]->cols; d[i]->br = v[i]->br; d[i]->bc = v[i]->bc;
-        d[i]->scols = v[i]->scols; d[i]->flags = G53H_MAT_TILED;
+        d[i]->scols = v[i]->scols; d[i]->flags = m->i4t ? (G53H_MAT_I4 | G53H_MAT_I4T) : G53H_MAT_TILED;
     }
     m->tab_key[slot] = key;
     m->tab_dirty[layer] = 1;
@@ -258,10 +263,13 @@ int issue_reads(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStr
         f.w = stage; f.s = (const float *)(stage + sc_off);
         f.rows = m->geo.rows[i]; f.cols = m->geo.cols[i]; f.br = m->geo.br[i]; f.bc = m->geo.bc[i];
         f.scols = m->geo.scols[i];
+        /* int4 mode 2: the levels into staging after the FP8 bytes, then tiled into the slot */
+        uint8_t *lv = m->i4t ? stage + m->stage_lv : base + m->geo.off[i];
         if (hipMemcpyAsync(stage, mats[i]->w, m->geo.fbytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
             hipMemcpyAsync(stage + sc_off, mats[i]->s, m->geo.fbytes[3 + i], hipMemcpyHostToDevice, s) !=
                 hipSuccess ||
-            g53h_i4_from_f8_on(base + m->geo.off[i], (float *)(base + m->geo.off[3 + i]), &f, s))
+            g53h_i4_from_f8_on(lv, (float *)(base + m->geo.off[3 + i]), &f, s) ||
+            (m->i4t && g53h_tile_i4_on(base + m->geo.off[i], lv, m->geo.rows[i], m->geo.cols[i], 0, s)))
             return 0;
         *nread += (int64_t)(m->geo.fbytes[i] + m->geo.fbytes[3 + i]);
     }
@@ -307,7 +315,7 @@ void view_of(const Glm53fCache *c, const Impl *m, int slot, Glm53fExpertQ *q)
         Glm53fMat &v = *mats[i];
         v.w = base + m->geo.off[i];
         v.s = (const float *)(base + m->geo.off[3 + i]);
-        v.dt = m->i4 ? GLM53F_WI4 : (m->tiled ? GLM53F_WF8T : GLM53F_WF8);
+        v.dt = m->i4 ? (m->i4t ? GLM53F_WI4T : GLM53F_WI4) : (m->tiled ? GLM53F_WF8T : GLM53F_WF8);
         v.rows = m->geo.rows[i]; v.cols = m->geo.cols[i];
         if (m->i4) {                                 /* glm53f_expert_i4_view's geometry */
             v.br = 1; v.bc = GLM53F_I4_GROUP; v.scols = m->geo.cols[i] / GLM53F_I4_GROUP;
@@ -457,6 +465,13 @@ void cache_hint(Glm53fExpertSrc *self, int layer, const int *ids, int n)
 
 extern "C" int g53h_cache_is(const Glm53fExpertSrc *src) { return src && src->get == cache_get; }
 
+extern "C" int g53h_cache_slot_kind(const Glm53fExpertSrc *src)
+{
+    if (!g53h_cache_is(src)) return 0;
+    const Impl *m = impl_of((const Glm53fCache *)src);
+    return !m ? 0 : m->tiled ? 1 : m->i4t ? 3 : 0;
+}
+
 extern "C" int g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **table_d,
                                       const G53hExpert **table_h)
 {
@@ -548,7 +563,11 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
     m->tiled = !getenv("GLM53F_CACHE_ROWMAJOR") && m->geo.rows[0] == 2048 && m->geo.cols[0] == 4096 &&
                m->geo.rows[1] == 2048 && m->geo.cols[1] == 4096 && m->geo.rows[2] == 4096 && m->geo.cols[2] == 2048;
     for (int i = 0; i < 3; i++) m->tiled = m->tiled && m->geo.br[i] == 128 && m->geo.bc[i] == 128;
+    /* int4 mode 2 at the shapes the octet test above accepts (their rows are multiples of 8 and
+     * columns of 256, as the int4 tiling needs) */
+    m->i4t = m->i4 && i4 == 2 && m->tiled;
     if (m->i4) m->tiled = false;
+    if (m->i4t) c->i4 = 2;
     c->nslot = (int)(budget_bytes / c->slot_bytes);
     if (c->nslot < cfg->topk + 1) {
         fprintf(stderr, "glm53f_cache: budget %.2f GB gives %d slots of %.2f MB; top-%d needs at least %d\n",
@@ -579,15 +598,21 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
     ok = ok && hipStreamCreateWithFlags(&m->prefetch, hipStreamNonBlocking) == hipSuccess;
     if (ok && (m->tiled || m->i4)) {
         size_t sb = 0;                               /* the largest matrix (with its scales) */
+        size_t lb = 0;                               /* the largest matrix's int4 levels */
         for (int i = 0; i < 3; i++) {
             const size_t need = m->i4 ? al(m->geo.fbytes[i], 256) + m->geo.fbytes[3 + i] : m->geo.bytes[i];
             if (need > sb) sb = need;
+            if (m->i4 && m->geo.bytes[i] > lb) lb = m->geo.bytes[i];
+        }
+        if (m->i4t) {
+            m->stage_lv = al(sb, 256);
+            sb = m->stage_lv + lb;
         }
         m->stage_demand = (uint8_t *)g53h_alloc(sb);
         m->stage_prefetch = (uint8_t *)g53h_alloc(sb);
         ok = m->stage_demand && m->stage_prefetch;
     }
-    if (ok && m->tiled) {
+    if (ok && (m->tiled || m->i4t)) {
         const size_t tb = (size_t)c->n_layers * (size_t)c->n_experts * sizeof(G53hExpert);
         m->tab_h = (G53hExpert *)g53h_host_alloc(tb);
         m->tab_d = (G53hExpert *)g53h_alloc(tb);

@@ -48,7 +48,7 @@ class G53hMoeLayer(C.Structure):
 # -------------------------------------------------------------- structs (glm53f.h) ----
 GLM53F_MAX_LAYERS = 256
 GLM53F_MAX_EOS = 8
-GLM53F_WF32, GLM53F_WBF16, GLM53F_WF8, GLM53F_WI4, GLM53F_WF8T = 0, 1, 2, 3, 0x102
+GLM53F_WF32, GLM53F_WBF16, GLM53F_WF8, GLM53F_WI4, GLM53F_WF8T, GLM53F_WI4T = 0, 1, 2, 3, 0x102, 0x103
 
 
 class Glm53fCfg(C.Structure):
@@ -258,6 +258,7 @@ _SIGS = {
     "glm53f_cache_report": (None, [C.POINTER(Glm53fCache), C.c_char_p]),
     "glm53f_cache_sync": (C.c_int, [C.POINTER(Glm53fCache)]),
     "g53h_cache_is": (C.c_int, [C.POINTER(Glm53fExpertSrc)]),
+    "g53h_cache_slot_kind": (C.c_int, [C.POINTER(Glm53fExpertSrc)]),
     "g53h_set_speculate": (C.c_int, [C.c_int]),
     "g53h_speculate_counts": (None, [C.c_void_p]),
     "g53h_cache_layer_table": (C.c_int, [C.POINTER(Glm53fExpertSrc), C.c_int, C.POINTER(C.c_void_p),

@@ -35,8 +35,10 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--steps", type=int, default=16)
-    ap.add_argument("--slots", type=int, default=1200, help="cache slots (25.2 MB each); the default holds every expert")
+    ap.add_argument("--slots", type=int, default=1200, help="cache slots (25.2 MB each, 14.2 MB int4); the default holds every expert")
     ap.add_argument("--passes", type=int, default=3, help="timed passes over the steps, after two warm ones")
+    ap.add_argument("--int4", type=int, default=0, choices=[0, 1, 2],
+                    help="the cache's int4 mode: 0 FP8 slots, 1 the reference's int4 slots, 2 int4-tiled slots")
     a = ap.parse_args()
     L = glm53h.init(0)
     NL, STEPS = a.layers, a.steps
@@ -60,11 +62,11 @@ def main():
           "store")
     check(L.g53h_store_synth_key_scales(C.byref(store)), "key scales")
     probe = glm53h.Glm53fCache()
-    check(L.g53h_cache_init_store(C.byref(probe), C.byref(store), C.byref(cf), 1 << 30, 0, 0), "cache")
+    check(L.g53h_cache_init_store(C.byref(probe), C.byref(store), C.byref(cf), 1 << 30, 0, a.int4), "cache")
     sb = probe.slot_bytes
     L.glm53f_cache_free(C.byref(probe))
     cache = glm53h.Glm53fCache()
-    check(L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), sb * a.slots, 0, 0), "cache")
+    check(L.g53h_cache_init_store(C.byref(cache), C.byref(store), C.byref(cf), sb * a.slots, 0, a.int4), "cache")
     ws = []
     for l in range(NL):
         w = glm53h.Glm53fMoeW()

@@ -168,30 +168,33 @@ void glm53f_forget_host_weights(void)
 }
 
 /* Bytes of a matrix's codes and scales: FP8 [rows][cols] codes and [ceil(rows/br)][scols]
- * scales; int4 (GLM53F_WI4) [rows][cols/2] packed levels and [rows][scols] steps. */
+ * scales; int4 (GLM53F_WI4, and GLM53F_WI4T with the levels int4-tiled) [rows][cols/2] packed
+ * levels and [rows][scols] steps. */
+static int mat_i4(const Glm53fMat *m) { return m->dt == GLM53F_WI4 || m->dt == GLM53F_WI4T; }
 static size_t mat_code_bytes(const Glm53fMat *m)
 {
-    return m->dt == GLM53F_WI4 ? (size_t)m->rows * (size_t)(m->cols / 2) : (size_t)m->rows * (size_t)m->cols;
+    return mat_i4(m) ? (size_t)m->rows * (size_t)(m->cols / 2) : (size_t)m->rows * (size_t)m->cols;
 }
 static size_t mat_scale_bytes(const Glm53fMat *m)
 {
-    const size_t srows = m->dt == GLM53F_WI4 ? (size_t)m->rows : (size_t)((m->rows + m->br - 1) / m->br);
+    const size_t srows = mat_i4(m) ? (size_t)m->rows : (size_t)((m->rows + m->br - 1) / m->br);
     return srows * (size_t)m->scols * sizeof(float);
 }
 static int mat_flags(const Glm53fMat *m)
 {
-    return m->dt == GLM53F_WF8T ? G53H_MAT_TILED : (m->dt == GLM53F_WI4 ? G53H_MAT_I4 : 0);
+    return m->dt == GLM53F_WF8T ? G53H_MAT_TILED
+           : m->dt == GLM53F_WI4 ? G53H_MAT_I4 : m->dt == GLM53F_WI4T ? (G53H_MAT_I4 | G53H_MAT_I4T) : 0;
 }
 
 static void check_f8(const Glm53fMat *m, const char *what)
 {
     if (!m->w) { fprintf(stderr, "glm53f: FATAL, multiply through an unbound matrix (%s)\n", what); abort(); }
-    if (m->dt != GLM53F_WF8 && m->dt != GLM53F_WF8T && m->dt != GLM53F_WI4) {
+    if (m->dt != GLM53F_WF8 && m->dt != GLM53F_WF8T && !mat_i4(m)) {
         fprintf(stderr, "glm53f: FATAL, %s has storage type %d; the MI355X expert path multiplies "
                         "FP8 E4M3 and int4 (GLM53F_WI4) matrices only\n", what, m->dt);
         abort();
     }
-    if (m->dt == GLM53F_WI4 && (m->cols & 1)) {
+    if (mat_i4(m) && (m->cols & 1)) {
         fprintf(stderr, "glm53f: FATAL, %s is int4 with %d columns (two levels per byte need an even count)\n",
                 what, m->cols);
         abort();
@@ -311,6 +314,11 @@ static G53Buf g_mat[3];
 static G53hMat dev_mat_staged(const Glm53fMat *m, G53Buf *b, const char *what)
 {
     check_f8(m, what);
+    if (m->dt == GLM53F_WI4T) {
+        fprintf(stderr, "glm53f: FATAL, %s is an int4-tiled cache view (GLM53F_WI4T); only glm53f_moe reads "
+                        "those\n", what);
+        abort();
+    }
     const int dev = g53h_is_device_ptr(m->w);
     if (dev && m->dt != GLM53F_WF8T) return view_mat_f8(m);
     const size_t cb = mat_code_bytes(m), sb = mat_scale_bytes(m);
@@ -357,7 +365,7 @@ void glm53f_i4_from_f8(unsigned char *q, float *steps, const Glm53fMat *src)
 {
     ensure_device();
     check_f8(src, "glm53f_i4_from_f8");
-    if (src->dt == GLM53F_WI4 || src->cols % GLM53F_I4_GROUP) {
+    if (mat_i4(src) || src->cols % GLM53F_I4_GROUP) {
         fprintf(stderr, "glm53f: FATAL, glm53f_i4_from_f8 needs an FP8 matrix with columns a multiple of %d\n",
                 GLM53F_I4_GROUP);
         abort();
@@ -736,6 +744,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
      * below on the experts the gets returned. No cache call happens while the kernel runs, so
      * no slot it reads is refilled under it. */
     const G53hExpert *stab_d = NULL, *stab_h = NULL;
+    const int kind = g53h_cache_slot_kind(src);     /* 1 octet-tiled FP8 slots, 3 int4-tiled */
     int spec = spec_enabled() && spec_worth() && dt == 1 && K <= 15 && NE <= 1024 && E == 4096 && c->moe_inter == 2048 &&
                G53_MB_OUT_OFF + 4 * G53H_NERR + ob <= G53H_MBOX_BYTES &&
                (!with_shared || shared_tileable(w)) && g53h_cache_layer_table(src, w->layer, &stab_d, &stab_h) == 0;
@@ -746,7 +755,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         memset(&SL, 0, sizeof SL);
         SL.hidden = E; SL.inter = c->moe_inter; SL.topk = K; SL.norm_topk = c->norm_topk;
         SL.routed_scale = c->routed_scale; SL.swiglu_limit = c->swiglu_limit;
-        SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = 1;
+        SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = kind == 3 ? 3 : 1;
         SL.n_experts = NE; SL.experts = stab_d;
         SL.shared = with_shared ? shared_desc(w) : NULL;
         HP(7);
@@ -796,7 +805,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     HP(2);
     /* the chosen experts' views (slot order), the shared expert after them */
     G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
-    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1, i4r = 1;
+    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1, i4r = 1, i4t = 1;
     memset(tab, 0, (size_t)(K + 1) * sizeof(G53hExpert));
     for (int j = 0; j < K; j++) {
         Glm53fExpertQ q;
@@ -816,8 +825,9 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         tab[j].down = view_mat_f8(&q.down);
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_TILED)) tiled = 0;
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4)) i4r = 0;
+        if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4T)) i4t = 0;
     }
-    if (!nh) i4r = 0;
+    if (!nh) i4r = i4t = 0;
     HP(3);
     if (spec) {                  /* every chosen expert was in the kernel's table: the output is done */
         g_spec_n[0]++;
@@ -845,6 +855,25 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         }
         if (i4r) tiled = 0;
     }
+    /* int4-tiled views: the one-launch int4 decode when the shared expert is octet-tiled (or
+     * absent); else their levels untiled for the row kernels */
+    const int one_i4t = i4t && (!with_shared || (tab[K].gate.flags & G53H_MAT_TILED));
+    if (i4t && !one_i4t) {
+        static G53Buf g_i4u[GLM53F_MAX_TOPK];
+        for (int j = 0; j < K; j++) {
+            G53hMat *ms[3] = {&tab[j].gate, &tab[j].up, &tab[j].down};
+            if (!ms[0]->w) continue;
+            size_t need = 0;
+            for (int i = 0; i < 3; i++) need += (((size_t)ms[i]->rows * (ms[i]->cols / 2)) + 255) & ~(size_t)255;
+            uint8_t *b = (uint8_t *)buf_get(&g_i4u[j], need);
+            for (int i = 0; i < 3; i++) {
+                if (g53h_tile_i4(b, ms[i]->w, ms[i]->rows, ms[i]->cols, 1)) g53_die("converting an int4 expert view");
+                ms[i]->w = b;
+                ms[i]->flags = G53H_MAT_I4;
+                b += (((size_t)ms[i]->rows * (ms[i]->cols / 2)) + 255) & ~(size_t)255;
+            }
+        }
+    }
     G53hMoeLayer L;
     memset(&L, 0, sizeof L);
     L.hidden = E; L.inter = c->moe_inter; L.topk = K; L.norm_topk = c->norm_topk;
@@ -857,7 +886,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
             L.block_c = 0;
     }
     G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
-    if (tiled) {
+    if (tiled || one_i4t) {
         /* compact table: slot j holds the j-th chosen expert (the kernel is told indices 0 .. K-1),
          * slot K the shared expert */
         int *ident = (int *)buf_get(&g_ident, GLM53F_MAX_TOPK * sizeof(int));
@@ -869,7 +898,9 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
             ident_ready = 1;
         }
         if (g53h_h2d_async(tab_d, tab, (size_t)(K + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
-        L.n_experts = K; L.experts = tab_d; L.shared = with_shared ? tab_d + K : NULL; L.tiled = 1;
+        L.n_experts = K; L.experts = tab_d; L.shared = with_shared ? tab_d + K : NULL;
+        L.tiled = one_i4t ? 3 : 1;
+        L.block_c = 128;
         if (g53h_moe_routed_given(od, xd, 1, &L, ident, w_d)) g53_die("glm53f_moe");
     } else {
         /* the table indexed by expert: the chosen entries filled, the others zero */
@@ -923,7 +954,10 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off, int tile
     uint8_t *s = dst + *off;
     *off += (sb + 255) & ~(size_t)255;
     const int is_t = m->dt == GLM53F_WF8T;
-    if (m->dt != GLM53F_WI4 && is_t != (tiled != 0)) {         /* convert on the way in */
+    if (m->dt == GLM53F_WI4T) {                                /* int4 levels back to rows */
+        uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
+        if (g53h_h2d(t, m->w, cb) || g53h_tile_i4(w, t, m->rows, m->cols, 1)) g53_die("copying a host expert to HBM");
+    } else if (m->dt != GLM53F_WI4 && is_t != (tiled != 0)) {  /* convert on the way in */
         uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
         if (g53h_h2d(t, m->w, cb) ||
             (is_t ? g53h_untile_f8(w, t, m->rows, m->cols) : g53h_tile_f8(w, t, m->rows, m->cols)))
@@ -934,7 +968,7 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off, int tile
     if (g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
     d.w = w; d.s = (const float *)s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
-    d.flags = m->dt == GLM53F_WI4 ? G53H_MAT_I4 : (tiled ? G53H_MAT_TILED : 0);
+    d.flags = mat_i4(m) ? G53H_MAT_I4 : (tiled ? G53H_MAT_TILED : 0);
     return d;
 }
 
@@ -950,10 +984,19 @@ static size_t expert_stage_bytes(const Glm53fExpertQ *q)
 
 /* An HBM view as the chunk's kernels read it: in place when its FP8 layout is the one they read
  * (tiled != 0: octet-tiled, else row-major), otherwise converted into the staging slot (ordered
- * on the stream before the kernels that read it). Int4 views are used as they are. */
+ * on the stream before the kernels that read it). Int4 views are used as they are, except
+ * int4-tiled ones, whose levels are untiled into the staging slot (the steps are read in place). */
 static G53hMat chunk_view(const Glm53fMat *m, uint8_t *dst, size_t *off, int tiled)
 {
     G53hMat d = view_mat_f8(m);
+    if (m->dt == GLM53F_WI4T) {
+        uint8_t *w = dst + *off;
+        *off += (mat_code_bytes(m) + 255) & ~(size_t)255;
+        if (g53h_tile_i4(w, (const uint8_t *)m->w, m->rows, m->cols, 1)) g53_die("converting an int4 expert view");
+        d.w = w;
+        d.flags = G53H_MAT_I4;
+        return d;
+    }
     const int is_t = m->dt == GLM53F_WF8T;
     if (m->dt == GLM53F_WI4 || is_t == (tiled != 0)) return d;
     uint8_t *w = dst + *off;
@@ -1078,7 +1121,7 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                     continue;
                 }
                 check_expert_shape(&q, c, w->layer, e);
-                const int q_i4 = q.gate.dt == GLM53F_WI4 || q.up.dt == GLM53F_WI4 || q.down.dt == GLM53F_WI4;
+                const int q_i4 = mat_i4(&q.gate) || mat_i4(&q.up) || mat_i4(&q.down);
                 if (q_i4) any_i4 = 1;
                 if (q.gate.bc != 128 || q.up.bc != 128 || q.down.bc != 128 || any_i4) block_c = 0;
                 if (want_tiled < 0)
@@ -1094,9 +1137,12 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                 const int dev = g53h_is_device_ptr(q.gate.w);
                 size_t off = 0;
                 if (dev) {
-                    const int conv = (q.gate.dt != GLM53F_WI4 && (q.gate.dt == GLM53F_WF8T) != tl) ||
-                                     (q.up.dt != GLM53F_WI4 && (q.up.dt == GLM53F_WF8T) != tl) ||
-                                     (q.down.dt != GLM53F_WI4 && (q.down.dt == GLM53F_WF8T) != tl);
+                    /* FP8 views in the other layout, and int4-tiled views (their levels are
+                     * untiled), are converted into the staging slot */
+                    const int conv = (!mat_i4(&q.gate) && (q.gate.dt == GLM53F_WF8T) != tl) ||
+                                     (!mat_i4(&q.up) && (q.up.dt == GLM53F_WF8T) != tl) ||
+                                     (!mat_i4(&q.down) && (q.down.dt == GLM53F_WF8T) != tl) ||
+                                     q.gate.dt == GLM53F_WI4T || q.up.dt == GLM53F_WI4T || q.down.dt == GLM53F_WI4T;
                     uint8_t *dst = conv ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
                     held[nh++] = e;                      /* released once its kernels are queued */
                     table[e].gate = chunk_view(&q.gate, dst, &off, tl);

@@ -96,8 +96,9 @@ typedef struct {
  * library; the router is fp32 (GLM53F_WF32) or bf16 (GLM53F_WBF16) bit patterns. GLM53F_WF8T is this
  * library's own: the expert views of its HBM cache (glm53f_cache.h) hold the same E4M3 codes in
  * the octet-tiled layout of g53h.h (G53H_MAT_TILED), for its kernels; the reference never makes
- * one. */
-enum { GLM53F_WF32 = 0, GLM53F_WBF16 = 1, GLM53F_WF8 = 2, GLM53F_WI4 = 3, GLM53F_WF8T = 0x102 };
+ * one. GLM53F_WI4T, also this library's own: the int4 views of its cache in int4 mode 2 (the
+ * levels int4-tiled, G53H_MAT_I4T of g53h.h; the steps as GLM53F_WI4's). */
+enum { GLM53F_WF32 = 0, GLM53F_WBF16 = 1, GLM53F_WF8 = 2, GLM53F_WI4 = 3, GLM53F_WF8T = 0x102, GLM53F_WI4T = 0x103 };
 
 /* Group size of the GLM53F_WI4 matrices the reference's engine produces
  * (include/glm53f/glm53f.h:124-125). */

@@ -117,7 +117,12 @@ typedef struct {
  * down}_proj.{weight,weight_scale_inv}", FP8 E4M3 codes with F32 scale grids); the slot geometry
  * comes from expert 0 of the first MoE layer (cfg->is_dense), as the reference probes it.
  * Fails (-1) if fewer than topk+1 slots fit, if HBM cannot hold the arena, if the probe expert
- * is missing or not FP8, or (i4 != 0) if a matrix's columns are not a multiple of 64. */
+ * is missing or not FP8, or (i4 != 0) if a matrix's columns are not a multiple of 64.
+ * i4 = 1 is the reference's int4 mode (its slot layout, GLM53F_WI4 views). i4 = 2, this
+ * library's own, holds the same slot size with the levels int4-tiled (GLM53F_WI4T views) at the
+ * shapes the one-launch decode reads (hidden 4096, inter 2048, 128 x 128 FP8 blocks), so that
+ * the drop-in decodes a token in one launch; its chunked paths untile the views they read. At
+ * other shapes i4 = 2 is i4 = 1. */
 int  glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
                        int n_io, int i4);
 void glm53f_cache_free(Glm53fCache *c);
@@ -146,13 +151,16 @@ int  glm53f_cache_sync(Glm53fCache *c);
  * its release is ordered on the device), else 0. */
 int  g53h_cache_is(const Glm53fExpertSrc *src);
 /* The device table of layer's experts whose reads have landed (no counterpart in the
- * reference): table_d [n_experts] of octet-tiled descriptors (gate.w NULL where the expert holds
- * no landed slot) on the compute stream's timeline, and table_h its host copy. It is current as
+ * reference): table_d [n_experts] of the slots' descriptors (octet-tiled FP8 or int4-tiled;
+ * gate.w NULL where the expert holds no landed slot) on the compute stream's timeline, and table_h its host copy. It is current as
  * of this call; any later cache call may evict or fill slots, so a kernel that reads it must
  * complete before the next cache call. Returns 0, a positive count of this layer's reads still
- * in flight (no table then), or -1 when src is not a cache with octet-tiled slots. */
+ * in flight (no table then), or -1 when src is not a cache with tiled slots (kind 1 or 3). */
 int  g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **table_d,
                             const G53hExpert **table_h);
+/* The kind of slots a cache holds (no counterpart in the reference): 1 octet-tiled FP8, 3
+ * int4-tiled (int4 mode 2), 0 otherwise (row-major FP8 or int4, or src not a cache). */
+int  g53h_cache_slot_kind(const Glm53fExpertSrc *src);
 /* The drop-in's speculative cached decode (no counterpart in the reference): with a cache of
  * octet-tiled slots, glm53f_moe at T = 1 runs the one-launch decode over the layer's table
  * before the reference's hint/get/release calls, which it then makes in the reference's order,

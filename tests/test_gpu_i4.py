@@ -257,15 +257,15 @@ def ref_i4_slot_bytes(sp):
     return (off + 4095) // 4096 * 4096
 
 
-def new_cache_i4(cf, st, slots, n_io):
+def new_cache_i4(cf, st, slots, n_io, mode=1):
     L = glm53h.lib()
     probe = glm53h.Glm53fCache()
-    assert L.g53h_cache_init_store(C.byref(probe), C.byref(st), C.byref(cf), 1 << 30, 0, 1) == 0
+    assert L.g53h_cache_init_store(C.byref(probe), C.byref(st), C.byref(cf), 1 << 30, 0, mode) == 0
     sb = probe.slot_bytes
     L.glm53f_cache_free(C.byref(probe))
     c = glm53h.Glm53fCache()
-    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), sb * slots, n_io, 1) == 0
-    assert c.nslot == slots and c.i4 == 1
+    assert L.g53h_cache_init_store(C.byref(c), C.byref(st), C.byref(cf), sb * slots, n_io, mode) == 0
+    assert c.nslot == slots and c.i4 == mode
     return c, sb
 
 
@@ -299,7 +299,9 @@ def test_cache_int4_mode_config1(L):
 
 def test_cache_int4_mode_config2(L):
     """Released shapes (14,155,776-byte int4 slots): two layers, three tokens, through the int4
-    cache, equal to host int4 views of the same experts quantised by the oracle."""
+    cache, equal to host int4 views of the same experts quantised by the oracle; the same in int4
+    mode 2 (the levels int4-tiled, the one-launch decode, speculative once every expert has
+    landed) and for a five-token chunk through the tiled slots."""
     sp = S.spec(2)
     NP = 12
     cf = make_cfg(sp)
@@ -316,7 +318,7 @@ def test_cache_int4_mode_config2(L):
             q[0].gate, q[0].up, q[0].down = imat(gq, gs, sp.I, sp.E), imat(uq, us, sp.I, sp.E), imat(dq, ds, sp.E, sp.I)
             return 0
 
-    def run(src, pf):
+    def run(src, pf, T=1):
         outs = []
         for t in range(3):
             for l in range(2):
@@ -329,11 +331,13 @@ def test_cache_int4_mode_config2(L):
                 w.layer, w.prefetch_n = l, pf
                 if pf and l == 0:
                     w.next_gate, w.next_bias = W[1].ctypes.data, B[1].ctypes.data
-                out = np.zeros((1, sp.E), np.float32)
-                xt = np.ascontiguousarray(x[t:t + 1])
-                L.glm53f_moe(out.ctypes.data, xt.ctypes.data, C.byref(w), C.byref(cf), 1, None)
-                outs.append(out[0])
+                out = np.zeros((T, sp.E), np.float32)
+                xt = np.ascontiguousarray(x[t:t + 1] if T == 1 else xT)
+                L.glm53f_moe(out.ctypes.data, xt.ctypes.data, C.byref(w), C.byref(cf), T, None)
+                outs.append(out[0] if T == 1 else out)
         return np.asarray(outs)
+
+    xT = np.ascontiguousarray(S.x_host(sp, 5, batch=8))
 
     say("config 2 int4 through host views")
     want = run(PoolI4(cf, {}).src, 0)
@@ -344,9 +348,33 @@ def test_cache_int4_mode_config2(L):
         c, sb = new_cache_i4(cf, st, 12, 2)
         try:
             assert sb == ref_i4_slot_bytes(sp) == 14155776
+            assert L.g53h_cache_slot_kind(C.byref(c.src)) == 0
             got = run(c.src, 6)
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         finally:
             L.glm53f_cache_free(C.byref(c))
+        # int4 mode 2: the same slot size with the levels int4-tiled; single-token layers in one
+        # launch (speculative once every expert has landed), chunks through untiled levels
+        wantT = run(PoolI4(cf, {}).src, 0, T=5)
+        for slots, n_io in [(12, 2), (600, 0)]:
+            say("config 2 int4-tiled cache, slots", slots)
+            c, sb = new_cache_i4(cf, st, slots, n_io, mode=2)
+            try:
+                assert sb == ref_i4_slot_bytes(sp) and L.g53h_cache_slot_kind(C.byref(c.src)) == 3
+                n = (C.c_int64 * 3)()
+                L.g53h_speculate_counts(n)
+                got = run(c.src, 6 if n_io else 0)
+                check(L.glm53f_cache_sync(C.byref(c)), "sync")
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+                if slots > 300:                      # every expert resident: the second pass speculates
+                    L.g53h_set_speculate(1)
+                    again = run(c.src, 0)
+                    L.g53h_speculate_counts(n)
+                    assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+                    assert n[0] >= 6, list(n)
+                gotT = run(c.src, 0, T=5)
+                assert np.array_equal(gotT.view(np.uint32), wantT.view(np.uint32))
+            finally:
+                L.glm53f_cache_free(C.byref(c))
     finally:
         L.g53h_store_synth_free(C.byref(st))
