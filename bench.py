@@ -471,7 +471,10 @@ def bench_stack(a):
     check(L.g53h_store_synth_init(C.byref(st), E, I, NL + 1, NE, NE, base.seed, C.c_float(base.expert_sigma)), "store")
     cache = glm53h.Glm53fCache()
     budget = 200 * 10 ** 9
-    if L.g53h_cache_init_store(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io, 0) != 0:
+    # --experts int4: the reference's int4 mode, in the cache's int4-tiled slots (mode 2): the
+    # experts are re-quantised as they are read, and a decode layer is one launch
+    i4mode = 2 if a.experts == "int4" else 0
+    if L.g53h_cache_init_store(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io, i4mode) != 0:
         sys.exit("glm53f_cache_init failed")
     specs = [S.spec(3, layer=l) for l in range(NL)]
     W = [S.router_host(s_) for s_ in specs]
@@ -595,6 +598,8 @@ def bench_stack(a):
                                f", {steps} steps, HBM expert cache of 200 GB, the rest in pinned host memory, "
                                "next-layer prefetch",
                    "layers": NL, "slots": nslot,
+                   "routed_experts": ("int4 (the reference's int4 mode, re-quantised as read; int4-tiled slots)"
+                                      if i4mode else "fp8"),
                    "prefetch_n": pf, "prefetch_reads_in_flight": n_io, "input_correlation": rho,
                    "parallelism": "single GPU"},
         "routing": routing,
@@ -607,8 +612,11 @@ def bench_stack(a):
         "speculative_layers": {"done": int(spec[0]), "run_again": int(spec[1]), "not_speculative": int(spec[2])},
         "prefetch_reads": int(bg_reads), "prefetch_used": int(bg_used),
         "h2d_GB": round(h2d / 1e9, 3), "h2d_GBps_avg": round(h2d / dt / 1e9, 2), "h2d_link_GBps": round(link, 2),
-        "hbm_GBps_experts": round((K + 1) * eb / (us_layer * 1e-6) / 1e9, 1),
-        "cpu_baseline": None if a.no_cpu else cpu_stack_layer(base, W[0], B[0], X[0, 0], sh, a.cpu_seconds),
+        "hbm_GBps_experts": round(((K * base.expert_i4_bytes() + eb) if i4mode else (K + 1) * eb) /
+                                  (us_layer * 1e-6) / 1e9, 1),
+        # (the reference's FP8 layer on the CPU; not measured for the int4 run)
+        "cpu_baseline": None if (a.no_cpu or i4mode) else cpu_stack_layer(base, W[0], B[0], X[0, 0], sh,
+                                                                          a.cpu_seconds),
     }
     print(json.dumps(line), flush=True)
 
@@ -643,7 +651,8 @@ def main():
     ap.add_argument("--experts", default="fp8", choices=["fp8", "int4"],
                     help="config 2: routed experts as the checkpoint's FP8 (the metric) or re-quantised to the "
                          "reference's int4 format (its --experts int4 mode): one launch over int4-tiled slots, or "
-                         "with --layout rowmajor the five-launch row-wave kernels")
+                         "with --layout rowmajor the five-launch row-wave kernels; config 5: the cache's int4 "
+                         "mode with int4-tiled slots (200 GB then holds every expert of 42 layers)")
     a = ap.parse_args()
     if a.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (expert-parallel "
