@@ -650,8 +650,10 @@ def main():
                          "row-major (k_dec_layer, bit-exact); configs 3-4: tiled or rowmajor")
     ap.add_argument("--experts", default="fp8", choices=["fp8", "int4"],
                     help="config 2: routed experts as the checkpoint's FP8 (the metric) or re-quantised to the "
-                         "reference's int4 format (its --experts int4 mode): one launch over int4-tiled slots, or "
-                         "with --layout rowmajor the five-launch row-wave kernels; config 5: the cache's int4 "
+                         "reference's int4 format (its --experts int4 mode): one launch on the FP4 matrix cores over "
+                         "int4 MFMA-tiled experts (--layout mfma, within the tolerance), one launch over int4-tiled "
+                         "slots (--layout tiled, bit-exact), or with --layout rowmajor the five-launch row-wave "
+                         "kernels; config 5: the cache's int4 "
                          "mode with int4-tiled slots (200 GB then holds every expert of 42 layers)")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -666,12 +668,14 @@ def main():
     L = glm53h.init(0)
     sp = S.spec(2)
     i4 = a.experts == "int4"
-    i4t = i4 and a.layout != "rowmajor"                 # int4: one launch over int4-tiled slots
-    i4 = i4 and not i4t                                  # (rowmajor: the five-launch row kernels)
-    mfma = a.layout == "mfma" and not (i4 or i4t)
+    i4m = i4 and a.layout == "mfma"                     # int4: one launch on the FP4 matrix cores
+    i4t = i4 and a.layout == "tiled"                    # int4: one launch over int4-tiled slots
+    i4 = i4 and a.layout == "rowmajor"                  # (rowmajor: the five-launch row kernels)
+    mfma = a.layout == "mfma"
     tiled = (a.layout == "tiled" and not i4) or i4t
-    kname = "k_rows" if i4 else ("k_dec_tiled_i4" if i4t else ("k_dec_mfma" if mfma else ("k_dec_tiled" if tiled else "k_dec_layer")))
-    layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4 or i4t, mfma=mfma)
+    kname = ("k_rows" if i4 else "k_dec_tiled_i4" if i4t else "k_dec_mfma_i4" if i4m else "k_dec_mfma" if mfma
+             else "k_dec_tiled" if tiled else "k_dec_layer")
+    layer = S.DeviceLayer.build(sp, tiled=tiled, i4=i4 or i4t or i4m, mfma=mfma)
     cp = Copies(layer)
     x = S.x_host(sp, NTOK, batch=0)
     xs = DevBuf.from_array(x)
@@ -727,7 +731,7 @@ def main():
         # expert) with the SwiGLU between them, timed together by the profiled run's events
         dom_bytes = sp.K * sp.expert_i4_bytes() + eb
         dom_us = per["row_kernels_us"]
-    elif i4t:
+    elif i4t or i4m:
         # int4 in one launch: the router, 8 int4 experts and the FP8 shared expert
         dom_bytes = sp.K * sp.expert_i4_bytes() + eb + router_bytes
     dom_gbps = dom_bytes / (dom_us * 1e-6) / 1e9
@@ -737,7 +741,7 @@ def main():
     # kernels' configs 3 and 4 (they read octet-tiled or row-major experts)
     exact, olayer = None, layer
     if mfma:
-        olayer = S.DeviceLayer.build(sp, tiled=True)
+        olayer = S.DeviceLayer.build(sp, tiled=True, i4=i4m)
         ocp = Copies(olayer)
         run_steps(L, ocp, xs, outs, sp.E, a.warmup)
         glm53h.sync()
@@ -747,13 +751,15 @@ def main():
         ex_us = L.g53h_elapsed_ms() * 1e3 / a.steps
         if L.g53h_decode_errors():
             sys.exit("the bit-exact decode kernel reported error flags")
-        ex_gbps = ((sp.K + 1) * sp.expert_bytes() + sp.NE * sp.E * 2 + sp.NE * 4) / (ex_us * 1e-6) / 1e9
-        exact = {"kernel": "k_dec_tiled", "parity": "bit-exact with the reference", "steps": a.steps,
+        ex_bytes = ((sp.K * sp.expert_i4_bytes() + sp.expert_bytes()) if i4m else (sp.K + 1) * sp.expert_bytes())
+        ex_gbps = (ex_bytes + sp.NE * sp.E * 2 + sp.NE * 4) / (ex_us * 1e-6) / 1e9
+        exact = {"kernel": "k_dec_tiled_i4" if i4m else "k_dec_tiled", "parity": "bit-exact with the reference",
+                 "steps": a.steps,
                  "us_per_layer": round(ex_us, 2), "achieved_GBps": round(ex_gbps, 1),
                  "hbm_peak_frac": round(ex_gbps / HBM_PEAK_GBPS, 4)}
         del ocp
-    prefill = None if (i4 or i4t or a.no_prefill) else prefill_beside(L, olayer, sp)
-    batched = None if (i4 or i4t or a.no_prefill) else batched_beside(L, olayer)
+    prefill = None if (i4 or i4t or i4m or a.no_prefill) else prefill_beside(L, olayer, sp)
+    batched = None if (i4 or i4t or i4m or a.no_prefill) else batched_beside(L, olayer)
     traffic = None                      # HBM bytes per launch from the committed counter summary
     tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 or i4t else ''}_traffic.json")
     if os.path.exists(tp):
@@ -775,9 +781,12 @@ def main():
         "config": {"workload": "BASELINE config 2: single-token decode of one MoE layer, hidden 4096, "
                                "moe_inter 2048, 288 experts resident in HBM, top-8 + 1 shared",
                    "tokens_cycled": NTOK, "router_shared_copies": NCOPY,
-                   "expert_layout": "int4 row-major" if i4 else ("int4-tiled" if i4t else a.layout),
+                   "expert_layout": ("int4 row-major" if i4 else "int4-tiled" if i4t else
+                                     "int4 MFMA-tiled" if i4m else a.layout),
                    "routed_experts": a.experts,
-                   "parity": ("routing bit-exact, outputs within 1e-2 abs + 2e-3 rel (FP8 matrix cores)" if mfma
+                   "parity": ("routing bit-exact, outputs within 1e-2 abs + 2e-3 rel (FP4 matrix cores, int4 "
+                              "levels exact)" if i4m else
+                              "routing bit-exact, outputs within 1e-2 abs + 2e-3 rel (FP8 matrix cores)" if mfma
                               else "bit-exact with the reference"),
                    "parallelism": "single GPU"},
         "hbm_GBps": round(gbps, 1),

@@ -78,6 +78,11 @@ typedef __attribute__((address_space(1))) const g53_u4 g53_mgv4;
 #else
 typedef const g53_u4 g53_mgv4;
 #endif
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __attribute__((address_space(1))) const float4 g53_mgf4;
+#else
+typedef const float4 g53_mgf4;
+#endif
 
 struct G53MfmaArgs {
     float *out;
@@ -206,6 +211,68 @@ __device__ __forceinline__ g53_m4f g53_dm_planesum(const g53_m4f &acc)
     return r;
 }
 
+/* ------------------------------------------------ int4 experts (FP4 matrix cores) ---- */
+/* A routed expert in the int4 MFMA-tiled layout (include/g53h.h, G53H_MAT_I4 | G53H_MAT_MTILED)
+ * with the released shapes and one step per row and 64 columns. */
+__device__ __forceinline__ bool g53_desc_i4m(const G53hExpert &e)
+{
+    const G53hMat *mm[3] = {&e.gate, &e.up, &e.down};
+    const int rows[3] = {G53_DEC_I, G53_DEC_I, G53_DEC_E}, cols[3] = {G53_DEC_E, G53_DEC_E, G53_DEC_I};
+    bool ok = true;
+    for (int i = 0; i < 3; i++)
+        ok = ok && mm[i]->w && mm[i]->s && (mm[i]->flags & G53H_MAT_I4) && (mm[i]->flags & G53H_MAT_MTILED) &&
+             mm[i]->rows == rows[i] && mm[i]->cols == cols[i] && mm[i]->bc == 64 && mm[i]->scols == cols[i] / 64;
+    return ok;
+}
+
+/* The int4 products of one block. Level l = 4 h + b (h, b < 4) minus 8: the A operand is FP4
+ * (E2M1), whose codes 0-3 are the values 0, 0.5, 1, 1.5, so the two-bit fields h and b of the
+ * lane's 32 levels are two FP4 planes as they lie ((r >> 2) & 0x3.., r & 0x3..), taken at A
+ * scales 2^3 (4 h) and 2^1 (b); a third product with every code -4 (0xE) at scale 2^1 adds
+ * -8 times the block's inputs. The matrix core reads lane l's 32 FP4 values as row l % 16 and
+ * columns (of B's order) 64 (g & 1) + 16 (g >> 1) + 0..15 and + 32 .. + 47 (g = l / 16), which
+ * is where the MFMA-tiled layout puts them. B: column m < 6 of K-group g carries plane m - 3 (g
+ * >> 1) of x over the block's 64-column half g >> 1 (zeros elsewhere), so that result column m
+ * is one plane of one half; each lane scales its four rows by their half's steps (st). */
+__device__ __forceinline__ void g53_dm_i4_mma(g53_m4f &acc, const g53_u4 &r, const g53_m8i &b, int bscale,
+                                              const float4 &st)
+{
+    const g53_m8i ah = {(int)((r.x >> 2) & 0x33333333u), (int)((r.y >> 2) & 0x33333333u),
+                        (int)((r.z >> 2) & 0x33333333u), (int)((r.w >> 2) & 0x33333333u), 0, 0, 0, 0};
+    const g53_m8i ab = {(int)(r.x & 0x33333333u), (int)(r.y & 0x33333333u), (int)(r.z & 0x33333333u),
+                        (int)(r.w & 0x33333333u), 0, 0, 0, 0};
+    const g53_m8i ac = {(int)0xEEEEEEEEu, (int)0xEEEEEEEEu, (int)0xEEEEEEEEu, (int)0xEEEEEEEEu, 0, 0, 0, 0};
+    g53_m4f c = {0.0f, 0.0f, 0.0f, 0.0f};
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah, b, c, 4, 0, 0, 130, 0, bscale);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ab, b, c, 4, 0, 0, 128, 0, bscale);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ac, b, c, 4, 0, 0, 128, 0, bscale);
+    acc[0] = __builtin_fmaf(c[0], st.x, acc[0]);
+    acc[1] = __builtin_fmaf(c[1], st.y, acc[1]);
+    acc[2] = __builtin_fmaf(c[2], st.z, acc[2]);
+    acc[3] = __builtin_fmaf(c[3], st.w, acc[3]);
+}
+
+/* This lane's B slot in a K-group's 128 LDS bytes (plane 0-2, or 3: the zeros) and its scale
+ * byte (the plane's, the same in all four K-groups of the column; 3: the unit scale). */
+__device__ __forceinline__ int g53_dm_i4_slot(int m, int grp)
+{
+    const int p = m - 3 * (grp >> 1);
+    return (unsigned)p < 3u ? p : 3;
+}
+__device__ __forceinline__ int g53_dm_i4_sc(int m) { return m < 6 ? m % 3 : 3; }
+
+/* The sums of the six columns into the lanes of column 0 (lanes 16 g): rows 4 g .. 4 g + 3. */
+__device__ __forceinline__ g53_m4f g53_dm_i4_colsum(const g53_m4f &acc)
+{
+    g53_m4f r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float t = (acc[i] + __shfl_down(acc[i], 1)) + __shfl_down(acc[i], 2);
+        r[i] = t + __shfl_down(t, 3);
+    }
+    return r;
+}
+
 __device__ __forceinline__ const uint8_t *g53_dm_uptr(const uint8_t *p)
 {
     const g53_u64 v = (g53_u64)(uintptr_t)p;
@@ -216,6 +283,10 @@ __device__ __forceinline__ const uint8_t *g53_dm_uptr(const uint8_t *p)
 #define G53_MTRACE(k) do { if (a.trace && lane == 0) \
     a.trace[(size_t)blockIdx.x * 192 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 
+/* I4: the routed experts are int4, int4 MFMA-tiled (G53H_MAT_I4 | G53H_MAT_MTILED; the reference's
+ * --experts int4), multiplied on the FP4 matrix cores (g53_dm_i4_mma); the shared expert stays
+ * FP8 MFMA-tiled. */
+template <bool I4>
 __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
 {
     __shared__ __attribute__((aligned(16))) uint8_t xq[G53_DEC_NBE * G53_DM_BB];      /* x, B operand    */
@@ -417,13 +488,53 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
             const int e = sidx[s];
             if (e >= 0 && e < a.NE) ex = dstage ? ((const G53hExpert *)dtab)[e] : a.experts[e];
             else ex.gate.w = nullptr;
-            usable = ex.gate.w != nullptr && g53_desc_mtiled(ex);
+            usable = ex.gate.w != nullptr && (I4 ? g53_desc_i4m(ex) : g53_desc_mtiled(ex));
             if (ex.gate.w && !usable && lane == 0) g53_flag_err(a.err, 8);
         }
         const bool present = __builtin_amdgcn_readfirstlane((int)usable) != 0;
         if (is_g) {
             if (!present) continue;                   /* its activations are never read */
             const int ogl = idx >> 1, og = go_lo + ogl, h = idx & 1;
+            g53_m4f vg;
+            if (I4 && s < K) {
+                /* int4: lane's row as for FP8; its 16 bytes of block kb at + kb * 512, its four
+                 * rows' steps of the half of its column (float4 at + kb * 16) */
+                const uint8_t *gw = g53_dm_uptr(ex.gate.w), *uw = g53_dm_uptr(ex.up.w);
+                const uint8_t *wb = m < 8 ? gw : uw;
+                const size_t u0 = (size_t)og * G53_DEC_NBE + 16 * h;
+                const uint8_t *pl = wb + u0 * 512 + (grp * 8 + (m & 7)) * 16;
+                const float *sb = (grp < 2 ? ex.gate.s : ex.up.s) + u0 * 16 + (m < 6 ? m / 3 : 0) * 8 + 4 * (grp & 1);
+                __builtin_amdgcn_sched_barrier(0);
+                constexpr int NB = G53_DEC_NBE / 2;
+                g53_u4 r[NB];
+                float4 stp[NB];
+#pragma unroll
+                for (int j = 0; j < NB; j++) {
+                    r[j] = G53_DM_LD((g53_mgv4 *)(pl + 512 * j));
+                    stp[j] = *(g53_mgf4 *)(sb + 16 * j);
+                }
+                if (!xr) {
+                    if (!g53_wait_lds(&xready, n_setup) && lane == 0) g53_flag_err(a.err, 1);
+                    xr = true;
+                }
+                g53_m4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+                const uint8_t *bq0 = xq + 16 * h * G53_DM_BB + grp * 128 + g53_dm_i4_slot(m, grp) * 32;
+                const uint8_t *bs0 = xsc + 16 * h * 64 + grp * 16 + g53_dm_i4_sc(m);
+                g53_m8i bn = *(const g53_m8i *)bq0;
+                int sn = bs0[0];
+#pragma unroll
+                for (int kb = 0; kb < NB; kb++) {
+                    const g53_m8i bc = bn;
+                    const int sc = sn;
+                    if (kb + 1 < NB) {
+                        bn = *(const g53_m8i *)(bq0 + (kb + 1) * G53_DM_BB);
+                        sn = bs0[(kb + 1) * 64];
+                    }
+                    g53_dm_i4_mma(acc, r[kb], bc, sc, stp[kb]);
+                    if ((kb % G53_DM_PIN) == G53_DM_PIN - 1) asm volatile("" : "+v"(acc));
+                }
+                vg = g53_dm_i4_colsum(acc);
+            } else {
             /* lane's row: gate rows for A rows 0-7, up rows for 8-15; its 16 bytes of half-tile i
              * of block kb at + kb KB + 512 i */
             const uint8_t *gw = g53_dm_uptr(ex.gate.w), *uw = g53_dm_uptr(ex.up.w);
@@ -494,10 +605,11 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
                 }
             }
 #endif
-            const g53_m4f v = g53_dm_planesum(acc);
+            vg = g53_dm_planesum(acc);
+            }
             if (m == 0)
 #pragma unroll
-                for (int i = 0; i < 4; i++) gup[s][ogl][h][4 * grp + i] = v[i];
+                for (int i = 0; i < 4; i++) gup[s][ogl][h][4 * grp + i] = vg[i];
             __builtin_amdgcn_s_waitcnt(0xc07f);
             __builtin_amdgcn_wave_barrier();
             G53_CBAR();
@@ -518,8 +630,92 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
         /* D half-task: down rows of octets oa, ob over column blocks 8 hd .. 8 hd + 7 */
         const int dp = idx >> 1, hd = idx & 1;
         const int oa = do_lo + 2 * dp, ob = oa + 1 < do_lo + n_do ? oa + 1 : oa;
+        /* the half's 1024 activations: lane l takes values 16 l .. 16 l + 15 of it (block
+         * l / 8, group l / 2 % 4), re-read coherently until every tag is this launch's, then
+         * writes them as B-operand planes into this wave's LDS */
+        auto stage_act = [&]() {
+            const __amdgpu_buffer_rsrc_t rsl = g53_rsrc(a.act + (size_t)s * G53_DEC_I + 1024 * hd);
+            int spins = 0, nap = 1;
+            for (;;) {
+                g53_u64 tv[2];
+#pragma unroll
+                for (int k = 0; k < 2; k++) tv[k] = g53_ld_coh64(rsl, 8 * ((lane + 64 * k) * 8 + 7));
+                const int stale = ((unsigned)(tv[0] >> 32) != a.epoch) | ((unsigned)(tv[1] >> 32) != a.epoch);
+                if (!__ballot(stale)) break;
+                if (++spins > a.spin / 16 + 1) { if (lane == 0) g53_flag_err(a.err, 1); break; }
+                for (int qq = 0; qq < nap; qq++) __builtin_amdgcn_s_sleep(8);
+                if (nap < 8) nap *= 2;
+            }
+            g53_u64 *act_s = a.act + (size_t)s * G53_DEC_I + 1024 * hd;
+            const __amdgpu_buffer_rsrc_t rs = g53_rsrc(act_s);
+            const int v0 = 16 * lane;
+            g53_mgv4 *src = (g53_mgv4 *)(act_s + v0);
+            float av[16];
+            uint32_t pend = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const g53_u4 qv = src[k];
+                av[2 * k] = __uint_as_float(qv.x);
+                av[2 * k + 1] = __uint_as_float(qv.z);
+                if (qv.y != a.epoch) pend |= 1u << (2 * k);
+                if (qv.w != a.epoch) pend |= 1u << (2 * k + 1);
+            }
+            spins = 0;
+            while (__ballot(pend != 0)) {
+                if (++spins > a.spin) { if (lane == 0) g53_flag_err(a.err, 1); break; }
+                g53_backoff();
+#pragma unroll
+                for (int mm = 0; mm < 16; mm++) {
+                    if (!(pend & (1u << mm))) continue;
+                    const g53_u64 tv = g53_ld_coh64(rs, 8 * (v0 + mm));
+                    if ((unsigned)(tv >> 32) == a.epoch) {
+                        av[mm] = __uint_as_float((uint32_t)tv);
+                        act_s[v0 + mm] = tv;
+                        pend &= ~(1u << mm);
+                    }
+                }
+            }
+            const int kb = lane >> 3, g = (lane >> 1) & 3, hf = lane & 1;
+            g53_dm_planes<16, G53_DM_NPA>(av, myaq + kb * G53_DM_BB + g * 128 + 16 * hf, myasc + kb * 64 + g * 16,
+                                          hf == 0);
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+        };
         g53_m4f v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (present) {
+        if (I4 && present && s < K) {
+            /* int4: rows of octet oa (A rows 0-7) and ob (8-15), blocks 8 hd .. 8 hd + 7 */
+            const uint8_t *dw = g53_dm_uptr(ex.down.w);
+            const uint8_t *pl = dw + ((size_t)(m < 8 ? oa : ob) * G53_DEC_NBI + 8 * hd) * 512 + (grp * 8 + (m & 7)) * 16;
+            const float *sb = ex.down.s + ((size_t)(grp < 2 ? oa : ob) * G53_DEC_NBI + 8 * hd) * 16 +
+                              (m < 6 ? m / 3 : 0) * 8 + 4 * (grp & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            constexpr int NB = G53_DEC_NBI / 2;
+            g53_u4 r[NB];
+            float4 stp[NB];
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                r[j] = G53_DM_LD((g53_mgv4 *)(pl + 512 * j));
+                stp[j] = *(g53_mgf4 *)(sb + 16 * j);
+            }
+            stage_act();
+            g53_m4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            const uint8_t *bq0 = myaq + grp * 128 + g53_dm_i4_slot(m, grp) * 32;
+            const uint8_t *bs0 = myasc + grp * 16 + g53_dm_i4_sc(m);
+            g53_m8i bn = *(const g53_m8i *)bq0;
+            int sn = bs0[0];
+#pragma unroll
+            for (int kb = 0; kb < NB; kb++) {
+                const g53_m8i bc = bn;
+                const int sc = sn;
+                if (kb + 1 < NB) {
+                    bn = *(const g53_m8i *)(bq0 + (kb + 1) * G53_DM_BB);
+                    sn = bs0[(kb + 1) * 64];
+                }
+                g53_dm_i4_mma(acc, r[kb], bc, sc, stp[kb]);
+                if ((kb % G53_DM_PIN) == G53_DM_PIN - 1) asm volatile("" : "+v"(acc));
+            }
+            v = g53_dm_i4_colsum(acc);
+        } else if (present) {
             const uint8_t *dw = g53_dm_uptr(ex.down.w);
             const uint8_t *pl = dw + (size_t)(m < 8 ? oa : ob) * (G53_DEC_NBI * 1024) + (8 * hd) * 1024 +
                                 (grp * 8 + (m & 7)) * 16;
@@ -531,57 +727,7 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
             g53_m8i r[NB];
 #pragma unroll
             for (int j = 0; j < NB; j++) r[j] = g53_dm_ld(q + 64 * j);
-            /* the half's 1024 activations: lane l takes values 16 l .. 16 l + 15 of it (block
-             * l / 8, group l / 2 % 4), re-read coherently until every tag is this launch's, then
-             * writes them as B-operand planes into this wave's LDS */
-            {
-                const __amdgpu_buffer_rsrc_t rsl = g53_rsrc(a.act + (size_t)s * G53_DEC_I + 1024 * hd);
-                int spins = 0, nap = 1;
-                for (;;) {
-                    g53_u64 tv[2];
-#pragma unroll
-                    for (int k = 0; k < 2; k++) tv[k] = g53_ld_coh64(rsl, 8 * ((lane + 64 * k) * 8 + 7));
-                    const int stale = ((unsigned)(tv[0] >> 32) != a.epoch) | ((unsigned)(tv[1] >> 32) != a.epoch);
-                    if (!__ballot(stale)) break;
-                    if (++spins > a.spin / 16 + 1) { if (lane == 0) g53_flag_err(a.err, 1); break; }
-                    for (int qq = 0; qq < nap; qq++) __builtin_amdgcn_s_sleep(8);
-                    if (nap < 8) nap *= 2;
-                }
-                g53_u64 *act_s = a.act + (size_t)s * G53_DEC_I + 1024 * hd;
-                const __amdgpu_buffer_rsrc_t rs = g53_rsrc(act_s);
-                const int v0 = 16 * lane;
-                g53_mgv4 *src = (g53_mgv4 *)(act_s + v0);
-                float av[16];
-                uint32_t pend = 0;
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const g53_u4 qv = src[k];
-                    av[2 * k] = __uint_as_float(qv.x);
-                    av[2 * k + 1] = __uint_as_float(qv.z);
-                    if (qv.y != a.epoch) pend |= 1u << (2 * k);
-                    if (qv.w != a.epoch) pend |= 1u << (2 * k + 1);
-                }
-                spins = 0;
-                while (__ballot(pend != 0)) {
-                    if (++spins > a.spin) { if (lane == 0) g53_flag_err(a.err, 1); break; }
-                    g53_backoff();
-#pragma unroll
-                    for (int mm = 0; mm < 16; mm++) {
-                        if (!(pend & (1u << mm))) continue;
-                        const g53_u64 tv = g53_ld_coh64(rs, 8 * (v0 + mm));
-                        if ((unsigned)(tv >> 32) == a.epoch) {
-                            av[mm] = __uint_as_float((uint32_t)tv);
-                            act_s[v0 + mm] = tv;
-                            pend &= ~(1u << mm);
-                        }
-                    }
-                }
-                const int kb = lane >> 3, g = (lane >> 1) & 3, hf = lane & 1;
-                g53_dm_planes<16, G53_DM_NPA>(av, myaq + kb * G53_DM_BB + g * 128 + 16 * hf, myasc + kb * 64 + g * 16,
-                                              hf == 0);
-                __builtin_amdgcn_s_waitcnt(0xc07f);
-                __builtin_amdgcn_wave_barrier();
-            }
+            stage_act();
             g53_m4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
             const int sbits = __float_as_int(scv);
             const uint8_t *bq0 = myaq + grp * 128 + min(m, 3) * 32;
@@ -663,7 +809,7 @@ extern "C" int g53h_set_mfma_decode_trace(void *dev_buf)
 
 static int dm_takes(const G53hMoeLayer *L, const int *idx_in)
 {
-    return L->tiled == 2 && L->block_c == 128 && L->hidden == G53_DEC_E && L->inter == G53_DEC_I &&
+    return (L->tiled == 2 || L->tiled == 4) && L->block_c == 128 && L->hidden == G53_DEC_E && L->inter == G53_DEC_I &&
            (idx_in || (L->router_dt == 1 && L->router)) && L->topk >= 1 && L->topk <= G53_DEC_MAXK &&
            L->n_experts >= 1 && L->n_experts <= G53_DEC_MAXNE;
 }
@@ -674,7 +820,7 @@ static int dm_size_grid(void)
         const int cus = g53h_num_cus();
         int per = 0;
         g_dm_grid = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_dec_mfma, G53_DM_NT, 0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_dec_mfma<false>, G53_DM_NT, 0) != hipSuccess)
             (void)hipGetLastError();
         else if (per >= 1 && cus >= 128 && cus <= 512)
             g_dm_grid = cus;
@@ -714,7 +860,10 @@ int g53h_decode_mtiled(float *out, const float *x, const G53hMoeLayer *L, int *i
     e.NE = L->n_experts; e.K = L->topk; e.norm_topk = L->norm_topk; e.epoch = g_dm_epoch;
     e.spin = g53h_spin_limit(); e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dm_trace;
     g53h_prof_mark(G53_PROF_START);
-    hipLaunchKernelGGL(k_dec_mfma, dim3(g_dm_grid), dim3(G53_DM_NT), 0, g53h_stream(), e);
+    if (L->tiled == 4)                 /* int4 MFMA-tiled routed experts */
+        hipLaunchKernelGGL(k_dec_mfma<true>, dim3(g_dm_grid), dim3(G53_DM_NT), 0, g53h_stream(), e);
+    else
+        hipLaunchKernelGGL(k_dec_mfma<false>, dim3(g_dm_grid), dim3(G53_DM_NT), 0, g53h_stream(), e);
     g53h_prof_mark(G53_PROF_FUSED);
     G53_LAUNCHED("k_dec_mfma");
     return 0;

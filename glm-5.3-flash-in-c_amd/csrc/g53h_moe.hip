@@ -334,7 +334,7 @@ extern "C" int g53h_moe_routed_given(float *out, const float *x, int T, const G5
     if (g53h_ready() || g53_check_layer(L, T)) return -1;
     if (T == 0) return 0;
     if (T == 1 && L->tiled) {                    /* one launch that skips the routing */
-        const int r = L->tiled == 2 ? g53h_decode_mtiled(out, x, L, nullptr, nullptr, idx, wts)
+        const int r = (L->tiled == 2 || L->tiled == 4) ? g53h_decode_mtiled(out, x, L, nullptr, nullptr, idx, wts)
                                     : g53h_decode_tiled(out, x, L, nullptr, nullptr, idx, wts);
         if (r <= 0) return r;
     }
@@ -376,7 +376,7 @@ extern "C" int g53h_moe(float *out, const float *x, int T, const G53hMoeLayer *L
     if (T == 0) return 0;
     if (!L->router || !L->bias) return g53h_fail("g53h_moe: no router");
     if (T == 1) {                                    /* single-token decode: one fused launch */
-        const int r = L->tiled == 2 ? g53h_decode_mtiled(out, x, L, idx_out, w_out, nullptr, nullptr)
+        const int r = (L->tiled == 2 || L->tiled == 4) ? g53h_decode_mtiled(out, x, L, idx_out, w_out, nullptr, nullptr)
                       : L->tiled  ? g53h_decode_tiled(out, x, L, idx_out, w_out, nullptr, nullptr)
                                   : g53h_decode_fused(out, x, L, idx_out, w_out);
         if (r <= 0) return r;

@@ -33,6 +33,8 @@ hipStream_t g53h_copy_stream(void);   /* side stream for host-to-HBM expert copi
 int g53h_tile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, hipStream_t s);
 int g53h_mtile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse, hipStream_t s);
 int g53h_tile_i4_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse, hipStream_t s);
+int g53h_mtile_i4_on(uint8_t *dw, float *ds, const uint8_t *sw, const float *ss, int rows, int cols, int inverse,
+                     hipStream_t s);
 int g53h_i4_from_f8_on(uint8_t *q_d, float *steps_d, const G53hMat *src, hipStream_t s);
 
 /* Library workspace in HBM, grown on demand (grow = sync + free + alloc), 256-B aligned.

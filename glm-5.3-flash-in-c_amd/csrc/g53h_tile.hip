@@ -226,6 +226,99 @@ extern "C" int g53h_tile_i4_host(uint8_t *dst, const uint8_t *src, int rows, int
     return 0;
 }
 
+/* ------------------------------------------------ int4, MFMA-tiled (G53H_MAT_I4 | MTILED) ---- */
+namespace {
+
+/* 8-byte piece q of the int4 MFMA-tiled matrix: unit u = q / 64 (row octet u / nb, 128-column
+ * block u % nb), lane slot (q % 64) / 2 = 8 g + m, half q % 2: row 8 (u / nb) + m, columns
+ * 128 (u % nb) + 64 (g & 1) + 16 (g >> 1) + 32 half .. + 15, i.e. 8 bytes of the row-major row. */
+__host__ __device__ inline void g53_i4m_piece(long q, int nb, int &row, int &col0)
+{
+    const long u = q >> 6;
+    const int ls = (int)(q & 63) >> 1, hf = (int)(q & 1), g = ls >> 3, m = ls & 7;
+    row = (int)(u / nb) * 8 + m;
+    col0 = (int)(u % nb) * 128 + 64 * (g & 1) + 16 * (g >> 1) + 32 * hf;
+}
+
+/* Step q of the tiled steps: unit q / 16, half (q / 8) % 2, row q % 8 of the octet. */
+__host__ __device__ inline void g53_i4m_step(long q, int nb, int &row, int &grp)
+{
+    const long u = q >> 4;
+    row = (int)(u / nb) * 8 + (int)(q & 7);
+    grp = (int)(u % nb) * 2 + (int)((q >> 3) & 1);
+}
+
+__global__ void __launch_bounds__(256) k_mtile_i4(uint8_t *__restrict__ dw, float *__restrict__ ds,
+                                                  const uint8_t *__restrict__ sw, const float *__restrict__ ss,
+                                                  int cols, long npc, long nst, int inverse)
+{
+    const long q = (long)blockIdx.x * 256 + threadIdx.x;
+    const int nb = cols / 128;
+    if (q < npc) {
+        int row, c0;
+        g53_i4m_piece(q, nb, row, c0);
+        uint2 *t = (uint2 *)((inverse ? sw : dw) + 8 * q);
+        uint2 *r = (uint2 *)((inverse ? dw : sw) + (size_t)row * (cols / 2) + c0 / 2);
+        if (inverse) *r = *t;
+        else *t = *r;
+    }
+    if (q < nst) {
+        int row, grp;
+        g53_i4m_step(q, nb, row, grp);
+        if (inverse) ds[(size_t)row * (cols / 64) + grp] = ss[q];
+        else ds[q] = ss[(size_t)row * (cols / 64) + grp];
+    }
+}
+
+}
+
+int g53h_mtile_i4_on(uint8_t *dw, float *ds, const uint8_t *sw, const float *ss, int rows, int cols, int inverse,
+                     hipStream_t s)
+{
+    if (g53h_ready()) return -1;
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128)
+        return g53h_fail("g53h_mtile_i4: a %d x %d matrix cannot be MFMA-tiled (rows a multiple of 8, columns of 128)",
+                         rows, cols);
+    if (dw == sw || (const void *)ds == (const void *)ss)
+        return g53h_fail("g53h_mtile_i4: in-place conversion is not supported");
+    const long npc = (long)rows * cols / 16, nst = (long)rows * (cols / 64);
+    hipLaunchKernelGGL(k_mtile_i4, dim3((unsigned)((npc + 255) / 256)), dim3(256), 0, s, dw, ds, sw, ss, cols, npc,
+                       nst, inverse);
+    G53_LAUNCHED("k_mtile_i4");
+    return 0;
+}
+
+extern "C" int g53h_mtile_i4(uint8_t *dst_w, float *dst_s, const uint8_t *src_w, const float *src_s, int rows,
+                             int cols, int inverse)
+{
+    if (g53h_ready()) return -1;
+    return g53h_mtile_i4_on(dst_w, dst_s, src_w, src_s, rows, cols, inverse, g53h_stream());
+}
+
+extern "C" int g53h_mtile_i4_host(uint8_t *dst_w, float *dst_s, const uint8_t *src_w, const float *src_s, int rows,
+                                  int cols, int inverse)
+{
+    if (rows <= 0 || cols <= 0 || rows % 8 || cols % 128 || dst_w == src_w) return -1;
+    const int nb = cols / 128;
+    const long npc = (long)rows * cols / 16, nst = (long)rows * (cols / 64);
+    for (long q = 0; q < npc; q++) {
+        int row, c0;
+        g53_i4m_piece(q, nb, row, c0);
+        uint8_t *r = (uint8_t *)(inverse ? dst_w : src_w) + (size_t)row * (cols / 2) + c0 / 2;
+        uint8_t *t = (uint8_t *)(inverse ? src_w : dst_w) + 8 * q;
+        if (inverse) memcpy(r, t, 8);
+        else memcpy(t, r, 8);
+    }
+    if (dst_s && src_s)
+        for (long q = 0; q < nst; q++) {
+            int row, grp;
+            g53_i4m_step(q, nb, row, grp);
+            if (inverse) dst_s[(size_t)row * (cols / 64) + grp] = src_s[q];
+            else dst_s[q] = src_s[(size_t)row * (cols / 64) + grp];
+        }
+    return 0;
+}
+
 int g53h_mtile_f8_on(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse, hipStream_t s)
 {
     if (g53h_ready() || g53_tile_shape(rows, cols)) return -1;

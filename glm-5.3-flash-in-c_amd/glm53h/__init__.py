@@ -218,6 +218,8 @@ _SIGS = {
     "g53h_mtile_f8_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "g53h_tile_i4": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "g53h_tile_i4_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "g53h_mtile_i4": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
+    "g53h_mtile_i4_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),
     "g53h_tile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "g53h_untile_f8": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int]),
     "g53h_tile_f8_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]),

@@ -149,9 +149,12 @@ class DeviceLayer:
         (G53H_MAT_I4: levels, and one step per row and 64 columns; the reference's
         --experts int4), the shared expert staying FP8; the layer then has block_c 0.
         i4 and tiled: the int4 levels int4-tiled (G53H_MAT_I4T), the layout of the one-launch
-        int4 decode, and the shared expert octet-tiled; the layer has tiled 3, block_c 128."""
-        assert not (mfma and (tiled or i4))
+        int4 decode, and the shared expert octet-tiled; the layer has tiled 3, block_c 128.
+        i4 and mfma: the int4 levels and steps int4 MFMA-tiled (G53H_MAT_I4 | G53H_MAT_MTILED), the
+        layout of the FP4 matrix-core decode, and the shared expert FP8 MFMA-tiled; tiled 4."""
+        assert not (mfma and tiled)
         self = cls(sp)
+        self.i4m = bool(mfma and i4)
         self.i4t = bool(tiled and i4)
         if self.i4t:
             tiled = False
@@ -178,7 +181,8 @@ class DeviceLayer:
             s_stage = _align(max(r * c for r, c in shapes))
             stage = DevBuf(s_stage + max(((r + sp.br - 1) // sp.br) * ((c + sp.bc - 1) // sp.bc) * 4
                                          for r, c in shapes))
-            stage4 = DevBuf(max(r * c // 2 for r, c in shapes)) if self.i4t else None
+            stage4 = DevBuf(max(r * c // 2 for r, c in shapes)) if (self.i4t or self.i4m) else None
+            stage4s = DevBuf(max(r * (c // 64) * 4 for r, c in shapes)) if self.i4m else None
         for i in range(nslots):
             base = self.arena.ptr + i * self.slot_bytes
             mats = []
@@ -196,15 +200,19 @@ class DeviceLayer:
                     if self.i4t:                 # quantised row-major into staging, then tiled
                         check(L.g53h_i4_from_f8(stage4.ptr, st, C.byref(f)), "g53h_i4_from_f8")
                         check(L.g53h_tile_i4(q, stage4.ptr, r, c, 0), "g53h_tile_i4")
+                    elif self.i4m:               # levels and steps into staging, then MFMA-tiled
+                        check(L.g53h_i4_from_f8(stage4.ptr, stage4s.ptr, C.byref(f)), "g53h_i4_from_f8")
+                        check(L.g53h_mtile_i4(q, st, stage4.ptr, stage4s.ptr, r, c, 0), "g53h_mtile_i4")
                     else:
                         check(L.g53h_i4_from_f8(q, st, C.byref(f)), "g53h_i4_from_f8")
-                    mats.append(G53hMat(q, st, r, c, 1, 64, c // 64, 4 | (16 if self.i4t else 0)))
+                    mats.append(G53hMat(q, st, r, c, 1, 64, c // 64,
+                                        4 | (16 if self.i4t else 0) | (8 if self.i4m else 0)))
                 descs[i] = G53hExpert(*mats)
                 continue
             # an int4 layer keeps its FP8 shared expert octet-tiled where the shapes allow (the
             # row-wave kernel's fast FP8 path), as the drop-in does
             tile = self.tiled or (self.i4 and sp.bc == 128 and all(r % 8 == 0 and c % 128 == 0 for r, c in shapes))
-            assert tile or not self.i4t, "the int4-tiled layer needs an octet-tiled shared expert"
+            assert tile or not (self.i4t or self.i4m), "the int4-tiled layer needs a tiled shared expert"
             for m, (r, c) in enumerate(shapes):
                 strm = stream(K_SHARED, sp.layer, m) if i == NE else stream(K_EXPERT, sp.layer, i * 3 + m)
                 w, s = base + code_off[m], base + sc_off[m]
@@ -230,8 +238,8 @@ class DeviceLayer:
             routed_scale=sp.routed_scale, swiglu_limit=sp.limit, router=self.router.ptr, router_dt=1,
             bias=self.bias.ptr, experts=self.table.ptr,
             shared=(self.table.ptr + NE * C.sizeof(G53hExpert)) if sp.shared else None,
-            block_c=sp.bc if self.i4t else (0 if self.i4 else sp.bc),
-            tiled=3 if self.i4t else ((2 if self.mfma else 1) if self.tiled else 0))
+            block_c=sp.bc if (self.i4t or self.i4m) else (0 if self.i4 else sp.bc),
+            tiled=4 if self.i4m else (3 if self.i4t else ((2 if self.mfma else 1) if self.tiled else 0)))
         check(L.g53h_sync(), "g53h_sync")
         del stage
         return self
@@ -250,6 +258,11 @@ class DeviceLayer:
                     rm = np.zeros_like(w)
                     assert lib().g53h_tile_i4_host(rm.ctypes.data, w.ctypes.data, m.rows, m.cols, 1) == 0
                     w = rm
+                elif m.flags & 8:                 # int4 MFMA-tiled: levels and steps row-major
+                    rm, rs = np.zeros_like(w), np.zeros_like(s)
+                    assert lib().g53h_mtile_i4_host(rm.ctypes.data, rs.ctypes.data, w.ctypes.data, s.ctypes.data,
+                                                    m.rows, m.cols, 1) == 0
+                    w, s = rm, rs
                 out.append((w, s))
                 continue
             w = np.empty(m.rows * m.cols, np.uint8)

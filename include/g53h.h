@@ -86,6 +86,13 @@ int         g53h_mem_info(size_t *free_b, size_t *total_b);
  * stay [rows][cols / 64]. One 64-lane load of 16 bytes per lane reads a unit and leaves in each
  * lane exactly the 8 levels of one of the reference's eight fp32 accumulators of four groups. */
 #define G53H_MAT_I4T     16
+/* Int4 levels (G53H_MAT_I4 with G53H_MAT_MTILED) in the operand order of the FP4 matrix cores,
+ * the layout of the int4 k_dec_mfma: units of 8 rows x 128 columns (512 bytes), unit (r / 8,
+ * c / 128) at ((r / 8) (cols / 128) + c / 128) * 512; lane slot 8 g + m (g < 4, m < 8) of a unit
+ * holds 16 bytes: row m's columns 64 (g & 1) + 16 (g >> 1) + 0..15 and then + 32 .. + 47, each
+ * run as the 8 row-major bytes (the even column in the low nibble). The steps are tiled the same
+ * way: 16 floats per unit at its index * 16, [64-column half of the block][row m]. One 64-lane
+ * load of 16 bytes per lane reads two row octets' units of one block. */
 typedef struct {
     const uint8_t *w;
     const float   *s;
@@ -172,6 +179,10 @@ typedef struct {
                                        (G53H_MAT_MTILED), 3: routed experts int4, int4-tiled
                                        (G53H_MAT_I4 | G53H_MAT_I4T), the shared expert FP8
                                        octet-tiled (single-token decode only; block_c 128),
+                                       4: routed experts int4, int4 MFMA-tiled (G53H_MAT_I4 |
+                                       G53H_MAT_MTILED), the shared expert FP8 MFMA-tiled
+                                       (single-token decode by k_dec_mfma, within the
+                                       tolerance; block_c 128),
                                        0: row-major                                          */
     /* Experts in the int4 format (G53H_MAT_I4, per matrix) need block_c = 0 and tiled = 0: the
        row-wave kernels then take them (and any FP8 matrix, such as the shared expert, in the
@@ -335,6 +346,13 @@ int g53h_mtile_f8_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int
  * (G53H_MAT_I4T); inverse != 0 converts back. rows a multiple of 8, cols of 256. */
 int g53h_tile_i4(uint8_t *dst_d, const uint8_t *src_d, int rows, int cols, int inverse);
 int g53h_tile_i4_host(uint8_t *dst, const uint8_t *src, int rows, int cols, int inverse);
+/* Int4 levels [rows][cols / 2] and steps [rows][cols / 64] (GLM53F_WI4) to the int4 MFMA-tiled
+ * layout (G53H_MAT_I4 | G53H_MAT_MTILED), levels and steps together; inverse != 0 converts back.
+ * rows a multiple of 8, cols of 128; the host twin skips the steps when either is NULL. */
+int g53h_mtile_i4(uint8_t *dst_w, float *dst_s, const uint8_t *src_w, const float *src_s, int rows, int cols,
+                  int inverse);
+int g53h_mtile_i4_host(uint8_t *dst_w, float *dst_s, const uint8_t *src_w, const float *src_s, int rows, int cols,
+                       int inverse);
 
 /* -------------------------------------------------------- checks and inputs ---- */
 /* y[i] = expf(x[i]) by the device restatement of glibc's expf (for exhaustive checks). */

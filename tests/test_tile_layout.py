@@ -145,3 +145,36 @@ def test_int4_tiled_round_trip_and_accumulator_order():
                 for i in range(8):
                     s += (((int(t[m, p, g]) >> (4 * i)) & 15) - 8) * int(x[64 * g + acc + 8 * i])
             assert s == int(L[m, 64 * g:64 * g + 64] @ x[64 * g:64 * g + 64])
+
+
+def test_int4_mfma_tiled_operand_order_and_steps():
+    """Int4 MFMA-tiled units (G53H_MAT_I4 | G53H_MAT_MTILED): 8 rows x 128 columns per 512 bytes;
+    lane slot 8 g + m holds row m's levels in the FP4 operand order of the matrix cores: nibble j
+    (low first) is column 64 (g & 1) + 16 (g >> 1) + j for j < 16 and + 32 + (j - 16) after;
+    the steps, 16 floats per unit, are [64-column half][row]."""
+    lib = glm53h.lib()
+    rng = np.random.default_rng(9)
+    for rows, cols in [(8, 128), (16, 384), (24, 256)]:
+        a = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+        st = rng.standard_normal(rows * (cols // 64)).astype(np.float32)
+        t, ts = np.zeros_like(a), np.zeros_like(st)
+        assert lib.g53h_mtile_i4_host(t.ctypes.data, ts.ctypes.data, a.ctypes.data, st.ctypes.data, rows, cols, 0) == 0
+        back, bs = np.zeros_like(a), np.zeros_like(st)
+        assert lib.g53h_mtile_i4_host(back.ctypes.data, bs.ctypes.data, t.ctypes.data, ts.ctypes.data, rows, cols, 1) == 0
+        assert np.array_equal(back, a) and np.array_equal(bs, st)
+        Lv = levels(a, rows, cols)
+        S = st.reshape(rows, cols // 64)
+        nb = cols // 128
+        u8 = t.reshape(rows // 8, nb, 4, 8, 16)                     # octet, block, g, m, bytes
+        us = ts.reshape(rows // 8, nb, 2, 8)                        # octet, block, half, row
+        for o8 in range(rows // 8):
+            for blk in range(nb):
+                for g in range(4):
+                    base = blk * 128 + 64 * (g & 1) + 16 * (g >> 1)
+                    cols_j = [base + j if j < 16 else base + 32 + (j - 16) for j in range(32)]
+                    for m in range(8):
+                        by = u8[o8, blk, g, m]
+                        nib = [(int(by[j // 2]) >> (4 * (j % 2))) & 15 for j in range(32)]
+                        assert nib == list(Lv[o8 * 8 + m, cols_j])
+                for hf in range(2):
+                    assert np.array_equal(us[o8, blk, hf], S[o8 * 8:o8 * 8 + 8, 2 * blk + hf])
