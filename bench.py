@@ -761,7 +761,7 @@ def main():
     prefill = None if (i4 or i4t or i4m or a.no_prefill) else prefill_beside(L, olayer, sp)
     batched = None if (i4 or i4t or i4m or a.no_prefill) else batched_beside(L, olayer)
     traffic = None                      # HBM bytes per launch from the committed counter summary
-    tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 or i4t else ''}_traffic.json")
+    tp = os.path.join(ROOT, "profiles", f"{kname}_config2{'_int4' if i4 or i4t or i4m else ''}_traffic.json")
     if os.path.exists(tp):
         with open(tp) as f:
             traffic = json.load(f).get("traffic_bytes")
