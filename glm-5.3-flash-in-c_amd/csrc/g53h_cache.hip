@@ -78,8 +78,11 @@ struct Impl {
     bool i4 = false;                /* int4 slots: FP8 staged, quantised into the slot      */
     bool i4t = false;               /* int4 mode 2: the levels quantised into staging, then
                                        int4-tiled into the slot (the steps straight in)     */
+    bool i4m = false;               /* int4 mode 3: levels and steps quantised into staging,
+                                       then int4 MFMA-tiled into the slot together          */
     uint8_t *stage_demand = nullptr, *stage_prefetch = nullptr;
-    size_t stage_lv = 0;            /* int4 mode 2: the levels' offset in a staging buffer  */
+    size_t stage_lv = 0;            /* int4 modes 2, 3: the levels' offset in a staging buffer */
+    size_t stage_st = 0;            /* int4 mode 3: the steps' offset                       */
     std::vector<Copy> inflight;     /* copies not yet seen complete                         */
     std::vector<hipEvent_t> pool;   /* spare events                                         */
     /* tiled slots: the descriptor of every key whose read has been seen complete, per layer in
@@ -172,7 +175,8 @@ void table_set(Glm53fCache *c, Impl *m, int slot, int layer, int expert)
     for (int i = 0; i < 3; i++) {
         d[i]->w = (const uint8_t *)v[i]->w; d[i]->s = v[i]->s;
         d[i]->rows = v[i]->rows; d[i]->cols = v[i]->cols; d[i]->br = v[i]->br; d[i]->bc = v[i]->bc;
-        d[i]->scols = v[i]->scols; d[i]->flags = m->i4t ? (G53H_MAT_I4 | G53H_MAT_I4T) : G53H_MAT_TILED;
+        d[i]->scols = v[i]->scols;
+        d[i]->flags = m->i4t ? (G53H_MAT_I4 | G53H_MAT_I4T) : m->i4m ? (G53H_MAT_I4 | G53H_MAT_MTILED) : G53H_MAT_TILED;
     }
     m->tab_key[slot] = key;
     m->tab_dirty[layer] = 1;
@@ -263,13 +267,17 @@ int issue_reads(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStr
         f.w = stage; f.s = (const float *)(stage + sc_off);
         f.rows = m->geo.rows[i]; f.cols = m->geo.cols[i]; f.br = m->geo.br[i]; f.bc = m->geo.bc[i];
         f.scols = m->geo.scols[i];
-        /* int4 mode 2: the levels into staging after the FP8 bytes, then tiled into the slot */
-        uint8_t *lv = m->i4t ? stage + m->stage_lv : base + m->geo.off[i];
+        /* int4 modes 2, 3: the levels (mode 3: and the steps) into staging after the FP8 bytes,
+         * then tiled into the slot */
+        uint8_t *lv = (m->i4t || m->i4m) ? stage + m->stage_lv : base + m->geo.off[i];
+        float *sl = (float *)(m->i4m ? stage + m->stage_st : base + m->geo.off[3 + i]);
         if (hipMemcpyAsync(stage, mats[i]->w, m->geo.fbytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
             hipMemcpyAsync(stage + sc_off, mats[i]->s, m->geo.fbytes[3 + i], hipMemcpyHostToDevice, s) !=
                 hipSuccess ||
-            g53h_i4_from_f8_on(lv, (float *)(base + m->geo.off[3 + i]), &f, s) ||
-            (m->i4t && g53h_tile_i4_on(base + m->geo.off[i], lv, m->geo.rows[i], m->geo.cols[i], 0, s)))
+            g53h_i4_from_f8_on(lv, sl, &f, s) ||
+            (m->i4t && g53h_tile_i4_on(base + m->geo.off[i], lv, m->geo.rows[i], m->geo.cols[i], 0, s)) ||
+            (m->i4m && g53h_mtile_i4_on(base + m->geo.off[i], (float *)(base + m->geo.off[3 + i]), lv, sl,
+                                        m->geo.rows[i], m->geo.cols[i], 0, s)))
             return 0;
         *nread += (int64_t)(m->geo.fbytes[i] + m->geo.fbytes[3 + i]);
     }
@@ -315,7 +323,7 @@ void view_of(const Glm53fCache *c, const Impl *m, int slot, Glm53fExpertQ *q)
         Glm53fMat &v = *mats[i];
         v.w = base + m->geo.off[i];
         v.s = (const float *)(base + m->geo.off[3 + i]);
-        v.dt = m->i4 ? (m->i4t ? GLM53F_WI4T : GLM53F_WI4) : (m->tiled ? GLM53F_WF8T : GLM53F_WF8);
+        v.dt = m->i4 ? (m->i4t ? GLM53F_WI4T : m->i4m ? GLM53F_WI4M : GLM53F_WI4) : (m->tiled ? GLM53F_WF8T : GLM53F_WF8);
         v.rows = m->geo.rows[i]; v.cols = m->geo.cols[i];
         if (m->i4) {                                 /* glm53f_expert_i4_view's geometry */
             v.br = 1; v.bc = GLM53F_I4_GROUP; v.scols = m->geo.cols[i] / GLM53F_I4_GROUP;
@@ -469,7 +477,7 @@ extern "C" int g53h_cache_slot_kind(const Glm53fExpertSrc *src)
 {
     if (!g53h_cache_is(src)) return 0;
     const Impl *m = impl_of((const Glm53fCache *)src);
-    return !m ? 0 : m->tiled ? 1 : m->i4t ? 3 : 0;
+    return !m ? 0 : m->tiled ? 1 : m->i4t ? 3 : m->i4m ? 4 : 0;
 }
 
 extern "C" int g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **table_d,
@@ -566,8 +574,10 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
     /* int4 mode 2 at the shapes the octet test above accepts (their rows are multiples of 8 and
      * columns of 256, as the int4 tiling needs) */
     m->i4t = m->i4 && i4 == 2 && m->tiled;
+    m->i4m = m->i4 && i4 == 3 && m->tiled;      /* int4 mode 3: the same shapes, MFMA-tiled */
     if (m->i4) m->tiled = false;
     if (m->i4t) c->i4 = 2;
+    if (m->i4m) c->i4 = 3;
     c->nslot = (int)(budget_bytes / c->slot_bytes);
     if (c->nslot < cfg->topk + 1) {
         fprintf(stderr, "glm53f_cache: budget %.2f GB gives %d slots of %.2f MB; top-%d needs at least %d\n",
@@ -599,20 +609,26 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
     if (ok && (m->tiled || m->i4)) {
         size_t sb = 0;                               /* the largest matrix (with its scales) */
         size_t lb = 0;                               /* the largest matrix's int4 levels */
+        size_t stb = 0;                              /* and its steps */
         for (int i = 0; i < 3; i++) {
             const size_t need = m->i4 ? al(m->geo.fbytes[i], 256) + m->geo.fbytes[3 + i] : m->geo.bytes[i];
             if (need > sb) sb = need;
             if (m->i4 && m->geo.bytes[i] > lb) lb = m->geo.bytes[i];
+            if (m->i4 && m->geo.bytes[3 + i] > stb) stb = m->geo.bytes[3 + i];
         }
-        if (m->i4t) {
+        if (m->i4t || m->i4m) {
             m->stage_lv = al(sb, 256);
             sb = m->stage_lv + lb;
+        }
+        if (m->i4m) {
+            m->stage_st = al(sb, 256);
+            sb = m->stage_st + stb;
         }
         m->stage_demand = (uint8_t *)g53h_alloc(sb);
         m->stage_prefetch = (uint8_t *)g53h_alloc(sb);
         ok = m->stage_demand && m->stage_prefetch;
     }
-    if (ok && (m->tiled || m->i4t)) {
+    if (ok && (m->tiled || m->i4t || m->i4m)) {
         const size_t tb = (size_t)c->n_layers * (size_t)c->n_experts * sizeof(G53hExpert);
         m->tab_h = (G53hExpert *)g53h_host_alloc(tb);
         m->tab_d = (G53hExpert *)g53h_alloc(tb);

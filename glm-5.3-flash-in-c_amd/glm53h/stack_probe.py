@@ -37,8 +37,8 @@ def main():
     ap.add_argument("--steps", type=int, default=16)
     ap.add_argument("--slots", type=int, default=1200, help="cache slots (25.2 MB each, 14.2 MB int4); the default holds every expert")
     ap.add_argument("--passes", type=int, default=3, help="timed passes over the steps, after two warm ones")
-    ap.add_argument("--int4", type=int, default=0, choices=[0, 1, 2],
-                    help="the cache's int4 mode: 0 FP8 slots, 1 the reference's int4 slots, 2 int4-tiled slots")
+    ap.add_argument("--int4", type=int, default=0, choices=[0, 1, 2, 3],
+                    help="the cache's int4 mode: 0 FP8 slots, 1 the reference's int4 slots, 2 int4-tiled slots, 3 int4 MFMA-tiled slots")
     a = ap.parse_args()
     L = glm53h.init(0)
     NL, STEPS = a.layers, a.steps

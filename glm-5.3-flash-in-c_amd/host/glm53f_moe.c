@@ -168,9 +168,10 @@ void glm53f_forget_host_weights(void)
 }
 
 /* Bytes of a matrix's codes and scales: FP8 [rows][cols] codes and [ceil(rows/br)][scols]
- * scales; int4 (GLM53F_WI4, and GLM53F_WI4T with the levels int4-tiled) [rows][cols/2] packed
+ * scales; int4 (GLM53F_WI4, GLM53F_WI4T with the levels int4-tiled, GLM53F_WI4M with levels and
+ * steps int4 MFMA-tiled) [rows][cols/2] packed
  * levels and [rows][scols] steps. */
-static int mat_i4(const Glm53fMat *m) { return m->dt == GLM53F_WI4 || m->dt == GLM53F_WI4T; }
+static int mat_i4(const Glm53fMat *m) { return m->dt == GLM53F_WI4 || m->dt == GLM53F_WI4T || m->dt == GLM53F_WI4M; }
 static size_t mat_code_bytes(const Glm53fMat *m)
 {
     return mat_i4(m) ? (size_t)m->rows * (size_t)(m->cols / 2) : (size_t)m->rows * (size_t)m->cols;
@@ -183,7 +184,8 @@ static size_t mat_scale_bytes(const Glm53fMat *m)
 static int mat_flags(const Glm53fMat *m)
 {
     return m->dt == GLM53F_WF8T ? G53H_MAT_TILED
-           : m->dt == GLM53F_WI4 ? G53H_MAT_I4 : m->dt == GLM53F_WI4T ? (G53H_MAT_I4 | G53H_MAT_I4T) : 0;
+           : m->dt == GLM53F_WI4 ? G53H_MAT_I4 : m->dt == GLM53F_WI4T ? (G53H_MAT_I4 | G53H_MAT_I4T)
+           : m->dt == GLM53F_WI4M ? (G53H_MAT_I4 | G53H_MAT_MTILED) : 0;
 }
 
 static void check_f8(const Glm53fMat *m, const char *what)
@@ -260,35 +262,44 @@ static G53Buf g_xin, g_out, g_idx, g_w, g_flag, g_table, g_pred, g_tmp, g_contri
 /* The same in the octet-tiled layout (for the tiled decode kernel), resident as well: uploaded
  * row-major once, converted on the device, kept under the host address with its own tag. */
 static G53Buf g_tile_stage;
-static G53hMat dev_mat_resident_tiled(const Glm53fMat *m, const char *what)
+/* mfma != 0: the MFMA-tiled copy (G53H_MAT_MTILED) instead of the octet-tiled one; each layout
+ * is kept under its own key. */
+static G53hMat dev_mat_resident_tiled_as(const Glm53fMat *m, const char *what, int mfma)
 {
     check_rowmajor(m, what);
     if (m->dt != GLM53F_WF8) {
-        fprintf(stderr, "glm53f: FATAL, %s: only FP8 matrices are kept octet-tiled\n", what);
+        fprintf(stderr, "glm53f: FATAL, %s: only FP8 matrices are kept tiled\n", what);
         abort();
     }
     G53hMat d;
     memset(&d, 0, sizeof d);
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
-    d.flags = G53H_MAT_TILED;
+    d.flags = mfma ? G53H_MAT_MTILED : G53H_MAT_TILED;
     d.s = (const float *)resident(m->s, mat_scale_bytes(m));
     if (g53h_is_device_ptr(m->w)) {
         fprintf(stderr, "glm53f: FATAL, %s: an HBM matrix is used as it is, not converted\n", what);
         abort();
     }
     const size_t n = mat_code_bytes(m);
-    G53Res *r = res_find((const char *)m->w + 1);        /* the tiled copy's own key */
-    if (r && r->n == n && r->dt == -2 && res_same(r, m->w, n)) { d.w = (const uint8_t *)r->d; return d; }
+    const char *key = (const char *)m->w + (mfma ? 2 : 1); /* the tiled copy's own key */
+    const int rdt = mfma ? -3 : -2;
+    G53Res *r = res_find(key);
+    if (r && r->n == n && r->dt == rdt && res_same(r, m->w, n)) { d.w = (const uint8_t *)r->d; return d; }
     uint8_t *stage = (uint8_t *)buf_get(&g_tile_stage, n);
     uint8_t *t = (uint8_t *)g53h_alloc(n);
-    if (!t || g53h_h2d(stage, m->w, n) || g53h_tile_f8(t, stage, m->rows, m->cols) || g53h_sync())
+    if (!t || g53h_h2d(stage, m->w, n) ||
+        (mfma ? g53h_mtile_f8(t, stage, m->rows, m->cols, 0) : g53h_tile_f8(t, stage, m->rows, m->cols)) || g53h_sync())
         g53_die("tiling a resident weight");
-    if (!r) r = res_insert((const char *)m->w + 1);
+    if (!r) r = res_insert(key);
     else if (g53h_sync() || g53h_free(r->d)) g53_die("replacing a resident weight");
-    r->n = n; r->d = t; r->dt = -2;
+    r->n = n; r->d = t; r->dt = rdt;
     res_record(r, m->w, n);
     d.w = t;
     return d;
+}
+static G53hMat dev_mat_resident_tiled(const Glm53fMat *m, const char *what)
+{
+    return dev_mat_resident_tiled_as(m, what, 0);
 }
 
 /* Host operand -> HBM (or the operand itself when it is HBM already). */
@@ -314,9 +325,9 @@ static G53Buf g_mat[3];
 static G53hMat dev_mat_staged(const Glm53fMat *m, G53Buf *b, const char *what)
 {
     check_f8(m, what);
-    if (m->dt == GLM53F_WI4T) {
-        fprintf(stderr, "glm53f: FATAL, %s is an int4-tiled cache view (GLM53F_WI4T); only glm53f_moe reads "
-                        "those\n", what);
+    if (m->dt == GLM53F_WI4T || m->dt == GLM53F_WI4M) {
+        fprintf(stderr, "glm53f: FATAL, %s is an int4-tiled cache view (GLM53F_WI4T / GLM53F_WI4M); only "
+                        "glm53f_moe reads those\n", what);
         abort();
     }
     const int dev = g53h_is_device_ptr(m->w);
@@ -661,22 +672,23 @@ int g53h_set_speculate(int on)
     return prev;
 }
 
-/* The shared expert's descriptor in HBM (octet-tiled, resident), one per layer, uploaded when
- * it changes. */
-static G53hExpert g_shh[GLM53F_MAX_LAYERS + 1];
-static G53Buf g_shd;
-static const G53hExpert *shared_desc(const Glm53fMoeW *w)
+/* The shared expert's descriptor in HBM (octet-tiled, or MFMA-tiled when mfma != 0; resident),
+ * one per layer and layout, uploaded when it changes. */
+static G53hExpert g_shh[2][GLM53F_MAX_LAYERS + 1];
+static G53Buf g_shd[2];
+static const G53hExpert *shared_desc(const Glm53fMoeW *w, int mfma)
 {
     const int l = w->layer >= 0 && w->layer <= GLM53F_MAX_LAYERS ? w->layer : GLM53F_MAX_LAYERS;
-    G53hExpert *d = (G53hExpert *)buf_get(&g_shd, (size_t)(GLM53F_MAX_LAYERS + 1) * sizeof(G53hExpert));
+    const int k = mfma ? 1 : 0;
+    G53hExpert *d = (G53hExpert *)buf_get(&g_shd[k], (size_t)(GLM53F_MAX_LAYERS + 1) * sizeof(G53hExpert));
     G53hExpert e;
     memset(&e, 0, sizeof e);
-    e.gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
-    e.up = dev_mat_resident_tiled(&w->sh_up, "shared up");
-    e.down = dev_mat_resident_tiled(&w->sh_down, "shared down");
-    if (memcmp(&e, &g_shh[l], sizeof e)) {
-        g_shh[l] = e;
-        if (g53h_h2d_async(d + l, &g_shh[l], sizeof e)) g53_die("glm53f_moe");
+    e.gate = dev_mat_resident_tiled_as(&w->sh_gate, "shared gate", k);
+    e.up = dev_mat_resident_tiled_as(&w->sh_up, "shared up", k);
+    e.down = dev_mat_resident_tiled_as(&w->sh_down, "shared down", k);
+    if (memcmp(&e, &g_shh[k][l], sizeof e)) {
+        g_shh[k][l] = e;
+        if (g53h_h2d_async(d + l, &g_shh[k][l], sizeof e)) g53_die("glm53f_moe");
     }
     return d + l;
 }
@@ -744,7 +756,8 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
      * below on the experts the gets returned. No cache call happens while the kernel runs, so
      * no slot it reads is refilled under it. */
     const G53hExpert *stab_d = NULL, *stab_h = NULL;
-    const int kind = g53h_cache_slot_kind(src);     /* 1 octet-tiled FP8 slots, 3 int4-tiled */
+    /* 1 octet-tiled FP8 slots, 3 int4-tiled, 4 int4 MFMA-tiled */
+    const int kind = g53h_cache_slot_kind(src);
     int spec = spec_enabled() && spec_worth() && dt == 1 && K <= 15 && NE <= 1024 && E == 4096 && c->moe_inter == 2048 &&
                G53_MB_OUT_OFF + 4 * G53H_NERR + ob <= G53H_MBOX_BYTES &&
                (!with_shared || shared_tileable(w)) && g53h_cache_layer_table(src, w->layer, &stab_d, &stab_h) == 0;
@@ -755,9 +768,9 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         memset(&SL, 0, sizeof SL);
         SL.hidden = E; SL.inter = c->moe_inter; SL.topk = K; SL.norm_topk = c->norm_topk;
         SL.routed_scale = c->routed_scale; SL.swiglu_limit = c->swiglu_limit;
-        SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = kind == 3 ? 3 : 1;
+        SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = kind == 3 || kind == 4 ? kind : 1;
         SL.n_experts = NE; SL.experts = stab_d;
-        SL.shared = with_shared ? shared_desc(w) : NULL;
+        SL.shared = with_shared ? shared_desc(w, kind == 4) : NULL;
         HP(7);
         if (x_host) upload_x(xd, x, E);
         if (per > 0 && g53h_decode_next(xd, ngate, ndt, nbias, NE, E)) g53_die("glm53f_router");
@@ -805,7 +818,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     HP(2);
     /* the chosen experts' views (slot order), the shared expert after them */
     G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
-    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1, i4r = 1, i4t = 1;
+    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1, i4r = 1, i4t = 1, i4m = 1;
     memset(tab, 0, (size_t)(K + 1) * sizeof(G53hExpert));
     for (int j = 0; j < K; j++) {
         Glm53fExpertQ q;
@@ -826,8 +839,11 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_TILED)) tiled = 0;
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4)) i4r = 0;
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4T)) i4t = 0;
+        if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4) ||
+            !(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_MTILED))
+            i4m = 0;
     }
-    if (!nh) i4r = i4t = 0;
+    if (!nh) i4r = i4t = i4m = 0;
     HP(3);
     if (spec) {                  /* every chosen expert was in the kernel's table: the output is done */
         g_spec_n[0]++;
@@ -843,10 +859,10 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         /* the shared expert resident in the layout of the routed slots */
         /* (int4 routed experts: the row-wave kernel's fast FP8 path reads it octet-tiled too) */
         const int tile_ok = (tiled || i4r) && shared_tileable(w);
-        if (tile_ok) {
-            tab[K].gate = dev_mat_resident_tiled(&w->sh_gate, "shared gate");
-            tab[K].up = dev_mat_resident_tiled(&w->sh_up, "shared up");
-            tab[K].down = dev_mat_resident_tiled(&w->sh_down, "shared down");
+        if (tile_ok) {           /* MFMA-tiled beside int4 MFMA-tiled views, else octet-tiled */
+            tab[K].gate = dev_mat_resident_tiled_as(&w->sh_gate, "shared gate", i4m);
+            tab[K].up = dev_mat_resident_tiled_as(&w->sh_up, "shared up", i4m);
+            tab[K].down = dev_mat_resident_tiled_as(&w->sh_down, "shared down", i4m);
         } else {
             tab[K].gate = dev_mat_resident(&w->sh_gate, "shared gate");
             tab[K].up = dev_mat_resident(&w->sh_up, "shared up");
@@ -858,19 +874,32 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     /* int4-tiled views: the one-launch int4 decode when the shared expert is octet-tiled (or
      * absent); else their levels untiled for the row kernels */
     const int one_i4t = i4t && (!with_shared || (tab[K].gate.flags & G53H_MAT_TILED));
-    if (i4t && !one_i4t) {
+    const int one_i4m = i4m && (!with_shared || (tab[K].gate.flags & G53H_MAT_MTILED));
+    if ((i4t && !one_i4t) || (i4m && !one_i4m)) {
+        /* the row kernels read row-major levels (and steps) */
         static G53Buf g_i4u[GLM53F_MAX_TOPK];
         for (int j = 0; j < K; j++) {
             G53hMat *ms[3] = {&tab[j].gate, &tab[j].up, &tab[j].down};
             if (!ms[0]->w) continue;
             size_t need = 0;
-            for (int i = 0; i < 3; i++) need += (((size_t)ms[i]->rows * (ms[i]->cols / 2)) + 255) & ~(size_t)255;
+            for (int i = 0; i < 3; i++)
+                need += ((((size_t)ms[i]->rows * (ms[i]->cols / 2)) + 255) & ~(size_t)255) +
+                        (i4m ? (((size_t)ms[i]->rows * ms[i]->scols * 4 + 255) & ~(size_t)255) : 0);
             uint8_t *b = (uint8_t *)buf_get(&g_i4u[j], need);
             for (int i = 0; i < 3; i++) {
-                if (g53h_tile_i4(b, ms[i]->w, ms[i]->rows, ms[i]->cols, 1)) g53_die("converting an int4 expert view");
-                ms[i]->w = b;
-                ms[i]->flags = G53H_MAT_I4;
+                uint8_t *lv = b;
                 b += (((size_t)ms[i]->rows * (ms[i]->cols / 2)) + 255) & ~(size_t)255;
+                if (i4m) {
+                    float *st = (float *)b;
+                    b += ((size_t)ms[i]->rows * ms[i]->scols * 4 + 255) & ~(size_t)255;
+                    if (g53h_mtile_i4(lv, st, ms[i]->w, ms[i]->s, ms[i]->rows, ms[i]->cols, 1))
+                        g53_die("converting an int4 expert view");
+                    ms[i]->s = st;
+                } else if (g53h_tile_i4(lv, ms[i]->w, ms[i]->rows, ms[i]->cols, 1)) {
+                    g53_die("converting an int4 expert view");
+                }
+                ms[i]->w = lv;
+                ms[i]->flags = G53H_MAT_I4;
             }
         }
     }
@@ -886,7 +915,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
             L.block_c = 0;
     }
     G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
-    if (tiled || one_i4t) {
+    if (tiled || one_i4t || one_i4m) {
         /* compact table: slot j holds the j-th chosen expert (the kernel is told indices 0 .. K-1),
          * slot K the shared expert */
         int *ident = (int *)buf_get(&g_ident, GLM53F_MAX_TOPK * sizeof(int));
@@ -899,7 +928,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         }
         if (g53h_h2d_async(tab_d, tab, (size_t)(K + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
         L.n_experts = K; L.experts = tab_d; L.shared = with_shared ? tab_d + K : NULL;
-        L.tiled = one_i4t ? 3 : 1;
+        L.tiled = one_i4m ? 4 : one_i4t ? 3 : 1;
         L.block_c = 128;
         if (g53h_moe_routed_given(od, xd, 1, &L, ident, w_d)) g53_die("glm53f_moe");
     } else {
@@ -954,9 +983,17 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off, int tile
     uint8_t *s = dst + *off;
     *off += (sb + 255) & ~(size_t)255;
     const int is_t = m->dt == GLM53F_WF8T;
+    int steps_done = 0;
     if (m->dt == GLM53F_WI4T) {                                /* int4 levels back to rows */
         uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
         if (g53h_h2d(t, m->w, cb) || g53h_tile_i4(w, t, m->rows, m->cols, 1)) g53_die("copying a host expert to HBM");
+    } else if (m->dt == GLM53F_WI4M) {                         /* levels and steps back to rows */
+        uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, ((cb + 255) & ~(size_t)255) + sb);
+        float *ts = (float *)(t + ((cb + 255) & ~(size_t)255));
+        if (g53h_h2d(t, m->w, cb) || g53h_h2d(ts, m->s, sb) ||
+            g53h_mtile_i4(w, (float *)s, t, ts, m->rows, m->cols, 1))
+            g53_die("copying a host expert to HBM");
+        steps_done = 1;
     } else if (m->dt != GLM53F_WI4 && is_t != (tiled != 0)) {  /* convert on the way in */
         uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
         if (g53h_h2d(t, m->w, cb) ||
@@ -965,7 +1002,7 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off, int tile
     } else if (g53h_h2d(w, m->w, cb)) {
         g53_die("copying a host expert to HBM");
     }
-    if (g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
+    if (!steps_done && g53h_h2d(s, m->s, sb)) g53_die("copying a host expert to HBM");
     d.w = w; d.s = (const float *)s;
     d.rows = m->rows; d.cols = m->cols; d.br = m->br; d.bc = m->bc; d.scols = m->scols;
     d.flags = mat_i4(m) ? G53H_MAT_I4 : (tiled ? G53H_MAT_TILED : 0);
@@ -989,6 +1026,17 @@ static size_t expert_stage_bytes(const Glm53fExpertQ *q)
 static G53hMat chunk_view(const Glm53fMat *m, uint8_t *dst, size_t *off, int tiled)
 {
     G53hMat d = view_mat_f8(m);
+    if (m->dt == GLM53F_WI4M) {                   /* levels and steps untiled into the slot */
+        uint8_t *w = dst + *off;
+        *off += (mat_code_bytes(m) + 255) & ~(size_t)255;
+        float *st = (float *)(dst + *off);
+        *off += (mat_scale_bytes(m) + 255) & ~(size_t)255;
+        if (g53h_mtile_i4(w, st, (const uint8_t *)m->w, m->s, m->rows, m->cols, 1))
+            g53_die("converting an int4 expert view");
+        d.w = w; d.s = st;
+        d.flags = G53H_MAT_I4;
+        return d;
+    }
     if (m->dt == GLM53F_WI4T) {
         uint8_t *w = dst + *off;
         *off += (mat_code_bytes(m) + 255) & ~(size_t)255;
@@ -1142,7 +1190,8 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                     const int conv = (!mat_i4(&q.gate) && (q.gate.dt == GLM53F_WF8T) != tl) ||
                                      (!mat_i4(&q.up) && (q.up.dt == GLM53F_WF8T) != tl) ||
                                      (!mat_i4(&q.down) && (q.down.dt == GLM53F_WF8T) != tl) ||
-                                     q.gate.dt == GLM53F_WI4T || q.up.dt == GLM53F_WI4T || q.down.dt == GLM53F_WI4T;
+                                     q.gate.dt == GLM53F_WI4T || q.up.dt == GLM53F_WI4T || q.down.dt == GLM53F_WI4T ||
+                                     q.gate.dt == GLM53F_WI4M || q.up.dt == GLM53F_WI4M || q.down.dt == GLM53F_WI4M;
                     uint8_t *dst = conv ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
                     held[nh++] = e;                      /* released once its kernels are queued */
                     table[e].gate = chunk_view(&q.gate, dst, &off, tl);

@@ -19,6 +19,7 @@ import glm53h.synth as S
 import oracle_lib as O
 from glm53h import DevBuf, G53hMat, check
 from test_gpu_cache import N_MOE_LAYERS, Layers, PyStore, make_cfg
+from test_gpu_grouped import within
 from test_gpu_parity import cfg_struct, fmat, same, say
 
 pytestmark = pytest.mark.gpu
@@ -301,7 +302,9 @@ def test_cache_int4_mode_config2(L):
     """Released shapes (14,155,776-byte int4 slots): two layers, three tokens, through the int4
     cache, equal to host int4 views of the same experts quantised by the oracle; the same in int4
     mode 2 (the levels int4-tiled, the one-launch decode, speculative once every expert has
-    landed) and for a five-token chunk through the tiled slots."""
+    landed) and for a five-token chunk through the tiled slots. In int4 mode 3 (levels and steps
+    int4 MFMA-tiled, the FP4 matrix-core decode) the single-token outputs are within the path's
+    tolerance (1e-2 abs + 2e-3 rel) and the chunk, through untiled views, bit-exact."""
     sp = S.spec(2)
     NP = 12
     cf = make_cfg(sp)
@@ -356,21 +359,28 @@ def test_cache_int4_mode_config2(L):
         # int4 mode 2: the same slot size with the levels int4-tiled; single-token layers in one
         # launch (speculative once every expert has landed), chunks through untiled levels
         wantT = run(PoolI4(cf, {}).src, 0, T=5)
-        for slots, n_io in [(12, 2), (600, 0)]:
-            say("config 2 int4-tiled cache, slots", slots)
-            c, sb = new_cache_i4(cf, st, slots, n_io, mode=2)
+
+        def same_or_within(got, what, mode):
+            if mode == 2:
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), what
+            else:
+                within(got, want, what)
+
+        for mode, slots, n_io in [(2, 12, 2), (2, 600, 0), (3, 12, 2), (3, 600, 0)]:
+            say("config 2 int4 cache, mode", mode, "slots", slots)
+            c, sb = new_cache_i4(cf, st, slots, n_io, mode=mode)
             try:
-                assert sb == ref_i4_slot_bytes(sp) and L.g53h_cache_slot_kind(C.byref(c.src)) == 3
+                assert sb == ref_i4_slot_bytes(sp) and L.g53h_cache_slot_kind(C.byref(c.src)) == mode + 1
                 n = (C.c_int64 * 3)()
                 L.g53h_speculate_counts(n)
                 got = run(c.src, 6 if n_io else 0)
                 check(L.glm53f_cache_sync(C.byref(c)), "sync")
-                assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+                same_or_within(got, f"mode {mode} slots {slots}", mode)
                 if slots > 300:                      # every expert resident: the second pass speculates
                     L.g53h_set_speculate(1)
                     again = run(c.src, 0)
                     L.g53h_speculate_counts(n)
-                    assert np.array_equal(again.view(np.uint32), want.view(np.uint32))
+                    same_or_within(again, f"mode {mode} speculative", mode)
                     assert n[0] >= 6, list(n)
                 gotT = run(c.src, 0, T=5)
                 assert np.array_equal(gotT.view(np.uint32), wantT.view(np.uint32))
