@@ -473,7 +473,9 @@ def bench_stack(a):
     budget = 200 * 10 ** 9
     # --experts int4: the reference's int4 mode, in the cache's int4-tiled slots (mode 2): the
     # experts are re-quantised as they are read, and a decode layer is one launch
-    i4mode = 2 if a.experts == "int4" else 0
+    # int4: the cache's mode 3 (int4 MFMA-tiled slots, the FP4 matrix-core decode) under the default
+    # --layout mfma, mode 2 (int4-tiled slots, bit-exact) under --layout tiled
+    i4mode = (3 if a.layout == "mfma" else 2) if a.experts == "int4" else 0
     if L.g53h_cache_init_store(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io, i4mode) != 0:
         sys.exit("glm53f_cache_init failed")
     specs = [S.spec(3, layer=l) for l in range(NL)]
@@ -598,8 +600,9 @@ def bench_stack(a):
                                f", {steps} steps, HBM expert cache of 200 GB, the rest in pinned host memory, "
                                "next-layer prefetch",
                    "layers": NL, "slots": nslot,
-                   "routed_experts": ("int4 (the reference's int4 mode, re-quantised as read; int4-tiled slots)"
-                                      if i4mode else "fp8"),
+                   "routed_experts": (("int4 (the reference's int4 mode, re-quantised as read; " +
+                                       ("int4 MFMA-tiled slots, FP4 matrix cores, within the tolerance)" if i4mode == 3
+                                        else "int4-tiled slots, bit-exact)")) if i4mode else "fp8"),
                    "prefetch_n": pf, "prefetch_reads_in_flight": n_io, "input_correlation": rho,
                    "parallelism": "single GPU"},
         "routing": routing,
@@ -654,7 +657,8 @@ def main():
                          "int4 MFMA-tiled experts (--layout mfma, within the tolerance), one launch over int4-tiled "
                          "slots (--layout tiled, bit-exact), or with --layout rowmajor the five-launch row-wave "
                          "kernels; config 5: the cache's int4 "
-                         "mode with int4-tiled slots (200 GB then holds every expert of 42 layers)")
+                         "mode 3 with int4 MFMA-tiled slots (--layout tiled: mode 2, int4-tiled slots, bit-exact); "
+                         "200 GB then holds every expert of 42 layers")
     a = ap.parse_args()
     if a.gpus != 1:
         sys.exit("bench.py measures one GPU: this build has no multi-GPU path (expert-parallel "
