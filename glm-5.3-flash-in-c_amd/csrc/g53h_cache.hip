@@ -75,6 +75,7 @@ struct Impl {
     /* octet-tiled slots (G53H_MAT_TILED): a matrix's codes land in the stream's staging buffer and
      * are tiled into the slot by a kernel on the same stream, so one buffer per stream suffices */
     bool tiled = false;
+    bool mt = false;                /* with tiled: FP8 slots MFMA-tiled (GLM53F_CACHE_MFMA)  */
     bool i4 = false;                /* int4 slots: FP8 staged, quantised into the slot      */
     bool i4t = false;               /* int4 mode 2: the levels quantised into staging, then
                                        int4-tiled into the slot (the steps straight in)     */
@@ -176,7 +177,8 @@ void table_set(Glm53fCache *c, Impl *m, int slot, int layer, int expert)
         d[i]->w = (const uint8_t *)v[i]->w; d[i]->s = v[i]->s;
         d[i]->rows = v[i]->rows; d[i]->cols = v[i]->cols; d[i]->br = v[i]->br; d[i]->bc = v[i]->bc;
         d[i]->scols = v[i]->scols;
-        d[i]->flags = m->i4t ? (G53H_MAT_I4 | G53H_MAT_I4T) : m->i4m ? (G53H_MAT_I4 | G53H_MAT_MTILED) : G53H_MAT_TILED;
+        d[i]->flags = m->i4t ? (G53H_MAT_I4 | G53H_MAT_I4T) : m->i4m ? (G53H_MAT_I4 | G53H_MAT_MTILED)
+                      : m->mt ? G53H_MAT_MTILED : G53H_MAT_TILED;
     }
     m->tab_key[slot] = key;
     m->tab_dirty[layer] = 1;
@@ -284,7 +286,8 @@ int issue_reads(Glm53fCache *c, Impl *m, int slot, int layer, int expert, hipStr
     for (int i = 0; !m->i4 && i < 3; i++) {
         if (m->tiled) {
             if (hipMemcpyAsync(stage, mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) != hipSuccess ||
-                g53h_tile_f8_on(base + m->geo.off[i], stage, m->geo.rows[i], m->geo.cols[i], s))
+                (m->mt ? g53h_mtile_f8_on(base + m->geo.off[i], stage, m->geo.rows[i], m->geo.cols[i], 0, s)
+                       : g53h_tile_f8_on(base + m->geo.off[i], stage, m->geo.rows[i], m->geo.cols[i], s)))
                 return 0;
         } else if (hipMemcpyAsync(base + m->geo.off[i], mats[i]->w, m->geo.bytes[i], hipMemcpyHostToDevice, s) !=
                    hipSuccess) {
@@ -323,7 +326,8 @@ void view_of(const Glm53fCache *c, const Impl *m, int slot, Glm53fExpertQ *q)
         Glm53fMat &v = *mats[i];
         v.w = base + m->geo.off[i];
         v.s = (const float *)(base + m->geo.off[3 + i]);
-        v.dt = m->i4 ? (m->i4t ? GLM53F_WI4T : m->i4m ? GLM53F_WI4M : GLM53F_WI4) : (m->tiled ? GLM53F_WF8T : GLM53F_WF8);
+        v.dt = m->i4 ? (m->i4t ? GLM53F_WI4T : m->i4m ? GLM53F_WI4M : GLM53F_WI4)
+                     : (m->tiled ? (m->mt ? GLM53F_WF8M : GLM53F_WF8T) : GLM53F_WF8);
         v.rows = m->geo.rows[i]; v.cols = m->geo.cols[i];
         if (m->i4) {                                 /* glm53f_expert_i4_view's geometry */
             v.br = 1; v.bc = GLM53F_I4_GROUP; v.scols = m->geo.cols[i] / GLM53F_I4_GROUP;
@@ -477,7 +481,7 @@ extern "C" int g53h_cache_slot_kind(const Glm53fExpertSrc *src)
 {
     if (!g53h_cache_is(src)) return 0;
     const Impl *m = impl_of((const Glm53fCache *)src);
-    return !m ? 0 : m->tiled ? 1 : m->i4t ? 3 : m->i4m ? 4 : 0;
+    return !m ? 0 : m->tiled ? (m->mt ? 2 : 1) : m->i4t ? 3 : m->i4m ? 4 : 0;
 }
 
 extern "C" int g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **table_d,
@@ -576,6 +580,11 @@ static int cache_setup(Glm53fCache *c, Impl *m, const Glm53fCfg *cfg, int64_t bu
     m->i4t = m->i4 && i4 == 2 && m->tiled;
     m->i4m = m->i4 && i4 == 3 && m->tiled;      /* int4 mode 3: the same shapes, MFMA-tiled */
     if (m->i4) m->tiled = false;
+    /* FP8 slots MFMA-tiled (the FP8 matrix-core decode) at the same shapes, when asked */
+    {
+        const char *e = getenv("GLM53F_CACHE_MFMA");
+        m->mt = m->tiled && e && atoi(e) != 0;
+    }
     if (m->i4t) c->i4 = 2;
     if (m->i4m) c->i4 = 3;
     c->nslot = (int)(budget_bytes / c->slot_bytes);

@@ -48,7 +48,8 @@ class G53hMoeLayer(C.Structure):
 # -------------------------------------------------------------- structs (glm53f.h) ----
 GLM53F_MAX_LAYERS = 256
 GLM53F_MAX_EOS = 8
-GLM53F_WF32, GLM53F_WBF16, GLM53F_WF8, GLM53F_WI4, GLM53F_WF8T, GLM53F_WI4T, GLM53F_WI4M = 0, 1, 2, 3, 0x102, 0x103, 0x104
+GLM53F_WF32, GLM53F_WBF16, GLM53F_WF8, GLM53F_WI4, GLM53F_WF8T, GLM53F_WI4T, GLM53F_WI4M, GLM53F_WF8M = (
+    0, 1, 2, 3, 0x102, 0x103, 0x104, 0x105)
 
 
 class Glm53fCfg(C.Structure):

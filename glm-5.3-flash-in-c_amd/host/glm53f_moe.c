@@ -183,7 +183,7 @@ static size_t mat_scale_bytes(const Glm53fMat *m)
 }
 static int mat_flags(const Glm53fMat *m)
 {
-    return m->dt == GLM53F_WF8T ? G53H_MAT_TILED
+    return m->dt == GLM53F_WF8T ? G53H_MAT_TILED : m->dt == GLM53F_WF8M ? G53H_MAT_MTILED
            : m->dt == GLM53F_WI4 ? G53H_MAT_I4 : m->dt == GLM53F_WI4T ? (G53H_MAT_I4 | G53H_MAT_I4T)
            : m->dt == GLM53F_WI4M ? (G53H_MAT_I4 | G53H_MAT_MTILED) : 0;
 }
@@ -191,7 +191,7 @@ static int mat_flags(const Glm53fMat *m)
 static void check_f8(const Glm53fMat *m, const char *what)
 {
     if (!m->w) { fprintf(stderr, "glm53f: FATAL, multiply through an unbound matrix (%s)\n", what); abort(); }
-    if (m->dt != GLM53F_WF8 && m->dt != GLM53F_WF8T && !mat_i4(m)) {
+    if (m->dt != GLM53F_WF8 && m->dt != GLM53F_WF8T && m->dt != GLM53F_WF8M && !mat_i4(m)) {
         fprintf(stderr, "glm53f: FATAL, %s has storage type %d; the MI355X expert path multiplies "
                         "FP8 E4M3 and int4 (GLM53F_WI4) matrices only\n", what, m->dt);
         abort();
@@ -206,8 +206,8 @@ static void check_f8(const Glm53fMat *m, const char *what)
                 what, m->br, m->bc, m->scols, m->cols);
         abort();
     }
-    if (m->dt == GLM53F_WF8T && (m->rows % 8 || m->cols % 128)) {
-        fprintf(stderr, "glm53f: FATAL, %s is octet-tiled with %d rows and %d columns (rows a multiple of 8, "
+    if ((m->dt == GLM53F_WF8T || m->dt == GLM53F_WF8M) && (m->rows % 8 || m->cols % 128)) {
+        fprintf(stderr, "glm53f: FATAL, %s is tiled with %d rows and %d columns (rows a multiple of 8, "
                         "columns of 128)\n", what, m->rows, m->cols);
         abort();
     }
@@ -216,8 +216,8 @@ static void check_f8(const Glm53fMat *m, const char *what)
 static void check_rowmajor(const Glm53fMat *m, const char *what)
 {
     check_f8(m, what);
-    if (m->dt == GLM53F_WF8T) {
-        fprintf(stderr, "glm53f: FATAL, %s is octet-tiled; layer weights are bound row-major (GLM53F_WF8)\n", what);
+    if (m->dt == GLM53F_WF8T || m->dt == GLM53F_WF8M) {
+        fprintf(stderr, "glm53f: FATAL, %s is tiled; layer weights are bound row-major (GLM53F_WF8)\n", what);
         abort();
     }
 }
@@ -325,9 +325,9 @@ static G53Buf g_mat[3];
 static G53hMat dev_mat_staged(const Glm53fMat *m, G53Buf *b, const char *what)
 {
     check_f8(m, what);
-    if (m->dt == GLM53F_WI4T || m->dt == GLM53F_WI4M) {
-        fprintf(stderr, "glm53f: FATAL, %s is an int4-tiled cache view (GLM53F_WI4T / GLM53F_WI4M); only "
-                        "glm53f_moe reads those\n", what);
+    if (m->dt == GLM53F_WI4T || m->dt == GLM53F_WI4M || m->dt == GLM53F_WF8M) {
+        fprintf(stderr, "glm53f: FATAL, %s is a tiled cache view (GLM53F_WI4T / GLM53F_WI4M / GLM53F_WF8M); "
+                        "only glm53f_moe reads those\n", what);
         abort();
     }
     const int dev = g53h_is_device_ptr(m->w);
@@ -756,7 +756,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
      * below on the experts the gets returned. No cache call happens while the kernel runs, so
      * no slot it reads is refilled under it. */
     const G53hExpert *stab_d = NULL, *stab_h = NULL;
-    /* 1 octet-tiled FP8 slots, 3 int4-tiled, 4 int4 MFMA-tiled */
+    /* 1 octet-tiled FP8 slots, 2 MFMA-tiled FP8, 3 int4-tiled, 4 int4 MFMA-tiled */
     const int kind = g53h_cache_slot_kind(src);
     int spec = spec_enabled() && spec_worth() && dt == 1 && K <= 15 && NE <= 1024 && E == 4096 && c->moe_inter == 2048 &&
                G53_MB_OUT_OFF + 4 * G53H_NERR + ob <= G53H_MBOX_BYTES &&
@@ -768,9 +768,9 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         memset(&SL, 0, sizeof SL);
         SL.hidden = E; SL.inter = c->moe_inter; SL.topk = K; SL.norm_topk = c->norm_topk;
         SL.routed_scale = c->routed_scale; SL.swiglu_limit = c->swiglu_limit;
-        SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = kind == 3 || kind == 4 ? kind : 1;
+        SL.router = gate; SL.router_dt = dt; SL.bias = bias; SL.block_c = 128; SL.tiled = kind >= 2 && kind <= 4 ? kind : 1;
         SL.n_experts = NE; SL.experts = stab_d;
-        SL.shared = with_shared ? shared_desc(w, kind == 4) : NULL;
+        SL.shared = with_shared ? shared_desc(w, kind == 2 || kind == 4) : NULL;
         HP(7);
         if (x_host) upload_x(xd, x, E);
         if (per > 0 && g53h_decode_next(xd, ngate, ndt, nbias, NE, E)) g53_die("glm53f_router");
@@ -818,7 +818,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     HP(2);
     /* the chosen experts' views (slot order), the shared expert after them */
     G53hExpert *tab = (G53hExpert *)pinned(&g_pin_tab, &g_pin_tab_n, (size_t)(NE + 1) * sizeof(G53hExpert));
-    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1, i4r = 1, i4t = 1, i4m = 1;
+    int held[GLM53F_MAX_TOPK], nh = 0, tiled = 1, mt = 1, i4r = 1, i4t = 1, i4m = 1;
     memset(tab, 0, (size_t)(K + 1) * sizeof(G53hExpert));
     for (int j = 0; j < K; j++) {
         Glm53fExpertQ q;
@@ -837,13 +837,16 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         tab[j].up = view_mat_f8(&q.up);
         tab[j].down = view_mat_f8(&q.down);
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_TILED)) tiled = 0;
+        if (((tab[j].gate.flags | tab[j].up.flags | tab[j].down.flags) & G53H_MAT_I4) ||
+            !(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_MTILED))
+            mt = 0;
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4)) i4r = 0;
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4T)) i4t = 0;
         if (!(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_I4) ||
             !(tab[j].gate.flags & tab[j].up.flags & tab[j].down.flags & G53H_MAT_MTILED))
             i4m = 0;
     }
-    if (!nh) i4r = i4t = i4m = 0;
+    if (!nh) i4r = i4t = i4m = mt = 0;
     HP(3);
     if (spec) {                  /* every chosen expert was in the kernel's table: the output is done */
         g_spec_n[0]++;
@@ -858,16 +861,17 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
     if (with_shared) {
         /* the shared expert resident in the layout of the routed slots */
         /* (int4 routed experts: the row-wave kernel's fast FP8 path reads it octet-tiled too) */
-        const int tile_ok = (tiled || i4r) && shared_tileable(w);
-        if (tile_ok) {           /* MFMA-tiled beside int4 MFMA-tiled views, else octet-tiled */
-            tab[K].gate = dev_mat_resident_tiled_as(&w->sh_gate, "shared gate", i4m);
-            tab[K].up = dev_mat_resident_tiled_as(&w->sh_up, "shared up", i4m);
-            tab[K].down = dev_mat_resident_tiled_as(&w->sh_down, "shared down", i4m);
+        const int tile_ok = (tiled || mt || i4r) && shared_tileable(w);
+        if (tile_ok) {           /* MFMA-tiled beside MFMA-tiled views, else octet-tiled */
+            tab[K].gate = dev_mat_resident_tiled_as(&w->sh_gate, "shared gate", i4m || mt);
+            tab[K].up = dev_mat_resident_tiled_as(&w->sh_up, "shared up", i4m || mt);
+            tab[K].down = dev_mat_resident_tiled_as(&w->sh_down, "shared down", i4m || mt);
         } else {
             tab[K].gate = dev_mat_resident(&w->sh_gate, "shared gate");
             tab[K].up = dev_mat_resident(&w->sh_up, "shared up");
             tab[K].down = dev_mat_resident(&w->sh_down, "shared down");
             tiled = 0;
+            mt = 0;
         }
         if (i4r) tiled = 0;
     }
@@ -875,6 +879,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
      * absent); else their levels untiled for the row kernels */
     const int one_i4t = i4t && (!with_shared || (tab[K].gate.flags & G53H_MAT_TILED));
     const int one_i4m = i4m && (!with_shared || (tab[K].gate.flags & G53H_MAT_MTILED));
+    const int one_mt = mt && (!with_shared || (tab[K].gate.flags & G53H_MAT_MTILED));
     if ((i4t && !one_i4t) || (i4m && !one_i4m)) {
         /* the row kernels read row-major levels (and steps) */
         static G53Buf g_i4u[GLM53F_MAX_TOPK];
@@ -915,7 +920,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
             L.block_c = 0;
     }
     G53hExpert *tab_d = (G53hExpert *)buf_get(&g_table, (size_t)(NE + 1) * sizeof(G53hExpert));
-    if (tiled || one_i4t || one_i4m) {
+    if (tiled || one_mt || one_i4t || one_i4m) {
         /* compact table: slot j holds the j-th chosen expert (the kernel is told indices 0 .. K-1),
          * slot K the shared expert */
         int *ident = (int *)buf_get(&g_ident, GLM53F_MAX_TOPK * sizeof(int));
@@ -928,7 +933,7 @@ static void decode_cached(float *out, const float *x, const Glm53fMoeW *w, const
         }
         if (g53h_h2d_async(tab_d, tab, (size_t)(K + 1) * sizeof(G53hExpert))) g53_die("glm53f_moe");
         L.n_experts = K; L.experts = tab_d; L.shared = with_shared ? tab_d + K : NULL;
-        L.tiled = one_i4m ? 4 : one_i4t ? 3 : 1;
+        L.tiled = one_i4m ? 4 : one_i4t ? 3 : one_mt ? 2 : 1;
         L.block_c = 128;
         if (g53h_moe_routed_given(od, xd, 1, &L, ident, w_d)) g53_die("glm53f_moe");
     } else {
@@ -994,6 +999,12 @@ static G53hMat stage_mat(const Glm53fMat *m, uint8_t *dst, size_t *off, int tile
             g53h_mtile_i4(w, (float *)s, t, ts, m->rows, m->cols, 1))
             g53_die("copying a host expert to HBM");
         steps_done = 1;
+    } else if (m->dt == GLM53F_WF8M) {        /* MFMA-tiled: back to rows, octet-tiled if asked */
+        uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, 2 * cb);
+        if (g53h_h2d(t, m->w, cb) ||
+            (tiled ? (g53h_mtile_f8(t + cb, t, m->rows, m->cols, 1) || g53h_tile_f8(w, t + cb, m->rows, m->cols))
+                   : g53h_mtile_f8(w, t, m->rows, m->cols, 1)))
+            g53_die("copying a host expert to HBM");
     } else if (m->dt != GLM53F_WI4 && is_t != (tiled != 0)) {  /* convert on the way in */
         uint8_t *t = (uint8_t *)buf_get(&g_tile_stage, cb);
         if (g53h_h2d(t, m->w, cb) ||
@@ -1043,6 +1054,18 @@ static G53hMat chunk_view(const Glm53fMat *m, uint8_t *dst, size_t *off, int til
         if (g53h_tile_i4(w, (const uint8_t *)m->w, m->rows, m->cols, 1)) g53_die("converting an int4 expert view");
         d.w = w;
         d.flags = G53H_MAT_I4;
+        return d;
+    }
+    if (m->dt == GLM53F_WF8M) {                   /* MFMA-tiled: back to rows, octet-tiled if asked */
+        uint8_t *w = dst + *off;
+        const size_t cb = mat_code_bytes(m);
+        *off += (cb + 255) & ~(size_t)255;
+        uint8_t *t = tiled ? (uint8_t *)buf_get(&g_tile_stage, cb) : w;
+        if (g53h_mtile_f8(t, (const uint8_t *)m->w, m->rows, m->cols, 1) ||
+            (tiled && g53h_tile_f8(w, t, m->rows, m->cols)))
+            g53_die("converting an expert view");
+        d.w = w;
+        d.flags = tiled ? G53H_MAT_TILED : 0;
         return d;
     }
     const int is_t = m->dt == GLM53F_WF8T;
@@ -1191,7 +1214,8 @@ static void moe_chunk(float *out, const float *x, const Glm53fMoeW *w, const Glm
                                      (!mat_i4(&q.up) && (q.up.dt == GLM53F_WF8T) != tl) ||
                                      (!mat_i4(&q.down) && (q.down.dt == GLM53F_WF8T) != tl) ||
                                      q.gate.dt == GLM53F_WI4T || q.up.dt == GLM53F_WI4T || q.down.dt == GLM53F_WI4T ||
-                                     q.gate.dt == GLM53F_WI4M || q.up.dt == GLM53F_WI4M || q.down.dt == GLM53F_WI4M;
+                                     q.gate.dt == GLM53F_WI4M || q.up.dt == GLM53F_WI4M || q.down.dt == GLM53F_WI4M ||
+                                     q.gate.dt == GLM53F_WF8M || q.up.dt == GLM53F_WF8M || q.down.dt == GLM53F_WF8M;
                     uint8_t *dst = conv ? (uint8_t *)buf_get(&g_hslots[u - b0].b, need) : NULL;
                     held[nh++] = e;                      /* released once its kernels are queued */
                     table[e].gate = chunk_view(&q.gate, dst, &off, tl);

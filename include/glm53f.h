@@ -99,9 +99,11 @@ typedef struct {
  * one. GLM53F_WI4T, also this library's own: the int4 views of its cache in int4 mode 2 (the
  * levels int4-tiled, G53H_MAT_I4T of g53h.h; the steps as GLM53F_WI4's). GLM53F_WI4M, also
  * this library's own: the int4 views of its cache in int4 mode 3 (levels and steps int4
- * MFMA-tiled, G53H_MAT_I4 | G53H_MAT_MTILED of g53h.h, the layout of the FP4 matrix-core decode). */
+ * MFMA-tiled, G53H_MAT_I4 | G53H_MAT_MTILED of g53h.h, the layout of the FP4 matrix-core decode).
+ * GLM53F_WF8M, also this library's own: the FP8 views of its cache with GLM53F_CACHE_MFMA set
+ * (E4M3 codes MFMA-tiled, G53H_MAT_MTILED, the layout of the FP8 matrix-core decode). */
 enum { GLM53F_WF32 = 0, GLM53F_WBF16 = 1, GLM53F_WF8 = 2, GLM53F_WI4 = 3, GLM53F_WF8T = 0x102, GLM53F_WI4T = 0x103,
-       GLM53F_WI4M = 0x104 };
+       GLM53F_WI4M = 0x104, GLM53F_WF8M = 0x105 };
 
 /* Group size of the GLM53F_WI4 matrices the reference's engine produces
  * (include/glm53f/glm53f.h:124-125). */

@@ -124,7 +124,10 @@ typedef struct {
  * the drop-in decodes a token in one launch; its chunked paths untile the views they read. At
  * other shapes i4 = 2 is i4 = 1. i4 = 3, also this library's own, is i4 = 2 with levels and
  * steps int4 MFMA-tiled (GLM53F_WI4M views): the drop-in then decodes a token in one launch on
- * the FP4 matrix cores, within the path's tolerance instead of bit for bit. */
+ * the FP4 matrix cores, within the path's tolerance instead of bit for bit. With the environment
+ * variable GLM53F_CACHE_MFMA set to a non-zero number at init, FP8 slots at those shapes are
+ * MFMA-tiled (GLM53F_WF8M views) and the drop-in decodes on the FP8 matrix cores, within the
+ * tolerance. */
 int  glm53f_cache_init(Glm53fCache *c, const Glm53fSt *st, const Glm53fCfg *cfg, int64_t budget_bytes,
                        int n_io, int i4);
 void glm53f_cache_free(Glm53fCache *c);
@@ -157,12 +160,12 @@ int  g53h_cache_is(const Glm53fExpertSrc *src);
  * gate.w NULL where the expert holds no landed slot) on the compute stream's timeline, and table_h its host copy. It is current as
  * of this call; any later cache call may evict or fill slots, so a kernel that reads it must
  * complete before the next cache call. Returns 0, a positive count of this layer's reads still
- * in flight (no table then), or -1 when src is not a cache with tiled slots (kind 1, 3 or 4). */
+ * in flight (no table then), or -1 when src is not a cache with tiled slots (kind 1 to 4). */
 int  g53h_cache_layer_table(Glm53fExpertSrc *src, int layer, const G53hExpert **table_d,
                             const G53hExpert **table_h);
-/* The kind of slots a cache holds (no counterpart in the reference): 1 octet-tiled FP8, 3
- * int4-tiled (int4 mode 2), 4 int4 MFMA-tiled (int4 mode 3), 0 otherwise (row-major FP8 or
- * int4, or src not a cache). */
+/* The kind of slots a cache holds (no counterpart in the reference): 1 octet-tiled FP8, 2
+ * MFMA-tiled FP8 (GLM53F_CACHE_MFMA set at its init), 3 int4-tiled (int4 mode 2), 4 int4
+ * MFMA-tiled (int4 mode 3), 0 otherwise (row-major FP8 or int4, or src not a cache). */
 int  g53h_cache_slot_kind(const Glm53fExpertSrc *src);
 /* The drop-in's speculative cached decode (no counterpart in the reference): with a cache of
  * octet-tiled slots, glm53f_moe at T = 1 runs the one-launch decode over the layer's table

@@ -9,8 +9,12 @@ oracle's bit for bit, and equals the one from a cache large enough to never evic
 prefetch (the cache decides what is resident when, never what a layer returns). The same run
 with the drop-in's speculative layer turned off (route, fetch, then compute) returns the same
 outputs (what the cache reads ahead, and when, depends on when copies are seen complete, in
-the reference as here, so its counts may differ)."""
+the reference as here, so its counts may differ). With GLM53F_CACHE_MFMA set, the slots hold the
+codes MFMA-tiled and the drop-in decodes on the FP8 matrix cores: the same stack's outputs are
+within the path's tolerance (1e-2 abs + 2e-3 rel) of the bit-exact ones, speculative once every
+expert is resident, and a three-token chunk through those slots is within it of the oracle."""
 import ctypes as C
+import os
 
 import numpy as np
 import pytest
@@ -19,6 +23,7 @@ import glm53h
 import glm53h.synth as S
 import oracle_lib as O
 from glm53h import check, zipf
+from test_gpu_grouped import within
 from test_gpu_parity import cfg_struct, fmat, same, say
 
 pytestmark = pytest.mark.gpu
@@ -55,7 +60,17 @@ def test_stack_through_cache_with_misses(L):
           "store")
     check(L.g53h_store_synth_key_scales(C.byref(store)), "key scales")
 
-    def run(slots, n_io, pf, passes=1):
+    def shared_w(l, pf=0):
+        w = glm53h.Glm53fMoeW()
+        w.gate, w.bias = W[l].ctypes.data, B[l].ctypes.data
+        (gw, gs), (uw, us), (dw, ds) = sh
+        w.sh_gate = fmat(gw, gs, sp.I, sp.E, sp.br, sp.bc)
+        w.sh_up = fmat(uw, us, sp.I, sp.E, sp.br, sp.bc)
+        w.sh_down = fmat(dw, ds, sp.E, sp.I, sp.br, sp.bc)
+        w.layer, w.prefetch_n = l, pf
+        return w
+
+    def run(slots, n_io, pf, passes=1, chunk=0):
         cache = glm53h.Glm53fCache()
         probe = glm53h.Glm53fCache()
         assert L.g53h_cache_init_store(C.byref(probe), C.byref(store), C.byref(cf), 1 << 30, 0, 0) == 0
@@ -89,11 +104,19 @@ def test_stack_through_cache_with_misses(L):
                 if k:           # a fresh record of outcomes: the cold pass's misses no longer count
                     L.g53h_set_speculate(1)
                 runs.append(one_pass())
-            stats = dict(hits=cache.hits, misses=cache.misses, evictions=cache.evictions, bg_reads=cache.bg_reads,
+            if chunk:           # a chunk of tokens on layer 0 through the same slots
+                w = shared_w(0)
+                w.src = C.pointer(cache.src)
+                o = np.zeros((chunk, sp.E), np.float32)
+                xt = np.ascontiguousarray(X[:chunk, 0])
+                L.glm53f_moe(o.ctypes.data, xt.ctypes.data, C.byref(w), C.byref(cf), chunk, None)
+                check(L.glm53f_cache_sync(C.byref(cache)), "sync")
+                runs.append(o)
+            stats = dict(kind=L.g53h_cache_slot_kind(C.byref(cache.src)), hits=cache.hits, misses=cache.misses, evictions=cache.evictions, bg_reads=cache.bg_reads,
                          bg_used=cache.bg_used, bytes=cache.bytes_read + cache.bg_bytes)
         finally:
             L.glm53f_cache_free(C.byref(cache))
-        return (runs if passes > 1 else runs[0]), stats
+        return (runs if passes > 1 or chunk else runs[0]), stats
 
     def counts():
         n = (C.c_int64 * 3)()
@@ -151,6 +174,27 @@ def test_stack_through_cache_with_misses(L):
         say("oracle: all", STEPS * NL, "outputs equal;", len(distinct), "distinct (layer, expert) keys used")
         # no two keys share a first gate scale, so no two payloads are alike
         assert len({d[2] for d in distinct}) == len(distinct)
+        assert st["kind"] == 1
+        # the same stack through MFMA-tiled FP8 slots: the FP8 matrix-core decode
+        os.environ["GLM53F_CACHE_MFMA"] = "1"
+        try:
+            say("stack: MFMA-tiled slots, 40 slots, prefetch 4 in flight, prefetch_n 6")
+            gotm, stm = run(40, 4, 6)
+            assert stm["kind"] == 2 and stm["misses"] > 0
+            within(gotm.reshape(-1, sp.E), want.reshape(-1, sp.E), "MFMA-tiled cache with misses")
+            say("stack: MFMA-tiled slots, 300 slots, the same tokens twice, then a 3-token chunk")
+            counts()
+            (m1, m2, mc), stm2 = run(300, 0, 0, passes=2, chunk=3)
+            sc3 = counts()
+            say("layers speculative done / again / not", sc3)
+            assert sc3[0] >= STEPS * NL
+            within(m2.reshape(-1, sp.E), want.reshape(-1, sp.E), "MFMA-tiled cache, speculative")
+            idx, _ = O.router(O.oracle(), X[:3, 0], sps[0], W[0], B[0])
+            mats = {int(e): key_mats(0, int(e)) for e in np.unique(idx)}
+            o, oi, _ = O.moe(O.oracle(), X[:3, 0], sps[0], W[0], B[0], mats, sh)
+            within(mc, o, "3-token chunk through MFMA-tiled slots")
+        finally:
+            del os.environ["GLM53F_CACHE_MFMA"]
     finally:
         L.g53h_store_synth_free(C.byref(store))
         L.glm53f_forget_host_weights()
