@@ -471,11 +471,17 @@ def bench_stack(a):
     check(L.g53h_store_synth_init(C.byref(st), E, I, NL + 1, NE, NE, base.seed, C.c_float(base.expert_sigma)), "store")
     cache = glm53h.Glm53fCache()
     budget = 200 * 10 ** 9
-    # --experts int4: the reference's int4 mode, in the cache's int4-tiled slots (mode 2): the
-    # experts are re-quantised as they are read, and a decode layer is one launch
-    # int4: the cache's mode 3 (int4 MFMA-tiled slots, the FP4 matrix-core decode) under the default
+    # --experts int4: the reference's int4 mode, the experts re-quantised as they are read, a decode
+    # layer one launch. int4: the cache's mode 3 (int4 MFMA-tiled slots, the FP4 matrix-core decode) under the default
     # --layout mfma, mode 2 (int4-tiled slots, bit-exact) under --layout tiled
     i4mode = (3 if a.layout == "mfma" else 2) if a.experts == "int4" else 0
+    # FP8: MFMA-tiled slots (the FP8 matrix-core decode) under the default --layout mfma, octet-tiled
+    # ones (the bit-exact decode) under --layout tiled; the cache reads the switch at its init
+    mt = a.experts == "fp8" and a.layout == "mfma"
+    if mt:
+        os.environ["GLM53F_CACHE_MFMA"] = "1"
+    else:
+        os.environ.pop("GLM53F_CACHE_MFMA", None)
     if L.g53h_cache_init_store(C.byref(cache), C.byref(st), C.byref(cf), budget, n_io, i4mode) != 0:
         sys.exit("glm53f_cache_init failed")
     specs = [S.spec(3, layer=l) for l in range(NL)]
@@ -551,9 +557,10 @@ def bench_stack(a):
         spans, routed = [], []
         for l in range(NL):
             tb.zero()
-            L.g53h_set_tiled_decode_trace(tb.ptr)
+            set_trace = L.g53h_set_mfma_decode_trace if (mt or i4mode == 3) else L.g53h_set_tiled_decode_trace
+            set_trace(tb.ptr)
             fn(optr, xptr[warm + steps - 1][l], wref[l], cref, 1, None)
-            L.g53h_set_tiled_decode_trace(None)
+            set_trace(None)
             glm53h.sync()
             t = tb.download(np.uint64).reshape(-1, 192).astype(np.int64)
             t = t[t[:, 0] > 0]
@@ -602,7 +609,9 @@ def bench_stack(a):
                    "layers": NL, "slots": nslot,
                    "routed_experts": (("int4 (the reference's int4 mode, re-quantised as read; " +
                                        ("int4 MFMA-tiled slots, FP4 matrix cores, within the tolerance)" if i4mode == 3
-                                        else "int4-tiled slots, bit-exact)")) if i4mode else "fp8"),
+                                        else "int4-tiled slots, bit-exact)")) if i4mode else
+                                      "fp8 (MFMA-tiled slots, FP8 matrix cores, within the tolerance)" if mt else
+                                      "fp8 (octet-tiled slots, bit-exact)"),
                    "prefetch_n": pf, "prefetch_reads_in_flight": n_io, "input_correlation": rho,
                    "parallelism": "single GPU"},
         "routing": routing,
@@ -650,7 +659,8 @@ def main():
     ap.add_argument("--layout", default="mfma", choices=["mfma", "tiled", "rowmajor"],
                     help="config 2: expert code layout in HBM: MFMA-tiled (k_dec_mfma, FP8 matrix cores, outputs "
                          "within the path's tolerance), octet-tiled (the cache's slots; k_dec_tiled, bit-exact) or "
-                         "row-major (k_dec_layer, bit-exact); configs 3-4: tiled or rowmajor")
+                         "row-major (k_dec_layer, bit-exact); configs 3-4: tiled or rowmajor; config 5: the cache's "
+                         "slots MFMA-tiled (k_dec_mfma, within the tolerance) or octet-tiled (k_dec_tiled, bit-exact)")
     ap.add_argument("--experts", default="fp8", choices=["fp8", "int4"],
                     help="config 2: routed experts as the checkpoint's FP8 (the metric) or re-quantised to the "
                          "reference's int4 format (its --experts int4 mode): one launch on the FP4 matrix cores over "
