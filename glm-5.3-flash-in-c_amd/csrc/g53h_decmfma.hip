@@ -103,6 +103,9 @@ struct G53MfmaArgs {
     float routed_scale, limit;
     int spin;
     g53_u64 *trace;
+    const uint16_t *nrouter;       /* optional: the next layer's bf16 router [NE][E] and bias, */
+    const float *nbias;            /* whose scores (choice = score + bias) spare waves write */
+    float *nscore, *nchoice;       /* to nscore / nchoice [NE] (the prediction's input)      */
 };
 
 __device__ __forceinline__ bool g53_desc_mtiled(const G53hExpert &e)
@@ -315,9 +318,10 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
     const int do_lo = G53_DM_NDO * b / G, n_do = G53_DM_NDO * (b + 1) / G - do_lo;
     const int ng = 2 * n_go, nd = 2 * ((n_do + 1) >> 1), nslot = hs + K;
     const int nR = a.idx_in ? 0 : (a.NE > b ? (a.NE - 1 - b) / G + 1 : 0);
+    const int nN = a.nrouter ? (a.NE > b ? (a.NE - 1 - b) / G + 1 : 0) : 0;   /* next-layer rows */
     const int words = (int)(sizeof(G53hExpert) / 4);
     const bool dstage = a.NE * (int)sizeof(G53hExpert) <= G53_DM_DTAB;
-    const int n_setup = G53_DM_NW - 1 - nR;
+    const int n_setup = G53_DM_NW - 1 - nR - nN;
 
     G53_MTRACE(0);
     if (threadIdx.x == 0) { qctr = 0; ndone = 0; routed = 0; nrouted = 0; inited = 0; xready = 0; sready = 0; }
@@ -333,10 +337,24 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
         if (lane == 0) g53_st_tag(a.score + b + w * G, g53_tag(a.epoch, g53_sigmoidf_tab((float)d, g53_exp2_tab_dev)));
         if (w == 0) G53_MTRACE(2);
         __builtin_amdgcn_s_setprio(0);
+    } else if (w < nR + nN) {
+        /* the next layer's router row b + (w - nR) G on the same x: its score and choice for the
+         * prediction (the arithmetic of k_router_scores, bit for bit) */
+        const int e = b + (w - nR) * G;
+        g53_u4 cr[8];
+        g53_mgv4 *q = (g53_mgv4 *)(a.nrouter + (size_t)e * G53_DEC_E + lane * 64);
+#pragma unroll
+        for (int k = 0; k < 8; k++) cr[k] = q[k];
+        const double d = g53_router_row(cr, a.x, lane);
+        if (lane == 0) {
+            const float sc = g53_sigmoidf_tab((float)d, g53_exp2_tab_dev);
+            a.nscore[e] = sc;
+            a.nchoice[e] = sc + a.nbias[e];
+        }
     } else if (w < G53_DM_NW - 1) {
         /* the set-up: x as B-operand planes (thread t: group t of 32 values), the expert table,
          * the shared descriptor, the exponential's table */
-        const int ti = threadIdx.x - 64 * nR, nt = (G53_DM_NW - 1 - nR) * 64;
+        const int ti = threadIdx.x - 64 * (nR + nN), nt = (G53_DM_NW - 1 - nR - nN) * 64;
         /* the shared descriptor first: the first tasks (the shared expert's) need it to issue
          * their code loads, and may start as soon as it is in LDS */
         int dw = 0;
@@ -859,6 +877,18 @@ int g53h_decode_mtiled(float *out, const float *x, const G53hMoeLayer *L, int *i
     e.err = g53h_errblock() + 1; e.idx_out = idx_out; e.w_out = w_out; e.idx_in = idx_in; e.w_in = w_in;
     e.NE = L->n_experts; e.K = L->topk; e.norm_topk = L->norm_topk; e.epoch = g_dm_epoch;
     e.spin = g53h_spin_limit(); e.routed_scale = L->routed_scale; e.limit = L->swiglu_limit; e.trace = g_dm_trace;
+    e.nrouter = nullptr; e.nbias = nullptr; e.nscore = e.nchoice = nullptr;
+    G53NextReq *nq = g53h_next_req();
+    const int rows = (L->n_experts + g_dm_grid - 1) / g_dm_grid;
+    /* the next layer's scores by spare waves: a bf16 router on this x, and at least two set-up
+     * waves left (router rows + next rows + the routing wave + 2 <= the workgroup's waves) */
+    if (nq->armed && nq->dt == 1 && nq->x == x && nq->NE == L->n_experts && nq->E == G53_DEC_E &&
+        (idx_in ? 0 : rows) + rows + 3 <= G53_DM_NW) {
+        float *nb = g53h_next_buf();
+        if (!nb) return -1;
+        e.nrouter = (const uint16_t *)nq->gate; e.nbias = nq->bias; e.nchoice = nb; e.nscore = nb + 1024;
+        nq->armed = 0;
+    }
     g53h_prof_mark(G53_PROF_START);
     if (L->tiled == 4)                 /* int4 MFMA-tiled routed experts */
         hipLaunchKernelGGL(k_dec_mfma<true>, dim3(g_dm_grid), dim3(G53_DM_NT), 0, g53h_stream(), e);

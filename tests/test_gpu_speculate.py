@@ -6,8 +6,8 @@ mailbox (g53h_decode_publish).
 Bar: the routing and the output bit-exact against the C oracle (src/core/glm53f_ops.c:945-976,
 1329-1340); the prediction index for index against the oracle's route_topn
 (src/core/glm53f_ops.c:1021-1042). Both ways of computing the next scores are covered: by the
-octet-tiled decode kernel's spare waves, and by a launch of their own when the decode kernel
-is one that does not take the request (the MFMA-tiled one)."""
+spare waves of the one-launch decode kernels (octet-tiled and MFMA-tiled), and by a launch of
+their own when no decode launch took the request."""
 import ctypes as C
 
 import numpy as np
@@ -84,8 +84,8 @@ def test_next_scores_in_the_tiled_decode(L, tiled):
         assert np.array_equal(ids, wi[0]) and same(w, ww[0]) and same(out, want[0])
 
 
-def test_next_scores_by_their_own_launch(L):
-    """The MFMA-tiled decode does not take the request: the publish launch computes the scores."""
+def test_next_scores_in_the_mfma_decode(L):
+    """The MFMA-tiled decode's spare waves compute the requested scores."""
     sp = S.spec(2)
     say("building the config-2 layer, MFMA-tiled")
     m = S.DeviceLayer.build(sp, mfma=True)
@@ -121,3 +121,24 @@ def test_publish_without_prediction(L, tiled):
     assert L.g53h_decode_publish(SLOT, 991, ROUTE_OFF, idx.ptr, sp.K, pred.ptr, 4, sp.NE - 1, OUT_OFF, out.ptr,
                                  sp.E * 4) != 0
     glm53h.sync()
+
+
+def test_next_scores_by_their_own_launch(L, tiled):
+    """A request that no decode launch took: the publish launch computes the scores."""
+    sp = tiled.sp
+    Wn, bn = next_router(sp)
+    x = S.x_host(sp, 1, batch=8)
+    xd = DevBuf.from_array(np.ascontiguousarray(x[0]))
+    out, idx, w = DevBuf(sp.E * 4), DevBuf(sp.K * 4), DevBuf(sp.K * 4)
+    tiled.forward(out, xd, 1, idx, w)
+    gate = DevBuf.from_array((np.ascontiguousarray(Wn, np.float32).view(np.uint32) >> 16).astype(np.uint16))
+    bd = DevBuf.from_array(np.ascontiguousarray(bn, np.float32))
+    pred = DevBuf(6 * 4)
+    say("next scores armed after the decode: the publish launch computes them")
+    check(L.g53h_decode_next(xd.ptr, gate.ptr, 1, bd.ptr, sp.NE, sp.E), "g53h_decode_next")
+    check(L.g53h_decode_publish(SLOT, 995, ROUTE_OFF, idx.ptr, sp.K, pred.ptr, 6, sp.NE, OUT_OFF, out.ptr, sp.E * 4),
+          "g53h_decode_publish")
+    check(L.g53h_mailbox_wait(SLOT, 995), "mailbox wait")
+    r = mailbox_words(L, ROUTE_OFF, sp.K + 1 + 6, np.int32)
+    glm53h.sync()
+    assert np.array_equal(r[sp.K + 1:], topn_oracle(x, Wn, bn, 6)[0])
