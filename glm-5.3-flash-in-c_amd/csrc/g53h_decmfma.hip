@@ -652,31 +652,43 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
          * l / 8, group l / 2 % 4), re-read coherently until every tag is this launch's, then
          * writes them as B-operand planes into this wave's LDS */
         auto stage_act = [&]() {
-            const __amdgpu_buffer_rsrc_t rsl = g53_rsrc(a.act + (size_t)s * G53_DEC_I + 1024 * hd);
-            int spins = 0, nap = 1;
-            for (;;) {
-                g53_u64 tv[2];
-#pragma unroll
-                for (int k = 0; k < 2; k++) tv[k] = g53_ld_coh64(rsl, 8 * ((lane + 64 * k) * 8 + 7));
-                const int stale = ((unsigned)(tv[0] >> 32) != a.epoch) | ((unsigned)(tv[1] >> 32) != a.epoch);
-                if (!__ballot(stale)) break;
-                if (++spins > a.spin / 16 + 1) { if (lane == 0) g53_flag_err(a.err, 1); break; }
-                for (int qq = 0; qq < nap; qq++) __builtin_amdgcn_s_sleep(8);
-                if (nap < 8) nap *= 2;
-            }
             g53_u64 *act_s = a.act + (size_t)s * G53_DEC_I + 1024 * hd;
             const __amdgpu_buffer_rsrc_t rs = g53_rsrc(act_s);
             const int v0 = 16 * lane;
             g53_mgv4 *src = (g53_mgv4 *)(act_s + v0);
             float av[16];
             uint32_t pend = 0;
+            auto load_all = [&]() {
+                pend = 0;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const g53_u4 qv = src[k];
-                av[2 * k] = __uint_as_float(qv.x);
-                av[2 * k + 1] = __uint_as_float(qv.z);
-                if (qv.y != a.epoch) pend |= 1u << (2 * k);
-                if (qv.w != a.epoch) pend |= 1u << (2 * k + 1);
+                for (int k = 0; k < 8; k++) {
+                    const g53_u4 qv = src[k];
+                    av[2 * k] = __uint_as_float(qv.x);
+                    av[2 * k + 1] = __uint_as_float(qv.z);
+                    if (qv.y != a.epoch) pend |= 1u << (2 * k);
+                    if (qv.w != a.epoch) pend |= 1u << (2 * k + 1);
+                }
+            };
+            /* the values first: usually the slot's activations are long complete, and one round
+             * trip suffices */
+            load_all();
+            int spins = 0;
+            if (__ballot(pend != 0)) {
+                /* not yet: the last value of every row octet (2 KB per poll instead of the half's
+                 * 8 KB), with a growing back-off, then the values again */
+                const __amdgpu_buffer_rsrc_t rsl = rs;
+                int nap = 1;
+                for (;;) {
+                    g53_u64 tv[2];
+#pragma unroll
+                    for (int k = 0; k < 2; k++) tv[k] = g53_ld_coh64(rsl, 8 * ((lane + 64 * k) * 8 + 7));
+                    const int stale = ((unsigned)(tv[0] >> 32) != a.epoch) | ((unsigned)(tv[1] >> 32) != a.epoch);
+                    if (!__ballot(stale)) break;
+                    if (++spins > a.spin / 16 + 1) { if (lane == 0) g53_flag_err(a.err, 1); break; }
+                    for (int qq = 0; qq < nap; qq++) __builtin_amdgcn_s_sleep(8);
+                    if (nap < 8) nap *= 2;
+                }
+                load_all();
             }
             spins = 0;
             while (__ballot(pend != 0)) {
