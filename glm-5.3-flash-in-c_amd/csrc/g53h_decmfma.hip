@@ -651,27 +651,27 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
         /* the half's 1024 activations: lane l takes values 16 l .. 16 l + 15 of it (block
          * l / 8, group l / 2 % 4), re-read coherently until every tag is this launch's, then
          * writes them as B-operand planes into this wave's LDS */
-        auto stage_act = [&]() {
-            g53_u64 *act_s = a.act + (size_t)s * G53_DEC_I + 1024 * hd;
-            const __amdgpu_buffer_rsrc_t rs = g53_rsrc(act_s);
-            const int v0 = 16 * lane;
-            g53_mgv4 *src = (g53_mgv4 *)(act_s + v0);
-            float av[16];
-            uint32_t pend = 0;
-            auto load_all = [&]() {
-                pend = 0;
+        g53_u64 *act_s = a.act + (size_t)s * G53_DEC_I + 1024 * hd;
+        const __amdgpu_buffer_rsrc_t rs = g53_rsrc(act_s);
+        const int v0 = 16 * lane;
+        g53_mgv4 *src = (g53_mgv4 *)(act_s + v0);
+        float av[16];
+        uint32_t pend = 0;
+        auto load_all = [&]() {
+            pend = 0;
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const g53_u4 qv = src[k];
-                    av[2 * k] = __uint_as_float(qv.x);
-                    av[2 * k + 1] = __uint_as_float(qv.z);
-                    if (qv.y != a.epoch) pend |= 1u << (2 * k);
-                    if (qv.w != a.epoch) pend |= 1u << (2 * k + 1);
-                }
-            };
-            /* the values first: usually the slot's activations are long complete, and one round
-             * trip suffices */
-            load_all();
+            for (int k = 0; k < 8; k++) {
+                const g53_u4 qv = src[k];
+                av[2 * k] = __uint_as_float(qv.x);
+                av[2 * k + 1] = __uint_as_float(qv.z);
+                if (qv.y != a.epoch) pend |= 1u << (2 * k);
+                if (qv.w != a.epoch) pend |= 1u << (2 * k + 1);
+            }
+        };
+        /* stage_act follows a load_all issued before the task's code loads: usually the slot's
+         * activations are long complete and that one round trip suffices, and the loads complete
+         * in order, so the activations need not wait for the codes */
+        auto stage_act = [&]() {
             int spins = 0;
             if (__ballot(pend != 0)) {
                 /* not yet: the last value of every row octet (2 KB per poll instead of the half's
@@ -718,6 +718,7 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
             const uint8_t *pl = dw + ((size_t)(m < 8 ? oa : ob) * G53_DEC_NBI + 8 * hd) * 512 + (grp * 8 + (m & 7)) * 16;
             const float *sb = ex.down.s + ((size_t)(grp < 2 ? oa : ob) * G53_DEC_NBI + 8 * hd) * 16 +
                               (m < 6 ? m / 3 : 0) * 8 + 4 * (grp & 1);
+            load_all();
             __builtin_amdgcn_sched_barrier(0);
             constexpr int NB = G53_DEC_NBI / 2;
             g53_u4 r[NB];
@@ -751,6 +752,7 @@ __global__ void __launch_bounds__(G53_DM_NT, 1) k_dec_mfma(G53MfmaArgs a)
                                 (grp * 8 + (m & 7)) * 16;
             const float *sp = ex.down.s + (size_t)(oa >> 4) * ex.down.scols + 8 * hd + (lane & 7);
             const float scv = *(const g53_gf *)sp;
+            load_all();
             __builtin_amdgcn_sched_barrier(0);
             g53_mgv4 *q = (g53_mgv4 *)pl;
             constexpr int NB = G53_DEC_NBI / 2;
